@@ -1,0 +1,380 @@
+/*
+ * CPU oracle for the attention hot path of power-cpu-llm: a restatement in C
+ * of the reference's portable attention, for checking and timing only.
+ *
+ * TEST INFRASTRUCTURE ONLY: loaded by tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline leg; never by the product library.
+ *
+ * Build with -O2 -ffp-contract=off (oracle/Makefile): the reference is Rust,
+ * which never contracts a*b+c, and uses an FMA only where it writes mul_add.
+ * Transcendentals come from the host libm (exp, expf). The reference links
+ * bit-exact ports of glibc 2.28's IBM exp and POWER8 expf (src/libm.rs:92,
+ * 294); host glibc agrees with them to within an ulp, so this oracle matches
+ * the reference to the last bit except where such an ulp decides a rounding.
+ */
+#include "attention_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* p9_ref_attention_heads (src/kernels/portable/reference.rs:327-393). */
+bool oracle_ref_attention_heads(const float *query, const float *keys, const float *values,
+                                size_t qheads, size_t kvheads, size_t dim, size_t nkeys,
+                                const uint8_t *allowed, float *scratch, float *out,
+                                size_t h_first, size_t h_end)
+{
+    if (h_first > h_end || h_end > qheads) /* reference.rs:341-343 */
+        return false;
+    if (kvheads == 0 || qheads < kvheads) /* the wrapper's shape checks (reference.rs:421-437) */
+        return false;
+    const size_t group = qheads / kvheads;
+    const size_t stride = kvheads * dim;
+    for (size_t h = h_first; h < h_end; ++h) {
+        const size_t kh = h / group; /* reference.rs:358 */
+        float max = -INFINITY;
+        for (size_t t = 0; t < nkeys; ++t) { /* reference.rs:360-376 */
+            scratch[t] = -INFINITY;
+            if (allowed && allowed[t] == 0)
+                continue;
+            double score = 0.0;
+            for (size_t d = 0; d < dim; ++d)
+                score += (double)query[h * dim + d] * (double)keys[t * stride + kh * dim + d];
+            scratch[t] = (float)score;
+            if (!isfinite(scratch[t]))
+                return false;
+            if (scratch[t] > max)
+                max = scratch[t];
+        }
+        double sum = 0.0; /* reference.rs:377-380: every key, masked ones add exp(-inf) */
+        for (size_t t = 0; t < nkeys; ++t)
+            sum += exp((double)scratch[t] - (double)max);
+        for (size_t t = 0; t < nkeys; ++t) /* reference.rs:381-383 */
+            scratch[t] = (float)(exp((double)scratch[t] - (double)max) / sum);
+        for (size_t d = 0; d < dim; ++d) { /* reference.rs:384-390: d outer, t inner */
+            double result = 0.0;
+            for (size_t t = 0; t < nkeys; ++t)
+                result += (double)scratch[t] * (double)values[t * stride + kh * dim + d];
+            out[(h - h_first) * dim + d] = (float)result;
+        }
+    }
+    return true;
+}
+
+/* softmax (src/kernels/portable/attention.rs:15-43). */
+static bool oracle_softmax_f32(float *scores, size_t n, const uint8_t *allowed)
+{
+    float max = -INFINITY;
+    for (size_t t = 0; t < n; ++t) {
+        if (allowed && allowed[t] == 0)
+            continue;
+        if (!isfinite(scores[t]))
+            return false;
+        if (scores[t] > max)
+            max = scores[t];
+    }
+    float sum = 0.0f;
+    for (size_t t = 0; t < n; ++t) {
+        const float e = (allowed && allowed[t] == 0) ? 0.0f : expf(scores[t] - max);
+        scores[t] = e;
+        sum += e;
+    }
+    for (size_t t = 0; t < n; ++t)
+        scores[t] /= sum;
+    return true;
+}
+
+/* pa_attention_f32_heads (src/kernels/portable/attention.rs:51-112). */
+bool oracle_pa_attention_f32_heads(const float *query, const float *keys, const float *values,
+                                   size_t qheads, size_t kvheads, size_t dim, size_t nkeys,
+                                   const uint8_t *allowed, float *scratch, float *out,
+                                   size_t h_first, size_t h_end)
+{
+    if (h_first > h_end || h_end > qheads)
+        return false;
+    if (dim % 16 != 0 || kvheads == 0 || qheads % kvheads != 0) /* attention.rs:68-70 */
+        return false;
+    const size_t group = qheads / kvheads;
+    const size_t stride = kvheads * dim;
+    for (size_t h = h_first; h < h_end; ++h) {
+        const float *q = query + h * dim;
+        const size_t kh = h / group;
+        for (size_t t = 0; t < nkeys; ++t) { /* attention.rs:87-95 */
+            const float *k = keys + t * stride + kh * dim;
+            float p[16] = {0};
+            for (size_t d = 0; d < dim; ++d)
+                p[d % 16] = fmaf(q[d], k[d], p[d % 16]);
+            float v[4];
+            for (int l = 0; l < 4; ++l)
+                v[l] = (p[l] + p[4 + l]) + (p[8 + l] + p[12 + l]);
+            scratch[t] = (v[0] + v[1]) + (v[2] + v[3]);
+        }
+        if (!oracle_softmax_f32(scratch, nkeys, allowed))
+            return false;
+        float *o = out + (h - h_first) * dim;
+        for (size_t d = 0; d < dim; ++d) /* attention.rs:99-106 */
+            o[d] = 0.0f;
+        for (size_t t = 0; t < nkeys; ++t) {
+            const float *vt = values + t * stride + kh * dim;
+            for (size_t d = 0; d < dim; ++d)
+                o[d] = fmaf(scratch[t], vt[d], o[d]);
+        }
+        for (size_t d = 0; d < dim; ++d) /* attention.rs:107-109 */
+            if (!isfinite(o[d]))
+                return false;
+    }
+    return true;
+}
+
+typedef bool (*heads_fn)(const float *, const float *, const float *, size_t, size_t, size_t,
+                         size_t, const uint8_t *, float *, float *, size_t, size_t);
+
+/* One single-query call per query over query heads kh_first*group ..
+ * kh_end*group, output row i at out + i*o_stride. */
+static bool oracle_multi_kv(heads_fn kernel, const float *query, size_t nq, size_t q_stride,
+                            const float *keys, const float *values, size_t qheads,
+                            size_t kvheads, size_t dim, size_t nkeys, const uint8_t *allowed,
+                            size_t mask_stride, float *scratch, float *out, size_t o_stride,
+                            size_t kh_first, size_t kh_end)
+{
+    if (kvheads == 0 || kh_first > kh_end || kh_end > kvheads || qheads % kvheads != 0)
+        return false;
+    const size_t group = qheads / kvheads;
+    for (size_t i = 0; i < nq; ++i) {
+        const uint8_t *mask = allowed ? allowed + i * mask_stride : NULL;
+        if (!kernel(query + i * q_stride, keys, values, qheads, kvheads, dim, nkeys, mask,
+                    scratch, out + i * o_stride, kh_first * group, kh_end * group))
+            return false;
+    }
+    return true;
+}
+
+bool oracle_pa_attention_f32_multi_kv(const float *query, size_t nq, size_t q_stride,
+                                      const float *keys, const float *values, size_t qheads,
+                                      size_t kvheads, size_t dim, size_t nkeys,
+                                      const uint8_t *allowed, size_t mask_stride,
+                                      float *scratch, float *out, size_t o_stride,
+                                      size_t kh_first, size_t kh_end)
+{
+    return oracle_multi_kv(oracle_pa_attention_f32_heads, query, nq, q_stride, keys, values,
+                           qheads, kvheads, dim, nkeys, allowed, mask_stride, scratch, out,
+                           o_stride, kh_first, kh_end);
+}
+
+bool oracle_ref_attention_multi_kv(const float *query, size_t nq, size_t q_stride,
+                                   const float *keys, const float *values, size_t qheads,
+                                   size_t kvheads, size_t dim, size_t nkeys,
+                                   const uint8_t *allowed, size_t mask_stride, float *scratch,
+                                   float *out, size_t o_stride, size_t kh_first, size_t kh_end)
+{
+    return oracle_multi_kv(oracle_ref_attention_heads, query, nq, q_stride, keys, values,
+                           qheads, kvheads, dim, nkeys, allowed, mask_stride, scratch, out,
+                           o_stride, kh_first, kh_end);
+}
+
+/* all_finite (src/kernels/reference.rs:88-94): no inf or NaN. */
+static bool oracle_all_finite(const float *x, size_t n)
+{
+    for (size_t i = 0; i < n; ++i)
+        if (!isfinite(x[i]))
+            return false;
+    return true;
+}
+
+/* kernels::reference::attention_heads (src/kernels/reference.rs:412-478). */
+int oracle_attention_heads_checked(const float *query, size_t query_len, const float *keys,
+                                   size_t keys_len, const float *values, size_t values_len,
+                                   size_t kv_heads, size_t head_dim, const uint8_t *allowed,
+                                   size_t mask_len, int has_mask, size_t h_first, size_t h_end,
+                                   int has_heads, float *out)
+{
+    if (kv_heads == 0 || head_dim == 0 || kv_heads > SIZE_MAX / head_dim)
+        return ORACLE_INVALID_SHAPE; /* reference.rs:421-424 */
+    const size_t width = kv_heads * head_dim;
+    if (query_len == 0 || query_len % head_dim != 0 || keys_len == 0 || keys_len % width != 0 ||
+        values_len != keys_len)
+        return ORACLE_INVALID_SHAPE; /* reference.rs:425-432 */
+    const size_t qheads = query_len / head_dim;
+    const size_t nkeys = keys_len / width;
+    if (qheads % kv_heads != 0)
+        return ORACLE_INVALID_SHAPE;
+    if (has_mask) { /* reference.rs:438-445 */
+        if (mask_len != nkeys)
+            return ORACLE_INVALID_SHAPE;
+        bool any = false;
+        for (size_t t = 0; t < nkeys; ++t)
+            any |= allowed[t] != 0;
+        if (!any)
+            return ORACLE_INVALID_PARAMETER;
+    }
+    if (!has_heads) {
+        h_first = 0;
+        h_end = qheads;
+    }
+    if (h_first > h_end || h_end > qheads)
+        return ORACLE_INVALID_SHAPE;
+    if (!oracle_all_finite(query, query_len) || !oracle_all_finite(keys, keys_len) ||
+        !oracle_all_finite(values, values_len))
+        return ORACLE_NON_FINITE_VALUE; /* reference.rs:450-452 */
+    uint8_t *mask = NULL;
+    if (has_mask) { /* bool -> u8 (reference.rs:453) */
+        mask = (uint8_t *)malloc(nkeys ? nkeys : 1);
+        for (size_t t = 0; t < nkeys; ++t)
+            mask[t] = allowed[t] != 0;
+    }
+    float *scratch = (float *)malloc(nkeys * sizeof(float));
+    const bool ok = oracle_ref_attention_heads(query, keys, values, qheads, kv_heads, head_dim,
+                                               nkeys, mask, scratch, out, h_first, h_end);
+    free(scratch);
+    free(mask);
+    if (!ok)
+        return ORACLE_NON_FINITE_VALUE;
+    return oracle_all_finite(out, (h_end - h_first) * head_dim) ? ORACLE_OK
+                                                                : ORACLE_NON_FINITE_VALUE;
+}
+
+/* encoder_mask (src/engine/attention.rs:1170-1182). */
+int oracle_encoder_mask(size_t first_key, size_t count, size_t query, size_t window,
+                        int has_window, uint8_t *out)
+{
+    if (count == 0 || (has_window && window == 0) || first_key > SIZE_MAX - count)
+        return ORACLE_INVALID_SHAPE;
+    for (size_t i = 0; i < count; ++i) {
+        const size_t k = first_key + i;
+        out[i] = k <= query && (!has_window || query - k < window);
+    }
+    return ORACLE_OK;
+}
+
+/* retained_count (src/engine/attention.rs:1166-1168). */
+size_t oracle_retained_count(size_t count, size_t window, int has_window)
+{
+    if (!has_window)
+        return count;
+    const size_t keep = window > 0 ? window - 1 : 0;
+    return count < keep ? count : keep;
+}
+
+/* ---- threaded CPU baseline (the engine's decomposition) ---------------- */
+
+struct job {
+    heads_fn kernel;
+    const float *query, *keys, *values;
+    size_t nq, qheads, kvheads, dim, nkeys;
+    int causal;
+    size_t first_key, first_query, window;
+    float *out;
+    /* head-split decode: items (query, head range) */
+    size_t per;
+    size_t parts;
+    /* this worker's contiguous range of items or queries */
+    size_t first, end;
+    bool heads_mode;
+    bool ok;
+};
+
+static void *oracle_worker(void *arg)
+{
+    struct job *j = (struct job *)arg;
+    float *scratch = (float *)malloc(j->nkeys * sizeof(float));
+    uint8_t *mask = (uint8_t *)malloc(j->nkeys);
+    const size_t width = j->qheads * j->dim;
+    j->ok = true;
+    if (j->heads_mode) {
+        for (size_t item = j->first; item < j->end && j->ok; ++item) {
+            const size_t i = item / j->parts;
+            const size_t a = (item % j->parts) * j->per;
+            const size_t b = a + j->per < j->qheads ? a + j->per : j->qheads;
+            const uint8_t *m = NULL;
+            if (j->causal) {
+                oracle_encoder_mask(j->first_key, j->nkeys, j->first_query + i, j->window,
+                                    j->window != 0, mask);
+                m = mask;
+            }
+            j->ok = j->kernel(j->query + i * width, j->keys, j->values, j->qheads, j->kvheads,
+                              j->dim, j->nkeys, m, scratch, j->out + i * width + a * j->dim,
+                              a, b);
+        }
+    } else {
+        /* attention.rs:783-785: blocks of 8 queries; the exact and portable
+         * backends run each block's queries one by one (power9_fma.rs:211-230). */
+        for (size_t i = j->first; i < j->end && j->ok; ++i) {
+            const uint8_t *m = NULL;
+            if (j->causal) {
+                oracle_encoder_mask(j->first_key, j->nkeys, j->first_query + i, j->window,
+                                    j->window != 0, mask);
+                m = mask;
+            }
+            j->ok = j->kernel(j->query + i * width, j->keys, j->values, j->qheads, j->kvheads,
+                              j->dim, j->nkeys, m, scratch, j->out + i * width, 0, j->qheads);
+        }
+    }
+    free(mask);
+    free(scratch);
+    return NULL;
+}
+
+bool oracle_threaded_attention(int binary32, int threads, const float *query, size_t nq,
+                               const float *keys, const float *values, size_t qheads,
+                               size_t kvheads, size_t dim, size_t nkeys, int causal,
+                               size_t first_key, size_t first_query, size_t window,
+                               float *out)
+{
+    if (threads < 1)
+        threads = 1;
+    struct job base;
+    memset(&base, 0, sizeof base);
+    base.kernel = binary32 ? oracle_pa_attention_f32_heads : oracle_ref_attention_heads;
+    base.query = query;
+    base.keys = keys;
+    base.values = values;
+    base.nq = nq;
+    base.qheads = qheads;
+    base.kvheads = kvheads;
+    base.dim = dim;
+    base.nkeys = nkeys;
+    base.causal = causal;
+    base.first_key = first_key;
+    base.first_query = first_query;
+    base.window = window;
+    base.out = out;
+    size_t length;
+    if (nq < (size_t)threads) { /* attention.rs:755-765 */
+        size_t split = (size_t)threads / nq;
+        if (split < 1)
+            split = 1;
+        if (split > qheads)
+            split = qheads;
+        base.per = (qheads + split - 1) / split;
+        base.parts = (qheads + base.per - 1) / base.per;
+        base.heads_mode = true;
+        length = nq * base.parts;
+    } else {
+        base.heads_mode = false;
+        length = nq;
+    }
+    /* Workers::ranges (src/engine/execution.rs:583-597). */
+    size_t n = (size_t)threads < length ? (size_t)threads : length;
+    if (n == 0)
+        return true;
+    struct job *jobs = (struct job *)calloc(n, sizeof *jobs);
+    pthread_t *tid = (pthread_t *)calloc(n, sizeof *tid);
+    const size_t per = length / n, rem = length % n;
+    for (size_t i = 0; i < n; ++i) {
+        jobs[i] = base;
+        jobs[i].first = i * per + (i < rem ? i : rem);
+        jobs[i].end = jobs[i].first + per + (i < rem ? 1 : 0);
+    }
+    for (size_t i = 1; i < n; ++i)
+        pthread_create(&tid[i], NULL, oracle_worker, &jobs[i]);
+    oracle_worker(&jobs[0]);
+    bool ok = jobs[0].ok;
+    for (size_t i = 1; i < n; ++i) {
+        pthread_join(tid[i], NULL);
+        ok = ok && jobs[i].ok;
+    }
+    free(tid);
+    free(jobs);
+    return ok;
+}

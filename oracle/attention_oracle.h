@@ -1,0 +1,103 @@
+/*
+ * CPU oracle for the attention hot path of power-cpu-llm.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker: only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it. The
+ * product path (power-cpu-llm_amd/) never links, loads or calls it.
+ *
+ * Every function restates a reference function; the citation is next to each
+ * declaration (paths relative to the reference checkout).
+ */
+#ifndef PCL_ATTENTION_ORACLE_H
+#define PCL_ATTENTION_ORACLE_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Error codes of kernels::reference::Error (src/kernels/reference.rs:6-11). */
+enum oracle_status {
+    ORACLE_OK = 0,
+    ORACLE_INVALID_SHAPE = 1,
+    ORACLE_INVALID_PARAMETER = 2,
+    ORACLE_NON_FINITE_VALUE = 3,
+};
+
+/* a1 — exact attention: p9_ref_attention_heads
+ * (src/kernels/portable/reference.rs:320-393). F64 score and value sums,
+ * F32 scores and probabilities, f64 softmax, scale one. scratch [nkeys]. */
+bool oracle_ref_attention_heads(const float *query, const float *keys, const float *values,
+                                size_t qheads, size_t kvheads, size_t dim, size_t nkeys,
+                                const uint8_t *allowed, float *scratch, float *out,
+                                size_t h_first, size_t h_end);
+
+/* a3/a4 — binary32 attention: pa_attention_f32_heads + softmax
+ * (src/kernels/portable/attention.rs:14-112). 16 FMA score lanes reduced as a
+ * fixed tree, f32 softmax (libm expf), FMA PV chain from +0. scratch [nkeys]. */
+bool oracle_pa_attention_f32_heads(const float *query, const float *keys, const float *values,
+                                   size_t qheads, size_t kvheads, size_t dim, size_t nkeys,
+                                   const uint8_t *allowed, float *scratch, float *out,
+                                   size_t h_first, size_t h_end);
+
+/* a7 contract — several queries, KV heads [kh_first, kh_end): one a3 call
+ * per query over that head range (the AttentionMulti ABI of
+ * src/kernels/quantized/int8.rs:446-484, pinned bitwise to single-query
+ * calls by src/kernels/quantized/int8/tests.rs:661-768). */
+bool oracle_pa_attention_f32_multi_kv(const float *query, size_t nq, size_t q_stride,
+                                      const float *keys, const float *values, size_t qheads,
+                                      size_t kvheads, size_t dim, size_t nkeys,
+                                      const uint8_t *allowed, size_t mask_stride,
+                                      float *scratch, float *out, size_t o_stride,
+                                      size_t kh_first, size_t kh_end);
+
+/* The exact backends' multi-query fallback: per query a1 over query heads
+ * kv.start*group..kv.end*group (src/kernels/quantized/power9_fma.rs:211-230).
+ * scratch [nkeys]. */
+bool oracle_ref_attention_multi_kv(const float *query, size_t nq, size_t q_stride,
+                                   const float *keys, const float *values, size_t qheads,
+                                   size_t kvheads, size_t dim, size_t nkeys,
+                                   const uint8_t *allowed, size_t mask_stride, float *scratch,
+                                   float *out, size_t o_stride, size_t kh_first, size_t kh_end);
+
+/* a2 — checked exact attention: kernels::reference::attention_heads
+ * (src/kernels/reference.rs:412-478). Lengths are element counts; has_mask /
+ * has_heads select Option::Some. out holds (h_end-h_first)*head_dim. */
+int oracle_attention_heads_checked(const float *query, size_t query_len, const float *keys,
+                                   size_t keys_len, const float *values, size_t values_len,
+                                   size_t kv_heads, size_t head_dim, const uint8_t *allowed,
+                                   size_t mask_len, int has_mask, size_t h_first, size_t h_end,
+                                   int has_heads, float *out);
+
+/* a10 — encoder_mask (src/engine/attention.rs:1170-1182): allowed(k) =
+ * k <= query && (no window || query - k < window) for k in
+ * [first_key, first_key+count). Returns ORACLE_INVALID_SHAPE on count 0,
+ * window 0 or overflow. */
+int oracle_encoder_mask(size_t first_key, size_t count, size_t query, size_t window,
+                        int has_window, uint8_t *out);
+
+/* a10 — retained_count (src/engine/attention.rs:1166-1168). */
+size_t oracle_retained_count(size_t count, size_t window, int has_window);
+
+/* CPU baseline: the exact (a1) or binary32 (a3) path threaded as the engine
+ * threads it (src/engine/attention.rs:755-836): one query's heads split
+ * into ceil(qheads/split) ranges with split = clamp(workers/queries, 1,
+ * qheads) when queries < workers, else contiguous query ranges
+ * (src/engine/execution.rs:571-599) walked in blocks of 8 queries.
+ * Masks come from encoder_mask(first_key, nkeys, first_query+i, window),
+ * or none when causal == 0 (decoder mode). Queries [nq][qheads*dim];
+ * out [nq][qheads*dim]. Returns false on a kernel error. */
+bool oracle_threaded_attention(int binary32, int threads, const float *query, size_t nq,
+                               const float *keys, const float *values, size_t qheads,
+                               size_t kvheads, size_t dim, size_t nkeys, int causal,
+                               size_t first_key, size_t first_query, size_t window,
+                               float *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

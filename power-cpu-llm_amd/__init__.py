@@ -1,0 +1,299 @@
+"""Python loader and host-side mirror of the gfx950 attention backend.
+
+The product is the C-ABI library libpcl_attention.so (include/pcl_attention.h).
+This module binds it with ctypes and mirrors the reference engine's attention
+interface on top of it, so callers and tests use the reference's names and
+error behaviour:
+
+  HipKernels.attention / attention_heads / attention_multi / attention_multi_kv
+      FmaKernels' attention methods (src/kernels/quantized/power9_fma.rs:158-255)
+      with the binary32 wrappers' validation (src/kernels/quantized/int8.rs:
+      489-663); errors raise AttentionError with the kind of
+      kernels::reference::Error (src/kernels/reference.rs:6-11).
+  Context
+      the device-resident entry: device pointers, descriptor masks, two KV
+      segments, launches on a stream.
+
+There is no CPU fallback: without the built library every entry raises.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libpcl_attention.so")
+
+OK, INVALID_SHAPE, INVALID_PARAMETER, NON_FINITE_VALUE = 0, 1, 2, 3
+ERROR_NAMES = {INVALID_SHAPE: "InvalidShape", INVALID_PARAMETER: "InvalidParameter",
+               NON_FINITE_VALUE: "NonFiniteValue"}
+KERNEL_AUTO, KERNEL_SPLIT_KV, KERNEL_TILED, KERNEL_TILED_SPLIT = 0, 1, 2, 3
+KERNEL_NAMES = {KERNEL_SPLIT_KV: "split_kv", KERNEL_TILED: "tiled",
+                KERNEL_TILED_SPLIT: "tiled_split"}
+
+# Every symbol include/pcl_attention.h declares.
+EXPORTS = (
+    "pcl_hip_attention_f32_heads",
+    "pcl_hip_attention_f32_multi_kv",
+    "pcl_attention_heads",
+    "pcl_attention_multi_kv",
+    "pcl_context_create",
+    "pcl_context_destroy",
+    "pcl_context_stream",
+    "pcl_attention_launch",
+    "pcl_attention_workspace_bytes",
+    "pcl_context_reserve",
+    "pcl_context_sync",
+    "pcl_attention_resolve_kernel",
+    "pcl_version",
+)
+
+
+class AttentionError(Exception):
+    """kernels::reference::Error: kind is InvalidShape, InvalidParameter or
+    NonFiniteValue."""
+
+    def __init__(self, code):
+        self.code = code
+        self.kind = ERROR_NAMES.get(code, "Unknown(%d)" % code)
+        super().__init__(self.kind)
+
+
+class PclDesc(ctypes.Structure):
+    """pcl_attention_desc."""
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("q_stride", ctypes.c_int64), ("nq", ctypes.c_int64),
+        ("k0", ctypes.c_void_p), ("v0", ctypes.c_void_p), ("n0", ctypes.c_int64),
+        ("k1", ctypes.c_void_p), ("v1", ctypes.c_void_p), ("n1", ctypes.c_int64),
+        ("qheads", ctypes.c_int64), ("kvheads", ctypes.c_int64), ("dim", ctypes.c_int64),
+        ("kh_first", ctypes.c_int64), ("kh_end", ctypes.c_int64),
+        ("mask", ctypes.c_void_p), ("mask_stride", ctypes.c_int64),
+        ("causal", ctypes.c_int32), ("window", ctypes.c_int64),
+        ("first_key", ctypes.c_int64), ("first_query", ctypes.c_int64),
+        ("q_scale", ctypes.c_float),
+        ("out", ctypes.c_void_p), ("o_stride", ctypes.c_int64),
+        ("kernel", ctypes.c_int32),
+    ]
+
+
+_lib = None
+
+
+def library_path():
+    return LIB_PATH
+
+
+def load():
+    """The loaded library; raises if it was not built (no fallback)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError("libpcl_attention.so is not built: run power-cpu-llm_amd/build.py "
+                           "(or __graft_entry__.build())")
+    lib = ctypes.CDLL(LIB_PATH)
+    fp, vp, sz, u8p = (ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_size_t,
+                       ctypes.POINTER(ctypes.c_uint8))
+    lib.pcl_hip_attention_f32_heads.restype = ctypes.c_bool
+    lib.pcl_hip_attention_f32_heads.argtypes = [fp, fp, fp, sz, sz, sz, sz, u8p, fp, fp, sz, sz]
+    lib.pcl_hip_attention_f32_multi_kv.restype = ctypes.c_bool
+    lib.pcl_hip_attention_f32_multi_kv.argtypes = [fp, sz, sz, fp, fp, sz, sz, sz, sz, u8p, sz,
+                                                   fp, fp, sz, sz, sz]
+    lib.pcl_attention_heads.restype = ctypes.c_int
+    lib.pcl_attention_heads.argtypes = [fp, sz, fp, sz, fp, sz, sz, sz, u8p, sz, ctypes.c_int,
+                                        sz, sz, ctypes.c_int, fp]
+    lib.pcl_attention_multi_kv.restype = ctypes.c_int
+    lib.pcl_attention_multi_kv.argtypes = [ctypes.POINTER(fp), sz, sz, fp, sz, fp, sz, sz, sz,
+                                           ctypes.POINTER(u8p), sz, sz, sz, fp]
+    lib.pcl_context_create.restype = ctypes.c_int
+    lib.pcl_context_create.argtypes = [ctypes.c_int, vp, ctypes.POINTER(vp)]
+    lib.pcl_context_destroy.restype = None
+    lib.pcl_context_destroy.argtypes = [vp]
+    lib.pcl_context_stream.restype = vp
+    lib.pcl_context_stream.argtypes = [vp]
+    lib.pcl_attention_launch.restype = ctypes.c_int
+    lib.pcl_attention_launch.argtypes = [vp, ctypes.POINTER(PclDesc)]
+    lib.pcl_attention_workspace_bytes.restype = sz
+    lib.pcl_attention_workspace_bytes.argtypes = [ctypes.POINTER(PclDesc)]
+    lib.pcl_context_reserve.restype = ctypes.c_int
+    lib.pcl_context_reserve.argtypes = [vp, sz]
+    lib.pcl_context_sync.restype = ctypes.c_int
+    lib.pcl_context_sync.argtypes = [vp, ctypes.POINTER(ctypes.c_int)]
+    lib.pcl_attention_resolve_kernel.restype = ctypes.c_int
+    lib.pcl_attention_resolve_kernel.argtypes = [ctypes.POINTER(PclDesc)]
+    lib.pcl_version.restype = ctypes.c_char_p
+    lib.pcl_version.argtypes = []
+    _lib = lib
+    return lib
+
+
+def _fptr(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def _u8ptr(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8))
+
+
+def _f32(x):
+    return np.ascontiguousarray(np.asarray(x, dtype=np.float32).reshape(-1))
+
+
+def _bools(x):
+    return np.ascontiguousarray(np.asarray(x, dtype=bool).reshape(-1)).astype(np.uint8)
+
+
+class HipKernels:
+    """The attention half of an FmaKernels table whose `attention` and
+    `attention_multi` pointers are this library's entries (a new
+    `Request::HipF32` backend; src/kernels/quantized/power9_fma.rs:83-125)."""
+
+    name = "hip-f32"
+
+    def __init__(self):
+        self.lib = load()
+
+    def attention(self, query, keys, values, kv_heads, head_dim, allowed=None):
+        """FmaKernels::attention (power9_fma.rs:160-170)."""
+        return self.attention_heads(query, keys, values, kv_heads, head_dim, allowed, None)
+
+    def attention_heads(self, query, keys, values, kv_heads, head_dim, allowed=None, heads=None):
+        """FmaKernels::attention_heads (power9_fma.rs:237-255) through
+        attention_with (int8.rs:596-663). heads: None or (start, end)."""
+        q, k, v = _f32(query), _f32(keys), _f32(values)
+        mask = _bools(allowed) if allowed is not None else np.zeros(1, np.uint8)
+        h0, h1 = (0, 0) if heads is None else (int(heads[0]), int(heads[1]))
+        qheads = q.size // head_dim if head_dim and q.size % head_dim == 0 else 0
+        nout = max(h1 - h0, 0) if heads is not None else qheads
+        out = np.zeros(max(nout * head_dim, 1), np.float32)
+        rc = self.lib.pcl_attention_heads(
+            _fptr(q), q.size, _fptr(k), k.size, _fptr(v), v.size, kv_heads, head_dim,
+            _u8ptr(mask), mask.size if allowed is not None else 0, int(allowed is not None),
+            h0, h1, int(heads is not None), _fptr(out))
+        if rc != OK:
+            raise AttentionError(rc)
+        return out[:nout * head_dim]
+
+    def attention_multi(self, queries, keys, values, kv_heads, head_dim, masks=None):
+        """FmaKernels::attention_multi (power9_fma.rs:174-192)."""
+        return self.attention_multi_kv(queries, keys, values, kv_heads, head_dim, masks,
+                                       (0, kv_heads))
+
+    def attention_multi_kv(self, queries, keys, values, kv_heads, head_dim, masks=None,
+                           kv=None):
+        """FmaKernels::attention_multi_kv (power9_fma.rs:197-232) through
+        attention_multi_with (int8.rs:489-573). Returns one array per query."""
+        qs = [_f32(x) for x in queries]
+        if not qs:
+            return []
+        qlen = qs[0].size
+        if any(x.size != qlen for x in qs):
+            raise AttentionError(INVALID_SHAPE)
+        k, v = _f32(keys), _f32(values)
+        kv0, kv1 = (0, kv_heads) if kv is None else (int(kv[0]), int(kv[1]))
+        width = kv_heads * head_dim
+        nkeys = k.size // width if width else 0
+        if masks is not None:
+            ms = [_bools(m) for m in masks]
+            if len(ms) != len(qs) or any(m.size != ms[0].size for m in ms):
+                raise AttentionError(INVALID_SHAPE)
+            mask_len = ms[0].size
+            mptrs = (ctypes.POINTER(ctypes.c_uint8) * len(ms))(*[_u8ptr(m) for m in ms])
+        else:
+            ms, mask_len, mptrs = None, 0, None
+        group = qlen // head_dim // kv_heads if head_dim and kv_heads else 0
+        olen = max(kv1 - kv0, 0) * group * head_dim
+        out = np.zeros(max(len(qs) * olen, 1), np.float32)
+        qptrs = (ctypes.POINTER(ctypes.c_float) * len(qs))(*[_fptr(x) for x in qs])
+        rc = self.lib.pcl_attention_multi_kv(
+            qptrs, len(qs), qlen, _fptr(k), k.size, _fptr(v), v.size, kv_heads, head_dim,
+            mptrs, mask_len, kv0, kv1, _fptr(out))
+        del nkeys
+        if rc != OK:
+            raise AttentionError(rc)
+        return [out[i * olen:(i + 1) * olen].copy() for i in range(len(qs))]
+
+
+def raw_heads(query, keys, values, qheads, kvheads, dim, nkeys, allowed, h_first, h_end):
+    """The AttentionF32 entry itself: (ok, out)."""
+    lib = load()
+    q, k, v = _f32(query), _f32(keys), _f32(values)
+    out = np.zeros(max((h_end - h_first) * dim, 1), np.float32)
+    m = _bools(allowed) if allowed is not None else None
+    ok = lib.pcl_hip_attention_f32_heads(_fptr(q), _fptr(k), _fptr(v), qheads, kvheads, dim,
+                                         nkeys, _u8ptr(m) if m is not None else None, None,
+                                         _fptr(out), h_first, h_end)
+    return bool(ok), out[:max(h_end - h_first, 0) * dim]
+
+
+def raw_multi_kv(query, nq, q_stride, keys, values, qheads, kvheads, dim, nkeys, allowed,
+                 mask_stride, o_stride, kh_first, kh_end):
+    """The AttentionMulti entry itself: (ok, out[nq*o_stride])."""
+    lib = load()
+    q, k, v = _f32(query), _f32(keys), _f32(values)
+    out = np.zeros(max(nq * o_stride, 1), np.float32)
+    m = _bools(allowed) if allowed is not None else None
+    ok = lib.pcl_hip_attention_f32_multi_kv(
+        _fptr(q), nq, q_stride, _fptr(k), _fptr(v), qheads, kvheads, dim, nkeys,
+        _u8ptr(m) if m is not None else None, mask_stride, None, _fptr(out), o_stride,
+        kh_first, kh_end)
+    return bool(ok), out[:nq * o_stride]
+
+
+class Context:
+    """The device-resident entry (pcl_context). Pointers are device addresses
+    (ints); torch tensors work through data_ptr()."""
+
+    def __init__(self, device=0, stream=None):
+        self.lib = load()
+        self.handle = ctypes.c_void_p()
+        rc = self.lib.pcl_context_create(device, stream, ctypes.byref(self.handle))
+        if rc != OK:
+            raise AttentionError(rc)
+
+    def close(self):
+        if self.handle:
+            self.lib.pcl_context_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def stream(self):
+        return self.lib.pcl_context_stream(self.handle)
+
+    @staticmethod
+    def desc(**kw):
+        d = PclDesc()
+        d.q_scale = 1.0
+        for k, v in kw.items():
+            setattr(d, k, v)
+        return d
+
+    def launch(self, desc):
+        rc = self.lib.pcl_attention_launch(self.handle, ctypes.byref(desc))
+        if rc != OK:
+            raise AttentionError(rc)
+
+    def reserve(self, nbytes):
+        rc = self.lib.pcl_context_reserve(self.handle, nbytes)
+        if rc != OK:
+            raise AttentionError(rc)
+
+    def workspace_bytes(self, desc):
+        return self.lib.pcl_attention_workspace_bytes(ctypes.byref(desc))
+
+    def resolve_kernel(self, desc):
+        return self.lib.pcl_attention_resolve_kernel(ctypes.byref(desc))
+
+    def sync(self):
+        """Wait; returns the device error flag (cleared)."""
+        err = ctypes.c_int(0)
+        rc = self.lib.pcl_context_sync(self.handle, ctypes.byref(err))
+        if rc != OK:
+            raise AttentionError(rc)
+        return err.value

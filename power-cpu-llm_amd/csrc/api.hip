@@ -1,0 +1,667 @@
+// Host side of the attention backend: contexts, descriptor validation,
+// kernel choice and the C ABI of include/pcl_attention.h.
+#include "attention_device.hpp"
+#include "pcl_attention.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+namespace pcl {
+hipError_t launch_split_kv(const Params &p, hipStream_t stream);
+hipError_t launch_combine(const Params &p, hipStream_t stream);
+hipError_t launch_tiled(const Params &p, int split, hipStream_t stream);
+int tiled_rows(int dk);
+} // namespace pcl
+
+using pcl::Params;
+
+struct pcl_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool own_stream = false;
+    void *ws = nullptr;
+    size_t ws_bytes = 0;
+    int *err = nullptr;
+    // Staging buffers of the host-pointer entries (grow-only).
+    void *stage[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
+    size_t stage_bytes[5] = {0, 0, 0, 0, 0};
+};
+
+namespace {
+
+constexpr int kMaxDim = 512;
+constexpr int kTiledMaxDk = 256;
+
+void report(const char *what, hipError_t e)
+{
+    std::fprintf(stderr, "pcl_attention: %s: %s\n", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void *p)
+{
+    return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+int64_t round_up(int64_t x, int64_t m)
+{
+    return (x + m - 1) / m * m;
+}
+
+// A validated launch: parameters, kernel and workspace.
+struct Plan {
+    Params p;
+    int kernel = PCL_KERNEL_SPLIT_KV;
+    size_t ws_floats = 0;
+    bool empty = false; // nothing to compute
+};
+
+// Visible key chunks of the whole launch (descriptor masks only narrow it).
+void chunk_range(const pcl_attention_desc &d, int64_t nkeys, int64_t *c_lo, int64_t *c_hi,
+                 bool *none)
+{
+    int64_t k_lo = 0, k_hi = nkeys;
+    if (!d.mask && d.causal) {
+        k_hi = std::min(std::max(d.first_query + d.nq - 1 - d.first_key + 1, (int64_t)0), nkeys);
+        if (d.window)
+            k_lo = std::min(std::max(d.first_query - d.window + 1 - d.first_key, (int64_t)0),
+                            nkeys);
+    }
+    *none = k_hi <= k_lo;
+    *c_lo = k_lo / pcl::kChunk;
+    *c_hi = (k_hi + pcl::kChunk - 1) / pcl::kChunk;
+}
+
+int choose_kernel(int requested, int dk, int64_t nrows, int64_t nkv, int64_t nch)
+{
+    if (requested == PCL_KERNEL_TILED || requested == PCL_KERNEL_TILED_SPLIT)
+        return dk <= kTiledMaxDk ? requested : PCL_KERNEL_SPLIT_KV;
+    if (requested == PCL_KERNEL_SPLIT_KV)
+        return requested;
+    if (dk > kTiledMaxDk || nrows < 64)
+        return PCL_KERNEL_SPLIT_KV;
+    const int64_t rows = pcl::tiled_rows(dk);
+    const int64_t blocks = (nrows + rows - 1) / rows * nkv;
+    if (blocks >= 128 || nch <= 1)
+        return PCL_KERNEL_TILED;
+    return PCL_KERNEL_TILED_SPLIT;
+}
+
+// Validate a descriptor and build the plan. h_lo/h_hi/h_base select and place
+// the written query heads (the whole KV-head range for the public entry).
+int make_plan(const pcl_attention_desc &d, int64_t h_lo, int64_t h_hi, int64_t h_base,
+              Plan *plan)
+{
+    if (d.qheads <= 0 || d.kvheads <= 0 || d.qheads % d.kvheads != 0 || d.dim <= 0 ||
+        d.dim % 16 != 0 || d.dim > kMaxDim || d.nq < 0 || d.n0 < 0 || d.n1 < 0 ||
+        d.kh_first < 0 || d.kh_first > d.kh_end || d.kh_end > d.kvheads || d.window < 0)
+        return PCL_INVALID_SHAPE;
+    const int64_t group = d.qheads / d.kvheads;
+    const int64_t nkeys = d.n0 + d.n1;
+    const int64_t nkv = d.kh_end - d.kh_first;
+    plan->empty = d.nq == 0 || nkv == 0 || h_lo >= h_hi;
+    if (plan->empty)
+        return PCL_OK;
+    if (nkeys <= 0 || !d.q || !d.out || (d.n0 > 0 && (!d.k0 || !d.v0)) ||
+        (d.n1 > 0 && (!d.k1 || !d.v1)))
+        return PCL_INVALID_SHAPE;
+    if (d.q_stride < d.qheads * d.dim || d.q_stride % 4 != 0 || d.o_stride % 4 != 0 ||
+        (d.mask && d.mask_stride < nkeys) || !aligned16(d.q) || !aligned16(d.out) ||
+        (d.n0 > 0 && (!aligned16(d.k0) || !aligned16(d.v0))) ||
+        (d.n1 > 0 && (!aligned16(d.k1) || !aligned16(d.v1))))
+        return PCL_INVALID_SHAPE;
+    const int64_t nrows = d.nq * group;
+    if (nrows > (int64_t)1 << 30 || nkeys > (int64_t)1 << 40)
+        return PCL_INVALID_SHAPE;
+    int64_t c_lo, c_hi;
+    bool none;
+    chunk_range(d, nkeys, &c_lo, &c_hi, &none);
+    if (none)
+        return PCL_INVALID_PARAMETER; // no query sees any key
+    // padded head dim: the kernels are instantiated for 64, 128, 256 and 512
+    const int dk = d.dim <= 64 ? 64 : d.dim <= 128 ? 128 : d.dim <= 256 ? 256 : 512;
+    const int64_t nch = c_hi - c_lo;
+
+    Params &p = plan->p;
+    std::memset(&p, 0, sizeof p);
+    p.q = d.q;
+    p.q_stride = d.q_stride;
+    p.nq = (int)d.nq;
+    p.q_scale = d.q_scale;
+    if (d.n0 > 0) {
+        p.k0 = d.k0;
+        p.v0 = d.v0;
+        p.n0 = d.n0;
+        p.k1 = d.n1 > 0 ? d.k1 : d.k0;
+        p.v1 = d.n1 > 0 ? d.v1 : d.v0;
+    } else {
+        p.k0 = p.k1 = d.k1;
+        p.v0 = p.v1 = d.v1;
+        p.n0 = 0;
+    }
+    p.nkeys = nkeys;
+    p.kv_stride = d.kvheads * d.dim;
+    p.dim = (int)d.dim;
+    p.group = (int)group;
+    p.kh_first = (int)d.kh_first;
+    p.nkv = (int)nkv;
+    p.h_lo = (int)h_lo;
+    p.h_hi = (int)h_hi;
+    p.h_base = (int)h_base;
+    p.mask = d.mask;
+    p.mask_stride = d.mask_stride;
+    p.causal = d.causal;
+    p.window = d.window;
+    p.first_key = d.first_key;
+    p.first_query = d.first_query;
+    p.out = d.out;
+    p.o_stride = d.o_stride;
+    p.nrows = (int)nrows;
+    p.units = (int)((nrows + pcl::kRows - 1) / pcl::kRows);
+    p.nrows_pad = p.units * pcl::kRows;
+    p.c_lo = (int)c_lo;
+    p.nch = (int)nch;
+    p.dk = dk;
+
+    plan->kernel = choose_kernel(d.kernel, dk, nrows, nkv, nch);
+    if (plan->kernel == PCL_KERNEL_TILED_SPLIT) {
+        // the tiled kernel's rows come in whole workgroup blocks
+        p.nrows_pad = (int)round_up(nrows, pcl::tiled_rows(dk));
+    }
+    const bool partials = plan->kernel == PCL_KERNEL_TILED_SPLIT ||
+                          (plan->kernel == PCL_KERNEL_SPLIT_KV && nch > 1);
+    plan->ws_floats = partials ? (size_t)nkv * p.nrows_pad * nch * (dk + 2) : 0;
+    return PCL_OK;
+}
+
+int ensure_workspace(pcl_context *ctx, size_t bytes)
+{
+    if (bytes <= ctx->ws_bytes)
+        return PCL_OK;
+    if (ctx->ws) {
+        (void)hipStreamSynchronize(ctx->stream);
+        (void)hipFree(ctx->ws);
+        ctx->ws = nullptr;
+        ctx->ws_bytes = 0;
+    }
+    const hipError_t e = hipMalloc(&ctx->ws, bytes);
+    if (e != hipSuccess) {
+        report("workspace allocation", e);
+        return PCL_NON_FINITE_VALUE;
+    }
+    ctx->ws_bytes = bytes;
+    return PCL_OK;
+}
+
+int run_plan(pcl_context *ctx, Plan &plan)
+{
+    if (plan.empty)
+        return PCL_OK;
+    Params &p = plan.p;
+    p.err = ctx->err;
+    if (plan.ws_floats) {
+        const int rc = ensure_workspace(ctx, plan.ws_floats * sizeof(float));
+        if (rc != PCL_OK)
+            return rc;
+        const size_t o_floats = (size_t)p.nkv * p.nrows_pad * p.nch * p.dk;
+        p.ws_o = static_cast<float *>(ctx->ws);
+        p.ws_ml = p.ws_o + o_floats;
+    }
+    hipError_t e = hipSuccess;
+    switch (plan.kernel) {
+    case PCL_KERNEL_SPLIT_KV:
+        e = pcl::launch_split_kv(p, ctx->stream);
+        if (e == hipSuccess && p.ws_o)
+            e = pcl::launch_combine(p, ctx->stream);
+        break;
+    case PCL_KERNEL_TILED:
+        e = pcl::launch_tiled(p, 0, ctx->stream);
+        break;
+    case PCL_KERNEL_TILED_SPLIT:
+        e = pcl::launch_tiled(p, 1, ctx->stream);
+        if (e == hipSuccess)
+            e = pcl::launch_combine(p, ctx->stream);
+        break;
+    default:
+        return PCL_INVALID_SHAPE;
+    }
+    if (e != hipSuccess) {
+        report("kernel launch", e);
+        return PCL_NON_FINITE_VALUE;
+    }
+    return PCL_OK;
+}
+
+// ---- host-pointer entries: one shared context, one call at a time ----------
+
+std::mutex g_abi_mutex;
+pcl_context *g_abi_ctx = nullptr;
+
+pcl_context *abi_context()
+{
+    if (!g_abi_ctx) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess)
+            dev = 0;
+        if (pcl_context_create(dev, nullptr, &g_abi_ctx) != PCL_OK)
+            g_abi_ctx = nullptr;
+    }
+    return g_abi_ctx;
+}
+
+void *stage_buffer(pcl_context *ctx, int slot, size_t bytes)
+{
+    bytes = std::max<size_t>(bytes, 16);
+    if (bytes > ctx->stage_bytes[slot]) {
+        if (ctx->stage[slot])
+            (void)hipFree(ctx->stage[slot]);
+        ctx->stage[slot] = nullptr;
+        ctx->stage_bytes[slot] = 0;
+        const hipError_t e = hipMalloc(&ctx->stage[slot], bytes);
+        if (e != hipSuccess) {
+            report("staging allocation", e);
+            return nullptr;
+        }
+        ctx->stage_bytes[slot] = bytes;
+    }
+    return ctx->stage[slot];
+}
+
+// Copy inputs to the device, run, copy the output rows back.
+bool run_host(const float *query, size_t q_floats, const float *keys, const float *values,
+              size_t kv_floats, const uint8_t *allowed, size_t mask_bytes,
+              pcl_attention_desc d, int64_t h_lo, int64_t h_hi, int64_t h_base, float *out,
+              size_t out_rows, size_t out_row_floats, size_t out_pitch_floats)
+{
+    std::lock_guard<std::mutex> lock(g_abi_mutex);
+    pcl_context *ctx = abi_context();
+    if (!ctx)
+        return false;
+    (void)hipSetDevice(ctx->device);
+    float *dq = static_cast<float *>(stage_buffer(ctx, 0, q_floats * sizeof(float)));
+    float *dk = static_cast<float *>(stage_buffer(ctx, 1, kv_floats * sizeof(float)));
+    float *dv = static_cast<float *>(stage_buffer(ctx, 2, kv_floats * sizeof(float)));
+    uint8_t *dm = allowed ? static_cast<uint8_t *>(stage_buffer(ctx, 3, mask_bytes)) : nullptr;
+    float *dout = static_cast<float *>(
+        stage_buffer(ctx, 4, out_rows * out_pitch_floats * sizeof(float)));
+    if (!dq || !dk || !dv || (allowed && !dm) || !dout)
+        return false;
+    hipError_t e = hipMemcpyAsync(dq, query, q_floats * sizeof(float), hipMemcpyHostToDevice,
+                                  ctx->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(dk, keys, kv_floats * sizeof(float), hipMemcpyHostToDevice,
+                           ctx->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(dv, values, kv_floats * sizeof(float), hipMemcpyHostToDevice,
+                           ctx->stream);
+    if (e == hipSuccess && allowed)
+        e = hipMemcpyAsync(dm, allowed, mask_bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e != hipSuccess) {
+        report("host to device copy", e);
+        return false;
+    }
+    d.q = dq;
+    d.k0 = dk;
+    d.v0 = dv;
+    d.mask = dm;
+    d.out = dout;
+    d.o_stride = (int64_t)out_pitch_floats;
+    Plan plan;
+    if (make_plan(d, h_lo, h_hi, h_base, &plan) != PCL_OK)
+        return false;
+    if (run_plan(ctx, plan) != PCL_OK)
+        return false;
+    e = hipMemcpy2DAsync(out, out_pitch_floats * sizeof(float), dout,
+                         out_pitch_floats * sizeof(float), out_row_floats * sizeof(float),
+                         out_rows, hipMemcpyDeviceToHost, ctx->stream);
+    if (e != hipSuccess) {
+        report("device to host copy", e);
+        return false;
+    }
+    int derr = 0;
+    if (pcl_context_sync(ctx, &derr) != PCL_OK)
+        return false;
+    return derr == 0;
+}
+
+bool all_finite(const float *x, size_t n)
+{
+    for (size_t i = 0; i < n; ++i)
+        if (!std::isfinite(x[i]))
+            return false;
+    return true;
+}
+
+} // namespace
+
+extern "C" {
+
+const char *pcl_version(void)
+{
+    return "pcl_attention 0.1 gfx950 (mfma_f32_16x16x4f32, chunk 256, tile 32)";
+}
+
+int pcl_context_create(int device, void *stream, pcl_context **out)
+{
+    if (!out)
+        return PCL_INVALID_SHAPE;
+    *out = nullptr;
+    hipError_t e = hipSetDevice(device);
+    if (e != hipSuccess) {
+        report("hipSetDevice", e);
+        return PCL_NON_FINITE_VALUE;
+    }
+    auto *ctx = new pcl_context;
+    ctx->device = device;
+    if (stream) {
+        ctx->stream = static_cast<hipStream_t>(stream);
+    } else {
+        e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+        if (e != hipSuccess) {
+            report("stream creation", e);
+            delete ctx;
+            return PCL_NON_FINITE_VALUE;
+        }
+        ctx->own_stream = true;
+    }
+    e = hipMalloc(&ctx->err, sizeof(int));
+    if (e == hipSuccess)
+        e = hipMemsetAsync(ctx->err, 0, sizeof(int), ctx->stream);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        report("error flag", e);
+        pcl_context_destroy(ctx);
+        return PCL_NON_FINITE_VALUE;
+    }
+    *out = ctx;
+    return PCL_OK;
+}
+
+void pcl_context_destroy(pcl_context *ctx)
+{
+    if (!ctx)
+        return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream)
+        (void)hipStreamSynchronize(ctx->stream);
+    for (int i = 0; i < 5; ++i)
+        if (ctx->stage[i])
+            (void)hipFree(ctx->stage[i]);
+    if (ctx->ws)
+        (void)hipFree(ctx->ws);
+    if (ctx->err)
+        (void)hipFree(ctx->err);
+    if (ctx->own_stream && ctx->stream)
+        (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+void *pcl_context_stream(pcl_context *ctx)
+{
+    return ctx ? ctx->stream : nullptr;
+}
+
+int pcl_context_reserve(pcl_context *ctx, size_t bytes)
+{
+    if (!ctx)
+        return PCL_INVALID_SHAPE;
+    (void)hipSetDevice(ctx->device);
+    return ensure_workspace(ctx, bytes);
+}
+
+size_t pcl_attention_workspace_bytes(const pcl_attention_desc *desc)
+{
+    if (!desc)
+        return 0;
+    Plan plan;
+    if (make_plan(*desc, desc->kh_first * (desc->kvheads ? desc->qheads / desc->kvheads : 0),
+                  desc->kh_end * (desc->kvheads ? desc->qheads / desc->kvheads : 0),
+                  desc->kh_first * (desc->kvheads ? desc->qheads / desc->kvheads : 0),
+                  &plan) != PCL_OK)
+        return 0;
+    return plan.ws_floats * sizeof(float);
+}
+
+int pcl_attention_resolve_kernel(const pcl_attention_desc *desc)
+{
+    if (!desc || desc->kvheads <= 0)
+        return -1;
+    const int64_t group = desc->qheads / desc->kvheads;
+    Plan plan;
+    if (make_plan(*desc, desc->kh_first * group, desc->kh_end * group, desc->kh_first * group,
+                  &plan) != PCL_OK)
+        return -1;
+    return plan.kernel;
+}
+
+int pcl_attention_launch(pcl_context *ctx, const pcl_attention_desc *desc)
+{
+    if (!ctx || !desc)
+        return PCL_INVALID_SHAPE;
+    if (desc->kvheads <= 0 || desc->qheads % desc->kvheads != 0)
+        return PCL_INVALID_SHAPE;
+    const int64_t group = desc->qheads / desc->kvheads;
+    Plan plan;
+    const int rc = make_plan(*desc, desc->kh_first * group, desc->kh_end * group,
+                             desc->kh_first * group, &plan);
+    if (rc != PCL_OK)
+        return rc;
+    (void)hipSetDevice(ctx->device);
+    return run_plan(ctx, plan);
+}
+
+int pcl_context_sync(pcl_context *ctx, int *device_error)
+{
+    if (!ctx)
+        return PCL_INVALID_SHAPE;
+    (void)hipSetDevice(ctx->device);
+    int h = 0;
+    hipError_t e = hipMemcpyAsync(&h, ctx->err, sizeof(int), hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(ctx->stream);
+    if (e == hipSuccess && h != 0)
+        e = hipMemsetAsync(ctx->err, 0, sizeof(int), ctx->stream);
+    if (e == hipSuccess && h != 0)
+        e = hipStreamSynchronize(ctx->stream);
+    if (device_error)
+        *device_error = h;
+    if (e != hipSuccess) {
+        report("synchronize", e);
+        return PCL_NON_FINITE_VALUE;
+    }
+    return PCL_OK;
+}
+
+bool pcl_hip_attention_f32_heads(const float *query, const float *keys, const float *values,
+                                 size_t qheads, size_t kvheads, size_t dim, size_t nkeys,
+                                 const uint8_t *allowed, float *scratch, float *out,
+                                 size_t h_first, size_t h_end)
+{
+    (void)scratch; // the device keeps its own score storage
+    if (h_first > h_end || h_end > qheads)
+        return false;
+    if (dim % 16 != 0 || dim == 0 || kvheads == 0 || qheads % kvheads != 0 || dim > kMaxDim)
+        return false;
+    if (h_first == h_end)
+        return true;
+    if (nkeys == 0)
+        return false;
+    const size_t group = qheads / kvheads;
+    pcl_attention_desc d;
+    std::memset(&d, 0, sizeof d);
+    d.q_stride = (int64_t)(qheads * dim);
+    d.nq = 1;
+    d.n0 = (int64_t)nkeys;
+    d.qheads = (int64_t)qheads;
+    d.kvheads = (int64_t)kvheads;
+    d.dim = (int64_t)dim;
+    d.kh_first = (int64_t)(h_first / group);
+    d.kh_end = (int64_t)((h_end - 1) / group + 1);
+    d.mask_stride = (int64_t)nkeys;
+    d.q_scale = 1.0f;
+    d.kernel = PCL_KERNEL_AUTO;
+    const size_t olen = (h_end - h_first) * dim;
+    return run_host(query, qheads * dim, keys, values, nkeys * kvheads * dim, allowed, nkeys, d,
+                    (int64_t)h_first, (int64_t)h_end, (int64_t)h_first, out, 1, olen, olen);
+}
+
+bool pcl_hip_attention_f32_multi_kv(const float *query, size_t nq, size_t q_stride,
+                                    const float *keys, const float *values, size_t qheads,
+                                    size_t kvheads, size_t dim, size_t nkeys,
+                                    const uint8_t *allowed, size_t mask_stride, float *scratch,
+                                    float *out, size_t o_stride, size_t kh_first, size_t kh_end)
+{
+    (void)scratch;
+    if (dim % 16 != 0 || dim == 0 || kvheads == 0 || qheads % kvheads != 0 || dim > kMaxDim)
+        return false;
+    if (kh_first >= kh_end || kh_end > kvheads)
+        return false;
+    const size_t group = qheads / kvheads;
+    const size_t olen = (kh_end - kh_first) * group * dim;
+    if (q_stride < qheads * dim || o_stride < olen || (allowed && mask_stride < nkeys))
+        return false;
+    if (nq == 0)
+        return true;
+    if (nkeys == 0)
+        return false;
+    // The device reads queries and outputs with 16-byte vectors: keep the
+    // strides a multiple of four floats on the device side.
+    const size_t dq_stride = (size_t)round_up((int64_t)q_stride, 4);
+    const size_t do_stride = (size_t)round_up((int64_t)olen, 4);
+    std::vector<float> qbuf;
+    const float *qsrc = query;
+    size_t q_floats = (nq - 1) * q_stride + qheads * dim;
+    if (dq_stride != q_stride) {
+        qbuf.assign(nq * dq_stride, 0.0f);
+        for (size_t i = 0; i < nq; ++i)
+            std::memcpy(&qbuf[i * dq_stride], query + i * q_stride, qheads * dim * sizeof(float));
+        qsrc = qbuf.data();
+        q_floats = qbuf.size();
+    }
+    pcl_attention_desc d;
+    std::memset(&d, 0, sizeof d);
+    d.q_stride = (int64_t)dq_stride;
+    d.nq = (int64_t)nq;
+    d.n0 = (int64_t)nkeys;
+    d.qheads = (int64_t)qheads;
+    d.kvheads = (int64_t)kvheads;
+    d.dim = (int64_t)dim;
+    d.kh_first = (int64_t)kh_first;
+    d.kh_end = (int64_t)kh_end;
+    d.mask_stride = (int64_t)mask_stride;
+    d.q_scale = 1.0f;
+    d.kernel = PCL_KERNEL_AUTO;
+    const size_t mask_bytes = allowed ? (nq - 1) * mask_stride + nkeys : 0;
+    std::vector<float> obuf;
+    float *odst = out;
+    if (do_stride != o_stride) {
+        obuf.assign(nq * do_stride, 0.0f);
+        odst = obuf.data();
+    }
+    const int64_t h0 = (int64_t)(kh_first * group);
+    const bool ok = run_host(qsrc, q_floats, keys, values, nkeys * kvheads * dim, allowed,
+                             mask_bytes, d, h0, (int64_t)(kh_end * group), h0, odst, nq, olen,
+                             do_stride);
+    if (ok && odst != out)
+        for (size_t i = 0; i < nq; ++i)
+            std::memcpy(out + i * o_stride, &obuf[i * do_stride], olen * sizeof(float));
+    return ok;
+}
+
+// attention_with (src/kernels/quantized/int8.rs:596-663) for this backend.
+int pcl_attention_heads(const float *query, size_t query_len, const float *keys,
+                        size_t keys_len, const float *values, size_t values_len,
+                        size_t kv_heads, size_t head_dim, const uint8_t *allowed,
+                        size_t mask_len, int has_mask, size_t h_first, size_t h_end,
+                        int has_heads, float *out)
+{
+    if (kv_heads == 0 || head_dim == 0 || kv_heads > SIZE_MAX / head_dim)
+        return PCL_INVALID_SHAPE;
+    const size_t width = kv_heads * head_dim;
+    if (query_len == 0 || head_dim % 16 != 0 || query_len % head_dim != 0 || keys_len == 0 ||
+        keys_len % width != 0 || values_len != keys_len)
+        return PCL_INVALID_SHAPE;
+    const size_t qheads = query_len / head_dim;
+    const size_t nkeys = keys_len / width;
+    if (qheads % kv_heads != 0)
+        return PCL_INVALID_SHAPE;
+    std::vector<uint8_t> mask;
+    if (has_mask) {
+        if (mask_len != nkeys)
+            return PCL_INVALID_SHAPE;
+        mask.resize(nkeys);
+        bool any = false;
+        for (size_t t = 0; t < nkeys; ++t) {
+            mask[t] = allowed[t] != 0;
+            any |= mask[t] != 0;
+        }
+        if (!any)
+            return PCL_INVALID_PARAMETER;
+    }
+    if (!has_heads) {
+        h_first = 0;
+        h_end = qheads;
+    }
+    if (h_first > h_end || h_end > qheads)
+        return PCL_INVALID_SHAPE;
+    if (!all_finite(query, query_len))
+        return PCL_NON_FINITE_VALUE;
+    const bool ok = pcl_hip_attention_f32_heads(query, keys, values, qheads, kv_heads, head_dim,
+                                                nkeys, has_mask ? mask.data() : nullptr,
+                                                nullptr, out, h_first, h_end);
+    return ok ? PCL_OK : PCL_NON_FINITE_VALUE;
+}
+
+// attention_multi_with (src/kernels/quantized/int8.rs:489-573) for this backend.
+int pcl_attention_multi_kv(const float *const *queries, size_t nq, size_t query_len,
+                           const float *keys, size_t keys_len, const float *values,
+                           size_t values_len, size_t kv_heads, size_t head_dim,
+                           const uint8_t *const *masks, size_t mask_len, size_t kv_first,
+                           size_t kv_end, float *out)
+{
+    if (nq == 0)
+        return PCL_OK;
+    if (kv_first >= kv_end || kv_end > kv_heads)
+        return PCL_INVALID_SHAPE;
+    if (kv_heads == 0 || head_dim == 0 || kv_heads > SIZE_MAX / head_dim)
+        return PCL_INVALID_SHAPE;
+    const size_t width = kv_heads * head_dim;
+    if (query_len == 0 || head_dim % 16 != 0 || query_len % head_dim != 0 || keys_len == 0 ||
+        keys_len % width != 0 || values_len != keys_len ||
+        (query_len / head_dim) % kv_heads != 0)
+        return PCL_INVALID_SHAPE;
+    const size_t nkeys = keys_len / width;
+    std::vector<uint8_t> mask;
+    if (masks) {
+        if (mask_len != nkeys)
+            return PCL_INVALID_SHAPE;
+        mask.resize(nq * nkeys);
+        for (size_t i = 0; i < nq; ++i) {
+            bool any = false;
+            for (size_t t = 0; t < nkeys; ++t) {
+                mask[i * nkeys + t] = masks[i][t] != 0;
+                any |= mask[i * nkeys + t] != 0;
+            }
+            if (!any)
+                return PCL_INVALID_PARAMETER;
+        }
+    }
+    for (size_t i = 0; i < nq; ++i)
+        if (!all_finite(queries[i], query_len))
+            return PCL_NON_FINITE_VALUE;
+    std::vector<float> flat(nq * query_len);
+    for (size_t i = 0; i < nq; ++i)
+        std::memcpy(&flat[i * query_len], queries[i], query_len * sizeof(float));
+    const size_t group = query_len / head_dim / kv_heads;
+    const size_t olen = (kv_end - kv_first) * group * head_dim;
+    const bool ok = pcl_hip_attention_f32_multi_kv(
+        flat.data(), nq, query_len, keys, values, query_len / head_dim, kv_heads, head_dim, nkeys,
+        masks ? mask.data() : nullptr, nkeys, nullptr, out, olen, kv_first, kv_end);
+    return ok ? PCL_OK : PCL_NON_FINITE_VALUE;
+}
+
+} // extern "C"

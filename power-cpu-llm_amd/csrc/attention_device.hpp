@@ -1,0 +1,200 @@
+// Canonical arithmetic of the attention backend (gfx950 device code).
+//
+// Every kernel in this library computes one (query, head) row with exactly
+// the operation sequence defined here, so results are bitwise independent of
+// which kernel ran, how rows were batched and how keys were split between
+// workgroups:
+//
+//   keys are cut into chunks of kChunk = 256 keys (by key index), a chunk
+//   into tiles of kTile = 32 keys, a tile into two MFMA blocks of 16 keys;
+//
+//   score s[key][row]: one v_mfma_f32_16x16x4f32 chain (A = 16 keys x 4
+//   dims, B = 4 dims x 16 rows) over u = 0..DK/32-1, jj = 0..7, the lane
+//   group g = lane/16 supplying dim 32u + 8g + jj;
+//
+//   per tile, online softmax inside the chunk (state m, l, O):
+//     t_max = max over allowed scores; m' = max(m, t_max);
+//     ms = m' or 0 when m' = -inf; alpha = exp(m - ms);
+//     p = allowed ? exp(s - ms) : 0; l = fma(l, alpha, rowsum(p));
+//     O = O * alpha, then O += P.V by one MFMA chain per 16x16 output block
+//     over (b, r) = (0..1, 0..3), the lane group g supplying key
+//     16b + 4g + r;
+//
+//   chunks are merged in ascending order into (M, L, Acc) starting from
+//   (-inf, 0, 0): M' = max(M, m); a = exp(M - Ms); b = exp(m - Ms);
+//   L = fma(L, a, l*b); Acc = fma(Acc, a, O*b); the output is Acc / L.
+//
+// A tile or chunk with no allowed key for a row leaves that row's state
+// bit-unchanged through these formulas, so kernels may skip such work.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pcl {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTile = 32;
+constexpr int kChunk = 256;
+constexpr int kTilesPerChunk = kChunk / kTile;
+constexpr int kRows = 16;
+constexpr float kLog2e = 1.44269504088896340736f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+enum ErrorBits { kErrScore = 1, kErrOutput = 2 };
+
+// Launch parameters shared by every kernel (host fills, passed by value).
+struct Params {
+    // queries: query i, head h at q + i*q_stride + h*dim
+    const float *q;
+    int64_t q_stride;
+    int nq;
+    float q_scale;
+    // keys/values: key t < n0 in segment 0, the rest in segment 1
+    const float *k0, *v0;
+    int64_t n0;
+    const float *k1, *v1;
+    int64_t nkeys;
+    int64_t kv_stride; // floats between consecutive keys (kvheads*dim)
+    int dim, group;
+    int kh_first; // first KV head of the launch
+    int nkv;      // KV heads in the launch
+    int h_lo, h_hi; // query heads written
+    // masks
+    const uint8_t *mask;
+    int64_t mask_stride;
+    int causal;
+    int64_t window;
+    int64_t first_key, first_query;
+    // output: query i, head h at out + i*o_stride + (h - h_base)*dim
+    float *out;
+    int64_t o_stride;
+    int h_base;
+    // rows: flat (query, head-in-group) index f = query*group + j
+    int nrows;     // nq*group
+    int nrows_pad; // rounded up to whole 16-row units
+    int units;     // nrows_pad / 16
+    // chunk partials for the ordered combine
+    float *ws_o;  // [nkv][nrows_pad][nch][DK]
+    float *ws_ml; // [nkv][nrows_pad][nch][2]
+    int c_lo;     // first chunk of the launch
+    int nch;      // chunks of the launch
+    int dk;       // padded head dim of the launch
+    int *err;
+};
+
+__device__ __forceinline__ f4 mfma(float a, float b, f4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// exp(x) as 2^(x*log2 e) on the hardware exp2; exp(0) = 1 and exp(-inf) = 0
+// exactly, which the skip rules above rely on.
+__device__ __forceinline__ float fexp(float x)
+{
+    return __builtin_amdgcn_exp2f(x * kLog2e);
+}
+
+__device__ __forceinline__ bool is_finite(float x)
+{
+    return __builtin_isfinite(x);
+}
+
+__device__ __forceinline__ const float *key_row(const Params &p, int64_t t)
+{
+    return t < p.n0 ? p.k0 + t * p.kv_stride : p.k1 + (t - p.n0) * p.kv_stride;
+}
+
+__device__ __forceinline__ const float *value_row(const Params &p, int64_t t)
+{
+    return t < p.n0 ? p.v0 + t * p.kv_stride : p.v1 + (t - p.n0) * p.kv_stride;
+}
+
+// Whether flat row `row` may attend key index `t`.
+__device__ __forceinline__ bool allowed(const Params &p, int row, int64_t t)
+{
+    if (row >= p.nrows || t >= p.nkeys)
+        return false;
+    const int query = row / p.group;
+    if (p.mask)
+        return p.mask[(int64_t)query * p.mask_stride + t] != 0;
+    if (!p.causal)
+        return true;
+    const int64_t kp = p.first_key + t;
+    const int64_t qp = p.first_query + query;
+    return kp <= qp && (p.window == 0 || qp - kp < p.window);
+}
+
+// Max of a tile's allowed scores for the lane's row (column lane%16): the
+// lane's eight values, then across the four lane groups.
+__device__ __forceinline__ float tile_max(const float s[2][4], const bool ok[2][4])
+{
+    float m = kNegInf;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            m = ok[b][r] ? fmaxf(m, s[b][r]) : m;
+    m = fmaxf(m, __shfl_xor(m, 16));
+    m = fmaxf(m, __shfl_xor(m, 32));
+    return m;
+}
+
+// p = exp(s - ms) for allowed keys (0 otherwise) and their row sum, by a
+// fixed tree: in-lane pairs, then lane groups xor 16, xor 32.
+__device__ __forceinline__ float tile_probs(const float s[2][4], const bool ok[2][4], float ms,
+                                            float p[2][4])
+{
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            p[b][r] = ok[b][r] ? fexp(s[b][r] - ms) : 0.0f;
+    const float x0 = (p[0][0] + p[0][1]) + (p[0][2] + p[0][3]);
+    const float x1 = (p[1][0] + p[1][1]) + (p[1][2] + p[1][3]);
+    float x = x0 + x1;
+    x = x + __shfl_xor(x, 16);
+    x = x + __shfl_xor(x, 32);
+    return x;
+}
+
+// Safe subtrahend for a running max (0 when nothing was allowed yet).
+__device__ __forceinline__ float safe_max(float m)
+{
+    return m == kNegInf ? 0.0f : m;
+}
+
+// Factors of the ordered chunk merge.
+struct MergeFactors {
+    float m, a, b;
+};
+
+__device__ __forceinline__ MergeFactors merge_factors(float M, float m)
+{
+    MergeFactors f;
+    f.m = fmaxf(M, m);
+    const float ms = safe_max(f.m);
+    f.a = fexp(M - ms);
+    f.b = fexp(m - ms);
+    return f;
+}
+
+__device__ __forceinline__ float merge_value(float acc, float o, const MergeFactors &f)
+{
+    return __builtin_fmaf(acc, f.a, o * f.b);
+}
+
+// True when any allowed score of the lane is not finite.
+__device__ __forceinline__ bool bad_scores(const float s[2][4], const bool ok[2][4])
+{
+    bool bad = false;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            bad |= ok[b][r] && !is_finite(s[b][r]);
+    return bad;
+}
+
+} // namespace pcl
