@@ -139,9 +139,11 @@ typedef struct pcl_attention_desc {
     int32_t kernel; /* enum pcl_kernel */
 } pcl_attention_desc;
 
-/* Create a context on a device. stream NULL: the context owns a new
- * non-blocking stream; otherwise launches go to the given hipStream_t. */
-int pcl_context_create(int device, void *stream, pcl_context **out);
+/* Create a context on a device that owns a new non-blocking stream. */
+int pcl_context_create(int device, pcl_context **out);
+/* Create a context that launches on the caller's hipStream_t `stream`
+ * (NULL = the device's null stream); the caller keeps ownership. */
+int pcl_context_create_on_stream(int device, void *stream, pcl_context **out);
 void pcl_context_destroy(pcl_context *ctx);
 /* The stream launches go to (a hipStream_t). */
 void *pcl_context_stream(pcl_context *ctx);

@@ -38,6 +38,7 @@ EXPORTS = (
     "pcl_attention_heads",
     "pcl_attention_multi_kv",
     "pcl_context_create",
+    "pcl_context_create_on_stream",
     "pcl_context_destroy",
     "pcl_context_stream",
     "pcl_attention_launch",
@@ -91,6 +92,14 @@ def load():
     if not os.path.exists(LIB_PATH):
         raise RuntimeError("libpcl_attention.so is not built: run power-cpu-llm_amd/build.py "
                            "(or __graft_entry__.build())")
+    # One HIP runtime per process. PyTorch bundles its own libamdhip64 and
+    # loads it under a different file name; if this library's ROCm runtime
+    # were loaded first, torch would load a second one and fail to see the
+    # GPU. Importing torch first makes this library bind to torch's runtime.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(LIB_PATH)
     fp, vp, sz, u8p = (ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_size_t,
                        ctypes.POINTER(ctypes.c_uint8))
@@ -106,7 +115,9 @@ def load():
     lib.pcl_attention_multi_kv.argtypes = [ctypes.POINTER(fp), sz, sz, fp, sz, fp, sz, sz, sz,
                                            ctypes.POINTER(u8p), sz, sz, sz, fp]
     lib.pcl_context_create.restype = ctypes.c_int
-    lib.pcl_context_create.argtypes = [ctypes.c_int, vp, ctypes.POINTER(vp)]
+    lib.pcl_context_create.argtypes = [ctypes.c_int, ctypes.POINTER(vp)]
+    lib.pcl_context_create_on_stream.restype = ctypes.c_int
+    lib.pcl_context_create_on_stream.argtypes = [ctypes.c_int, vp, ctypes.POINTER(vp)]
     lib.pcl_context_destroy.restype = None
     lib.pcl_context_destroy.argtypes = [vp]
     lib.pcl_context_stream.restype = vp
@@ -242,12 +253,18 @@ def raw_multi_kv(query, nq, q_stride, keys, values, qheads, kvheads, dim, nkeys,
 
 class Context:
     """The device-resident entry (pcl_context). Pointers are device addresses
-    (ints); torch tensors work through data_ptr()."""
+    (ints); torch tensors work through data_ptr(). stream None: the context
+    owns a new stream; otherwise a hipStream_t handle (0 = null stream), e.g.
+    torch.cuda.current_stream().cuda_stream."""
 
     def __init__(self, device=0, stream=None):
         self.lib = load()
         self.handle = ctypes.c_void_p()
-        rc = self.lib.pcl_context_create(device, stream, ctypes.byref(self.handle))
+        if stream is None:
+            rc = self.lib.pcl_context_create(device, ctypes.byref(self.handle))
+        else:
+            rc = self.lib.pcl_context_create_on_stream(device, ctypes.c_void_p(stream or None),
+                                                       ctypes.byref(self.handle))
         if rc != OK:
             raise AttentionError(rc)
 

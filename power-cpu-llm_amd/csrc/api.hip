@@ -246,7 +246,7 @@ pcl_context *abi_context()
         int dev = 0;
         if (hipGetDevice(&dev) != hipSuccess)
             dev = 0;
-        if (pcl_context_create(dev, nullptr, &g_abi_ctx) != PCL_OK)
+        if (pcl_context_create(dev, &g_abi_ctx) != PCL_OK)
             g_abi_ctx = nullptr;
     }
     return g_abi_ctx;
@@ -344,7 +344,7 @@ const char *pcl_version(void)
     return "pcl_attention 0.1 gfx950 (mfma_f32_16x16x4f32, chunk 256, tile 32)";
 }
 
-int pcl_context_create(int device, void *stream, pcl_context **out)
+static int context_create(int device, bool own, void *stream, pcl_context **out)
 {
     if (!out)
         return PCL_INVALID_SHAPE;
@@ -356,7 +356,7 @@ int pcl_context_create(int device, void *stream, pcl_context **out)
     }
     auto *ctx = new pcl_context;
     ctx->device = device;
-    if (stream) {
+    if (!own) {
         ctx->stream = static_cast<hipStream_t>(stream);
     } else {
         e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
@@ -379,6 +379,16 @@ int pcl_context_create(int device, void *stream, pcl_context **out)
     }
     *out = ctx;
     return PCL_OK;
+}
+
+int pcl_context_create(int device, pcl_context **out)
+{
+    return context_create(device, true, nullptr, out);
+}
+
+int pcl_context_create_on_stream(int device, void *stream, pcl_context **out)
+{
+    return context_create(device, false, stream, out);
 }
 
 void pcl_context_destroy(pcl_context *ctx)

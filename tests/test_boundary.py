@@ -1,0 +1,104 @@
+"""The C ABI boundary on the CPU: the library loads, exports every symbol
+include/pcl_attention.h declares, and rejects what the reference wrappers
+reject before any device work (no GPU needed for these paths)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "pcl_attention.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pcl_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(pcl):
+    lib = pcl.load()
+    names = declared_functions()
+    assert len(names) >= 14
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(pcl.EXPORTS)
+    assert b"gfx950" in lib.pcl_version()
+
+
+def test_library_is_built_for_gfx950_only(pcl):
+    data = open(pcl.library_path(), "rb").read()
+    assert b"gfx950" in data
+    for other in (b"gfx942", b"gfx90a", b"gfx1100"):
+        assert b"amdgcn-amd-amdhsa--" + other not in data
+
+
+def test_checked_wrapper_rejects_shapes_before_device_work(pcl):
+    # attention_with (src/kernels/quantized/int8.rs:607-636) validation
+    k = pcl.HipKernels()
+    q = np.ones(32, np.float32)
+    kv = np.ones(64, np.float32)
+    cases = [
+        (lambda: k.attention(q, kv, kv, 0, 32), "InvalidShape"),          # kv heads 0
+        (lambda: k.attention(q, kv, kv, 1, 0), "InvalidShape"),           # dim 0
+        (lambda: k.attention(q[:24], kv[:24], kv[:24], 1, 24), "InvalidShape"),  # dim % 16
+        (lambda: k.attention(q, kv, kv[:32], 1, 32), "InvalidShape"),     # len(V) != len(K)
+        (lambda: k.attention(q, kv[:48], kv[:48], 1, 32), "InvalidShape"),  # K not whole rows
+        (lambda: k.attention(np.ones(48, np.float32), kv, kv, 2, 16), "InvalidShape"),  # 3 % 2
+        (lambda: k.attention(q, kv, kv, 1, 32, [True]), "InvalidShape"),  # mask length
+        (lambda: k.attention(q, kv, kv, 1, 32, [False, False]), "InvalidParameter"),
+        (lambda: k.attention_heads(q, kv, kv, 1, 32, None, (0, 2)), "InvalidShape"),
+        (lambda: k.attention_heads(q, kv, kv, 1, 32, None, (1, 0)), "InvalidShape"),
+        (lambda: k.attention(np.full(32, np.nan, np.float32), kv, kv, 1, 32), "NonFiniteValue"),
+        (lambda: k.attention_multi_kv([q], kv, kv, 1, 32, None, (0, 0)), "InvalidShape"),
+        (lambda: k.attention_multi_kv([q], kv, kv, 1, 32, None, (0, 2)), "InvalidShape"),
+        (lambda: k.attention_multi([q, q], kv, kv, 1, 32, [[True, False], [False, False]]),
+         "InvalidParameter"),
+        (lambda: k.attention_multi([q], kv, kv, 1, 32, [[True]]), "InvalidShape"),
+        (lambda: k.attention_multi([np.full(32, np.inf, np.float32)], kv, kv, 1, 32),
+         "NonFiniteValue"),
+    ]
+    for fn, kind in cases:
+        with pytest.raises(pcl.AttentionError) as e:
+            fn()
+        assert e.value.kind == kind
+    assert k.attention_multi([], kv, kv, 1, 32) == []
+
+
+def test_raw_entries_reject_geometry_before_device_work(pcl):
+    one = np.ones(64, np.float32)
+    assert not pcl.raw_heads(one, one, one, 2, 1, 32, 1, None, 1, 3)[0]   # h_end > qheads
+    assert not pcl.raw_heads(one, one, one, 2, 1, 32, 1, None, 2, 1)[0]   # h_first > h_end
+    assert not pcl.raw_heads(one, one, one, 2, 0, 32, 1, None, 0, 1)[0]   # kvheads 0
+    assert not pcl.raw_heads(one, one, one, 3, 2, 16, 1, None, 0, 1)[0]   # qheads % kvheads
+    assert not pcl.raw_heads(one, one, one, 1, 1, 1024, 1, None, 0, 1)[0]  # dim > 512
+    assert not pcl.raw_multi_kv(one, 1, 32, one, one, 2, 1, 16, 1, None, 1, 32, 1, 1)[0]
+    assert not pcl.raw_multi_kv(one, 1, 16, one, one, 2, 1, 16, 1, None, 1, 32, 0, 1)[0]
+
+
+def test_descriptor_validation_on_the_host(pcl):
+    # workspace sizing and kernel choice run on the host only
+    d = pcl.Context.desc(q=16, q_stride=16 * 256, nq=1, k0=16, v0=16, n0=32768, qheads=16,
+                         kvheads=8, dim=256, kh_first=0, kh_end=8, causal=1, first_query=32767,
+                         out=16, o_stride=16 * 256)
+    lib = pcl.load()
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_SPLIT_KV
+    assert lib.pcl_attention_workspace_bytes(ctypes.byref(d)) > 0
+    d.window = 1024
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_SPLIT_KV
+    d.dim = 24
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == -1
+    d.dim, d.nq, d.first_query, d.window, d.n0 = 256, 4096, 0, 0, 4096
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_TILED
+    d.first_key = 5000  # no query sees a key
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == -1
+
+
+def test_product_path_has_no_cpu_fallback():
+    src = open(os.path.join(ROOT, "power-cpu-llm_amd", "__init__.py")).read()
+    assert "oracle" not in src.replace("the oracle", "")
+    for name in os.listdir(os.path.join(ROOT, "power-cpu-llm_amd", "csrc")):
+        text = open(os.path.join(ROOT, "power-cpu-llm_amd", "csrc", name)).read()
+        assert "oracle" not in text

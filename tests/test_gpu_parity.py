@@ -1,0 +1,457 @@
+"""GPU parity of the gfx950 attention backend against the CPU oracle.
+
+Ports the reference's attention tests to this backend (names follow them),
+checks BASELINE.json's five configs against the exact oracle within 1e-4
+max-abs with the same argmax per (query, head) row, and checks the
+size-independent properties the design promises (every kernel gives the
+same bits; head, query and KV-head ranges do not change results).
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+
+from helpers import Rng, normals, prescale, row_argmax_agree
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+THREADS = max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+    assert t.cuda.is_available(), "GPU tests need a GPU"
+    return t
+
+
+@pytest.fixture(scope="module")
+def kernels(pcl):
+    return pcl.HipKernels()
+
+
+@pytest.fixture(scope="module")
+def ctx(pcl, torch):
+    c = pcl.Context(0, torch.cuda.current_stream().cuda_stream)
+    yield c
+    c.close()
+
+
+def bits(x):
+    return np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+
+
+def assert_parity(got, want, dim, tol=TOL):
+    got = np.asarray(got, np.float32).reshape(-1)
+    want = np.asarray(want, np.float32).reshape(-1)
+    assert got.shape == want.shape
+    assert np.all(np.isfinite(got))
+    err = float(np.max(np.abs(got - want))) if got.size else 0.0
+    assert err <= tol, "max abs error %.3g" % err
+    ok, margin = row_argmax_agree(got, want, dim, tol)
+    assert ok, "argmax differs with top-1/top-2 margin %.3g" % margin
+    return err
+
+
+# ---- the engine interface (host pointers), reference tests ported ---------
+
+TWIN_GEOMETRIES = [
+    (16, 8, 256, 37), (16, 2, 512, 5), (4, 4, 16, 1), (2, 1, 32, 64), (6, 3, 48, 6),
+    (4, 2, 80, 7), (8, 2, 144, 3), (2, 1, 320, 130), (6, 2, 16, 9), (9, 3, 32, 2),
+    (10, 2, 48, 11), (8, 1, 16, 1), (4, 1, 96, 3), (16, 2, 512, 130),
+]
+
+
+def test_attention_f32_matches_reference_on_twin_geometries(kernels, oracle):
+    # src/kernels/quantized/int8/tests.rs:399-476, against the exact oracle
+    rng = Rng(0xa77e)
+    for qheads, kvh, dim, nkeys in TWIN_GEOMETRIES:
+        query = rng.units(qheads * dim, 0.5)
+        keys = rng.units(nkeys * kvh * dim, 0.5)
+        values = rng.units(nkeys * kvh * dim)
+        mask = np.array([t % 3 != 1 or nkeys == 1 for t in range(nkeys)])
+        for allowed in (None, mask):
+            got = kernels.attention(query, keys, values, kvh, dim, allowed)
+            ok, want = oracle.heads(query, keys, values, qheads, kvh, dim, nkeys, allowed)
+            assert ok
+            assert_parity(got, want, dim)
+            assert np.all(np.abs(got - want) <= 2e-5 * (1.0 + np.abs(want)))
+        bad = values.copy()
+        bad[(nkeys - 1) * kvh * dim + dim - 1] = np.inf
+        bad_keys = keys.copy()
+        bad_keys[dim - 1] = np.nan
+        with pytest.raises(Exception) as e:
+            kernels.attention(query, keys, bad, kvh, dim, None)
+        assert getattr(e.value, "kind", "") == "NonFiniteValue"
+        with pytest.raises(Exception) as e:
+            kernels.attention(query, bad_keys, values, kvh, dim, None)
+        assert getattr(e.value, "kind", "") == "NonFiniteValue"
+
+
+def test_attention_rejects_bad_shapes_masks_and_overflow(kernels, pcl):
+    q = np.ones(32, np.float32)
+    kv = np.ones(32, np.float32)
+    with pytest.raises(pcl.AttentionError) as e:
+        kernels.attention(q, kv, kv, 1, 32, [False])
+    assert e.value.kind == "InvalidParameter"
+    with pytest.raises(pcl.AttentionError) as e:
+        kernels.attention(q[:24], kv[:24], kv[:24], 1, 24, None)
+    assert e.value.kind == "InvalidShape"
+    big = np.full(32, np.finfo(np.float32).max, np.float32)
+    with pytest.raises(pcl.AttentionError) as e:
+        kernels.attention(big, big, kv, 1, 32, None)
+    assert e.value.kind == "NonFiniteValue"
+
+
+def test_attention_head_ranges_match_full_attention(kernels, oracle):
+    # int8/tests.rs:594-659: every head range is that slice, bitwise
+    rng = Rng(0x7f4a7c159e3779b9)
+    for qheads, kvh, dim, nkeys in [(16, 8, 32, 7), (8, 1, 64, 33), (4, 2, 16, 1),
+                                    (6, 2, 48, 5), (9, 3, 16, 2)]:
+        query = rng.units(qheads * dim)
+        keys = rng.units(nkeys * kvh * dim)
+        values = rng.units(nkeys * kvh * dim)
+        mask = np.array([t % 3 != 1 or t == 0 for t in range(nkeys)])
+        for allowed in (None, mask):
+            full = kernels.attention(query, keys, values, kvh, dim, allowed)
+            ok, want = oracle.heads(query, keys, values, qheads, kvh, dim, nkeys, allowed)
+            assert_parity(full, want, dim)
+            for a in range(qheads):
+                for b in range(a, qheads + 1):
+                    part = kernels.attention_heads(query, keys, values, kvh, dim, allowed, (a, b))
+                    assert np.array_equal(bits(part), bits(full[a * dim:b * dim])), (a, b)
+            with pytest.raises(Exception):
+                kernels.attention_heads(query, keys, values, kvh, dim, allowed, (0, qheads + 1))
+
+
+def test_attention_multi_matches_single_queries(kernels):
+    # int8/tests.rs:661-706
+    rng = Rng(0x51ed270b)
+    for qheads, kvh, dim, nkeys, nq in [(16, 8, 32, 9, 5), (8, 1, 64, 33, 3), (4, 2, 16, 2, 7),
+                                        (16, 2, 48, 1, 1)]:
+        queries = [rng.units(qheads * dim) for _ in range(nq)]
+        keys = rng.units(nkeys * kvh * dim)
+        values = rng.units(nkeys * kvh * dim)
+        masks = [np.array([t <= nkeys // 2 + i or t == 0 for t in range(nkeys)])
+                 for i in range(nq)]
+        for masked in (False, True):
+            m = masks if masked else None
+            multi = kernels.attention_multi(queries, keys, values, kvh, dim, m)
+            for i, q in enumerate(queries):
+                single = kernels.attention(q, keys, values, kvh, dim, m[i] if m else None)
+                assert np.array_equal(bits(multi[i]), bits(single))
+
+
+def test_attention_multi_kv_ranges_match_single_queries(kernels, oracle):
+    # int8/tests.rs:708-768: sliding windows, more keys than one block
+    rng = Rng(0x7a11ed)
+    for qheads, kvh, dim, nkeys, nq, window in [(16, 2, 512, 150, 6, 40),
+                                                (16, 8, 256, 300, 5, 130),
+                                                (4, 2, 16, 37, 9, 5)]:
+        queries = [rng.units(qheads * dim) for _ in range(nq)]
+        keys = rng.units(nkeys * kvh * dim)
+        values = rng.units(nkeys * kvh * dim)
+        masks = [np.array([t <= nkeys - nq + i and t + window > nkeys - nq + i
+                           for t in range(nkeys)]) for i in range(nq)]
+        group = qheads // kvh
+        for masked in (False, True):
+            m = masks if masked else None
+            singles = [kernels.attention(q, keys, values, kvh, dim, m[i] if m else None)
+                       for i, q in enumerate(queries)]
+            for i, q in enumerate(queries):
+                ok, want = oracle.heads(q, keys, values, qheads, kvh, dim, nkeys,
+                                        m[i] if m else None)
+                assert_parity(singles[i], want, dim)
+            for kv in [(0, kvh), (0, 1), (kvh - 1, kvh)]:
+                part = kernels.attention_multi_kv(queries, keys, values, kvh, dim, m, kv)
+                for i, single in enumerate(singles):
+                    want = single[kv[0] * group * dim:kv[1] * group * dim]
+                    assert np.array_equal(bits(part[i]), bits(want)), (kv, i, masked)
+
+
+def test_attention_score_bounds_handle_holes_and_query_tails(kernels, oracle):
+    # int8/tests.rs:1118-1177: holes, wholly masked blocks, disjoint masks
+    rng = Rng(0x78124)
+    qheads, kvh, nkeys = 3, 3, 259
+    for dim in (48, 256, 512):
+        keys = rng.units(nkeys * kvh * dim)
+        values = np.array([0.0 if i % 13 == 0 else (-0.0 if i % 13 == 1 else rng.unit())
+                           for i in range(nkeys * kvh * dim)], np.float32)
+        for nq in (1, 2, 3, 5):
+            queries = [rng.units(qheads * dim, 0.1) for _ in range(nq)]
+            lives = {0: [5, 7, 13, 17], 1: [129, 131, 139], 2: [255, 257], 3: [258]}
+            masks = [np.isin(np.arange(nkeys), lives[i % 4]) for i in range(nq)]
+            got = kernels.attention_multi_kv(queries, keys, values, kvh, dim, masks, (0, kvh))
+            for i in range(nq):
+                single = kernels.attention(queries[i], keys, values, kvh, dim, masks[i])
+                assert np.array_equal(bits(got[i]), bits(single)), (dim, nq, i)
+                ok, want = oracle.heads(queries[i], keys, values, qheads, kvh, dim, nkeys,
+                                        masks[i])
+                assert_parity(single, want, dim)
+
+
+def test_raw_entries_report_bad_geometry(pcl):
+    ok, _ = pcl.raw_heads(np.ones(32), np.ones(32), np.ones(32), 2, 1, 16, 1, None, 1, 3)
+    assert not ok  # h_end > qheads
+    ok, _ = pcl.raw_heads(np.ones(24), np.ones(24), np.ones(24), 1, 1, 24, 1, None, 0, 1)
+    assert not ok  # dim % 16
+    ok, out = pcl.raw_heads(np.ones(32), np.ones(32), np.ones(32), 2, 1, 16, 1, None, 1, 1)
+    assert ok and out.size == 0  # empty head range
+    ok, _ = pcl.raw_multi_kv(np.ones(32), 1, 32, np.ones(32), np.ones(32), 2, 1, 16, 1, None, 1,
+                             32, 1, 1)
+    assert not ok  # empty KV-head range
+
+
+# ---- device descriptors: every kernel gives the same bits ------------------
+
+def run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel, causal=0, window=0, first_key=0,
+             first_query=0, mask=None, split_at=None, kv=None, q_scale=1.0):
+    """One device launch over numpy inputs; returns (out, error flag)."""
+    dev = torch.device("cuda:0")
+    nq = q.shape[0]
+    nkeys = k.shape[0]
+    kv = kv or (0, kvh)
+    group = qheads // kvh
+    olen = (kv[1] - kv[0]) * group * dim
+    tq = torch.from_numpy(np.ascontiguousarray(q)).to(dev)
+    out = torch.full((nq, olen), float("nan"), device=dev)
+    kw = dict(q=tq.data_ptr(), q_stride=qheads * dim, nq=nq, qheads=qheads, kvheads=kvh,
+              dim=dim, kh_first=kv[0], kh_end=kv[1], causal=causal, window=window,
+              first_key=first_key, first_query=first_query, out=out.data_ptr(), o_stride=olen,
+              kernel=kernel, q_scale=q_scale)
+    keep = [tq, out]
+    if split_at is None:
+        tk = torch.from_numpy(np.ascontiguousarray(k)).to(dev)
+        tv = torch.from_numpy(np.ascontiguousarray(v)).to(dev)
+        kw.update(k0=tk.data_ptr(), v0=tv.data_ptr(), n0=nkeys)
+        keep += [tk, tv]
+    else:
+        parts = [torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+                 for x in (k[:split_at], v[:split_at], k[split_at:], v[split_at:])]
+        kw.update(k0=parts[0].data_ptr(), v0=parts[1].data_ptr(), n0=split_at,
+                  k1=parts[2].data_ptr(), v1=parts[3].data_ptr(), n1=nkeys - split_at)
+        keep += parts
+    if mask is not None:
+        tm = torch.from_numpy(np.ascontiguousarray(mask, dtype=np.uint8)).to(dev)
+        kw.update(mask=tm.data_ptr(), mask_stride=nkeys)
+        keep.append(tm)
+    d = ctx.desc(**kw)
+    ctx.launch(d)
+    err = ctx.sync()
+    return out.cpu().numpy(), err
+
+
+DESC_CASES = [
+    # qheads, kvh, dim, nq, nkeys, causal, window, first_query
+    (16, 8, 256, 1, 2048, 1, 0, 2047),
+    (16, 8, 256, 1, 700, 1, 100, 699),
+    (16, 2, 512, 1, 3000, 1, 0, 2999),
+    (16, 2, 512, 7, 900, 1, 0, 893),
+    (16, 8, 256, 300, 300, 1, 0, 0),
+    (16, 8, 256, 200, 1200, 1, 130, 1000),
+    (16, 8, 256, 64, 600, 0, 0, 0),
+    (8, 2, 128, 100, 500, 1, 0, 400),
+    (4, 4, 64, 70, 333, 1, 33, 263),
+    (6, 3, 48, 20, 90, 1, 0, 70),
+    (10, 2, 80, 33, 517, 1, 0, 484),
+    (16, 16, 16, 9, 1000, 1, 17, 991),
+]
+
+
+@pytest.mark.parametrize("case", DESC_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_every_kernel_gives_identical_bits(torch, ctx, oracle, case):
+    qheads, kvh, dim, nq, nkeys, causal, window, fq = case
+    g = np.random.default_rng(sum(case))
+    q = prescale(g.standard_normal((nq, qheads * dim), dtype=np.float32), dim)
+    k = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+    v = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+    outs = {}
+    for kernel in (1, 2, 3):
+        outs[kernel], err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel, causal,
+                                     window, 0, fq)
+        assert err == 0
+    assert np.array_equal(bits(outs[1]), bits(outs[2]))
+    assert np.array_equal(bits(outs[1]), bits(outs[3]))
+    for i in sorted({0, nq // 2, nq - 1}):
+        m = oracle.encoder_mask(0, nkeys, fq + i, window or None) if causal else None
+        ok, want = oracle.heads(q[i], k, v, qheads, kvh, dim, nkeys, m)
+        assert ok
+        assert_parity(outs[1][i], want, dim)
+
+
+def test_explicit_masks_segments_scale_and_kv_ranges_keep_bits(torch, ctx):
+    qheads, kvh, dim, nq, nkeys = 16, 8, 256, 40, 777
+    g = np.random.default_rng(99)
+    q = g.standard_normal((nq, qheads * dim), dtype=np.float32)
+    k = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+    v = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+    fq = nkeys - nq
+    mask = np.array([[t <= fq + i and fq + i - t < 300 for t in range(nkeys)]
+                     for i in range(nq)])
+    scale = np.float32(1.0 / 16.0)
+    base, err = run_desc(torch, ctx, prescale(q, dim), k, v, qheads, kvh, dim, 1, 1, 300, 0, fq)
+    assert err == 0
+    for kernel in (1, 2, 3):
+        # explicit byte masks equal the descriptor's causal window
+        got, err = run_desc(torch, ctx, prescale(q, dim), k, v, qheads, kvh, dim, kernel,
+                            mask=mask)
+        assert err == 0 and np.array_equal(bits(got), bits(base))
+        # the in-kernel q_scale equals the engine's host pre-scale
+        got, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel, 1, 300, 0, fq,
+                            q_scale=float(scale))
+        assert err == 0 and np.array_equal(bits(got), bits(base))
+        # two KV segments equal one buffer, also across a chunk boundary
+        for split in (256, 301):
+            got, err = run_desc(torch, ctx, prescale(q, dim), k, v, qheads, kvh, dim, kernel, 1,
+                                300, 0, fq, split_at=split)
+            assert err == 0 and np.array_equal(bits(got), bits(base))
+        # a KV-head range is that slice of the full result
+        got, err = run_desc(torch, ctx, prescale(q, dim), k, v, qheads, kvh, dim, kernel, 1,
+                            300, 0, fq, kv=(3, 6))
+        group = qheads // kvh
+        assert err == 0 and np.array_equal(bits(got), bits(base[:, 3 * group * dim:
+                                                                6 * group * dim]))
+
+
+def test_masked_suffix_does_not_change_results(torch, ctx):
+    """Decode of position p over keys [0, p] equals the same query inside a
+    longer call whose later keys are causally masked (chunk-size
+    independence of the engine, docs/architecture.md:34)."""
+    qheads, kvh, dim, nkeys = 16, 8, 256, 1500
+    g = np.random.default_rng(5)
+    q = prescale(g.standard_normal((nkeys, qheads * dim), dtype=np.float32), dim)
+    k = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+    v = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+    full, err = run_desc(torch, ctx, q[1000:1100], k, v, qheads, kvh, dim, 2, 1, 0, 0, 1000)
+    assert err == 0
+    for p in (1000, 1023, 1024, 1050, 1099):
+        one, err = run_desc(torch, ctx, q[p:p + 1], k[:p + 1], v[:p + 1], qheads, kvh, dim, 1,
+                            1, 0, 0, p)
+        assert err == 0 and np.array_equal(bits(one[0]), bits(full[p - 1000]))
+
+
+def test_device_error_flags(torch, ctx):
+    qheads, kvh, dim, nkeys = 4, 2, 64, 300
+    g = np.random.default_rng(8)
+    q = g.standard_normal((3, qheads * dim), dtype=np.float32)
+    k = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+    v = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+    bad_k = k.copy()
+    bad_k[10, 1, 5] = np.nan
+    bad_v = v.copy()
+    bad_v[20, 0, 3] = np.inf
+    for kernel in (1, 2, 3):
+        _, err = run_desc(torch, ctx, q, bad_k, v, qheads, kvh, dim, kernel)
+        assert err & 1
+        _, err = run_desc(torch, ctx, q, k, bad_v, qheads, kvh, dim, kernel)
+        assert err & 2
+        _, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel)
+        assert err == 0
+
+
+# ---- BASELINE.json configs ---------------------------------------------------
+
+def gpu_normals(torch, seed, shape):
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(seed)
+    return torch.randn(shape, generator=gen, device="cuda:0", dtype=torch.float32)
+
+
+def decode_config(torch, ctx, oracle, qheads, kvh, dim, nkeys, window, seed, unit_k=False):
+    q = gpu_normals(torch, seed, (1, qheads, dim)) * float(np.float32(1.0 / math.sqrt(dim)))
+    k = gpu_normals(torch, seed + 1, (nkeys, kvh, dim))
+    v = gpu_normals(torch, seed + 2, (nkeys, kvh, dim))
+    if unit_k:
+        k = k / k.norm(dim=-1, keepdim=True)
+    out = torch.empty((1, qheads, dim), device="cuda:0")
+    d = ctx.desc(q=q.data_ptr(), q_stride=qheads * dim, nq=1, k0=k.data_ptr(), v0=v.data_ptr(),
+                 n0=nkeys, qheads=qheads, kvheads=kvh, dim=dim, kh_first=0, kh_end=kvh,
+                 causal=1, window=window, first_key=0, first_query=nkeys - 1,
+                 out=out.data_ptr(), o_stride=qheads * dim, kernel=0)
+    ctx.launch(d)
+    assert ctx.sync() == 0
+    got = out.cpu().numpy().reshape(-1)
+    qn, kn, vn = (x.cpu().numpy().reshape(-1) for x in (q, k, v))
+    ok, want = oracle.threaded(qn, 1, kn, vn, qheads, kvh, dim, nkeys, True, 0, nkeys - 1,
+                               window, threads=THREADS)
+    assert ok
+    return assert_parity(got, want, dim)
+
+
+def test_config1_decode_2048(torch, ctx, oracle):
+    decode_config(torch, ctx, oracle, 16, 8, 256, 2048, 0, 0x5EED0001)
+
+
+def test_config2_sliding_decode_32k_window_1024(torch, ctx, oracle):
+    decode_config(torch, ctx, oracle, 16, 8, 256, 32768, 1024, 0x5EED0002)
+
+
+def test_config2_full_causal_decode_32k(torch, ctx, oracle):
+    decode_config(torch, ctx, oracle, 16, 8, 256, 32768, 0, 0x5EED0012)
+
+
+def test_config3_global_decode_131072_d512(torch, ctx, oracle):
+    decode_config(torch, ctx, oracle, 16, 2, 512, 131072, 0, 0x5EED0003, unit_k=True)
+
+
+@pytest.mark.parametrize("window", [1024, 0], ids=["window1024", "global"])
+def test_config4_prefill_4096(torch, ctx, oracle, window):
+    qheads, kvh, dim, n = 16, 8, 256, 4096
+    seed = 0x5EED0004
+    q = gpu_normals(torch, seed, (n, qheads, dim)) * float(np.float32(1.0 / 16.0))
+    k = gpu_normals(torch, seed + 1, (n, kvh, dim))
+    v = gpu_normals(torch, seed + 2, (n, kvh, dim))
+    outs = {}
+    for kernel in (2, 1):
+        out = torch.empty((n, qheads, dim), device="cuda:0")
+        d = ctx.desc(q=q.data_ptr(), q_stride=qheads * dim, nq=n, k0=k.data_ptr(),
+                     v0=v.data_ptr(), n0=n, qheads=qheads, kvheads=kvh, dim=dim, kh_first=0,
+                     kh_end=kvh, causal=1, window=window, first_key=0, first_query=0,
+                     out=out.data_ptr(), o_stride=qheads * dim, kernel=kernel)
+        ctx.reserve(ctx.workspace_bytes(d))
+        ctx.launch(d)
+        assert ctx.sync() == 0
+        outs[kernel] = out.cpu().numpy()
+    # the whole 4096 x 16 x 256 output: both kernels agree bitwise
+    assert np.array_equal(bits(outs[1]), bits(outs[2]))
+    qn, kn, vn = (x.cpu().numpy() for x in (q, k, v))
+    rows = sorted(set(list(range(4)) + list(range(1020, 1030)) + list(range(4090, 4096)) +
+                  list(np.random.default_rng(4).choice(n, 24, replace=False))))
+    for i in rows:
+        m = oracle.encoder_mask(0, n, i, window or None)
+        ok, want = oracle.heads(qn[i].reshape(-1), kn.reshape(-1), vn.reshape(-1), qheads, kvh,
+                                dim, n, m)
+        assert ok
+        assert_parity(outs[2][i], want, dim)
+
+
+def test_config5_canvas_48_denoising_steps(torch, ctx, oracle):
+    qheads, kvh, dim, prefix, canvas = 16, 8, 256, 2048, 256
+    kp = gpu_normals(torch, 0x5EED0005, (prefix, kvh, dim))
+    vp = gpu_normals(torch, 0x5EED0105, (prefix, kvh, dim))
+    kpn, vpn = kp.cpu().numpy(), vp.cpu().numpy()
+    rng = np.random.default_rng(48)
+    for step in range(48):
+        seed = 0x5EED0500 + step
+        q = gpu_normals(torch, seed, (canvas, qheads, dim)) * float(np.float32(1.0 / 16.0))
+        kc = gpu_normals(torch, seed + 1000, (canvas, kvh, dim))
+        vc = gpu_normals(torch, seed + 2000, (canvas, kvh, dim))
+        out = torch.empty((canvas, qheads, dim), device="cuda:0")
+        d = ctx.desc(q=q.data_ptr(), q_stride=qheads * dim, nq=canvas, k0=kp.data_ptr(),
+                     v0=vp.data_ptr(), n0=prefix, k1=kc.data_ptr(), v1=vc.data_ptr(), n1=canvas,
+                     qheads=qheads, kvheads=kvh, dim=dim, kh_first=0, kh_end=kvh, causal=0,
+                     out=out.data_ptr(), o_stride=qheads * dim, kernel=0)
+        ctx.reserve(ctx.workspace_bytes(d))
+        ctx.launch(d)
+        assert ctx.sync() == 0
+        got = out.cpu().numpy()
+        kn = np.concatenate([kpn, kc.cpu().numpy()]).reshape(-1)
+        vn = np.concatenate([vpn, vc.cpu().numpy()]).reshape(-1)
+        qn = q.cpu().numpy()
+        for i in rng.choice(canvas, 3, replace=False):
+            ok, want = oracle.heads(qn[i].reshape(-1), kn, vn, qheads, kvh, dim,
+                                    prefix + canvas)
+            assert ok
+            assert_parity(got[i], want, dim)
