@@ -25,6 +25,8 @@ struct pcl_context {
     bool own_stream = false;
     void *ws = nullptr;
     size_t ws_bytes = 0;
+    int *cnt = nullptr; // arrival counters of the split-KV combine (always zero at rest)
+    size_t cnt_ints = 0;
     int *err = nullptr;
     // Staging buffers of the host-pointer entries (grow-only).
     void *stage[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
@@ -171,9 +173,21 @@ int make_plan(const pcl_attention_desc &d, int64_t h_lo, int64_t h_hi, int64_t h
         // the tiled kernel's rows come in whole workgroup blocks
         p.nrows_pad = (int)round_up(nrows, pcl::tiled_rows(dk));
     }
+    const int64_t s_lo = c_lo / pcl::kSpanChunks;
+    const int64_t s_hi = (c_hi - 1) / pcl::kSpanChunks + 1;
+    p.s_lo = (int)s_lo;
+    p.nspan = (int)(s_hi - s_lo);
     const bool partials = plan->kernel == PCL_KERNEL_TILED_SPLIT ||
                           (plan->kernel == PCL_KERNEL_SPLIT_KV && nch > 1);
-    plan->ws_floats = partials ? (size_t)nkv * p.nrows_pad * nch * (dk + 2) : 0;
+    plan->ws_floats = 0;
+    if (partials) {
+        plan->ws_floats = (size_t)nkv * p.nrows_pad * nch * (dk + 2);
+        if (p.nspan > 1)
+            plan->ws_floats += (size_t)nkv * p.nrows_pad * p.nspan * (dk + 2);
+    } else if (plan->kernel == PCL_KERNEL_TILED && p.nspan > 1) {
+        // the tiled kernel's running totals across spans
+        plan->ws_floats = (size_t)nkv * p.nrows_pad * dk;
+    }
     return PCL_OK;
 }
 
@@ -196,19 +210,49 @@ int ensure_workspace(pcl_context *ctx, size_t bytes)
     return PCL_OK;
 }
 
+int ensure_counters(pcl_context *ctx, size_t n)
+{
+    if (n <= ctx->cnt_ints)
+        return PCL_OK;
+    if (ctx->cnt) {
+        (void)hipStreamSynchronize(ctx->stream);
+        (void)hipFree(ctx->cnt);
+        ctx->cnt = nullptr;
+        ctx->cnt_ints = 0;
+    }
+    hipError_t e = hipMalloc(&ctx->cnt, n * sizeof(int));
+    if (e == hipSuccess)
+        e = hipMemsetAsync(ctx->cnt, 0, n * sizeof(int), ctx->stream);
+    if (e != hipSuccess) {
+        report("counter allocation", e);
+        return PCL_NON_FINITE_VALUE;
+    }
+    ctx->cnt_ints = n;
+    return PCL_OK;
+}
+
 int run_plan(pcl_context *ctx, Plan &plan)
 {
     if (plan.empty)
         return PCL_OK;
     Params &p = plan.p;
     p.err = ctx->err;
+    // The split-KV kernel can merge its chunks itself (p.cnt, arrival
+    // counters), but on gfx950 the two combine kernels are faster at the
+    // sizes measured, so the counters stay unused (p.cnt = nullptr).
+    (void)ensure_counters;
     if (plan.ws_floats) {
         const int rc = ensure_workspace(ctx, plan.ws_floats * sizeof(float));
         if (rc != PCL_OK)
             return rc;
         const size_t o_floats = (size_t)p.nkv * p.nrows_pad * p.nch * p.dk;
+        const size_t ml_floats = (size_t)p.nkv * p.nrows_pad * p.nch * 2;
         p.ws_o = static_cast<float *>(ctx->ws);
         p.ws_ml = p.ws_o + o_floats;
+        if (p.nspan > 1) {
+            p.ws2_o = p.ws_ml + ml_floats;
+            p.ws2_ml = p.ws2_o + (size_t)p.nkv * p.nrows_pad * p.nspan * p.dk;
+        }
     }
     hipError_t e = hipSuccess;
     switch (plan.kernel) {
@@ -403,6 +447,8 @@ void pcl_context_destroy(pcl_context *ctx)
             (void)hipFree(ctx->stage[i]);
     if (ctx->ws)
         (void)hipFree(ctx->ws);
+    if (ctx->cnt)
+        (void)hipFree(ctx->cnt);
     if (ctx->err)
         (void)hipFree(ctx->err);
     if (ctx->own_stream && ctx->stream)

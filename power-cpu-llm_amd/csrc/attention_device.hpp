@@ -20,12 +20,21 @@
 //     over (b, r) = (0..1, 0..3), the lane group g supplying key
 //     16b + 4g + r;
 //
-//   chunks are merged in ascending order into (M, L, Acc) starting from
-//   (-inf, 0, 0): M' = max(M, m); a = exp(M - Ms); b = exp(m - Ms);
-//   L = fma(L, a, l*b); Acc = fma(Acc, a, O*b); the output is Acc / L.
+//   merge of a partial (m, l, O) into (M, L, Acc): M' = max(M, m);
+//   a = exp(M - Ms); b = exp(m - Ms) with Ms = M' or 0 when M' = -inf;
+//   L = fma(L, a, l*b); Acc = fma(Acc, a, O*b);
 //
-// A tile or chunk with no allowed key for a row leaves that row's state
-// bit-unchanged through these formulas, so kernels may skip such work.
+//   chunks are grouped into spans of kSpanChunks = 16 chunks (4096 keys, by
+//   chunk index): the chunks of a span are merged in ascending order from
+//   (-inf, 0, 0), then the spans are merged in ascending order from
+//   (-inf, 0, 0); the output is Acc / L. Two levels keep the longest serial
+//   merge chain of the split-KV combine short (16 + keys/4096 steps).
+//
+// A tile, chunk or span with no allowed key for a row leaves that row's
+// state bit-unchanged through these formulas, so kernels may skip such work.
+// The P.V chain's assignment of output dims to lanes does not change any
+// value, so kernels choose it freely; the score chain's assignment of dims to
+// MFMA k slots is fixed as above.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -38,6 +47,8 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 constexpr int kTile = 32;
 constexpr int kChunk = 256;
 constexpr int kTilesPerChunk = kChunk / kTile;
+constexpr int kSpanChunks = 16;
+constexpr int kSpanTiles = kSpanChunks * kTilesPerChunk;
 constexpr int kRows = 16;
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kNegInf = -__builtin_huge_valf();
@@ -78,11 +89,65 @@ struct Params {
     // chunk partials for the ordered combine
     float *ws_o;  // [nkv][nrows_pad][nch][DK]
     float *ws_ml; // [nkv][nrows_pad][nch][2]
-    int c_lo;     // first chunk of the launch
+    int c_lo;     // first chunk of the launch (absolute chunk index)
     int nch;      // chunks of the launch
-    int dk;       // padded head dim of the launch
+    // span partials of the two-level combine
+    float *ws2_o;  // [nkv][nrows_pad][nspan][DK]
+    float *ws2_ml; // [nkv][nrows_pad][nspan][2]
+    int s_lo;      // first span of the launch (absolute span index)
+    int nspan;     // spans of the launch
+    int dk;        // padded head dim of the launch
+    // arrival counters of the in-kernel combine, [nkv][units][nspan] then
+    // [nkv][units]; zero between launches (the last arrival resets each)
+    int *cnt;
     int *err;
 };
+
+// Global-memory accessors. Pointers taken from Params are generic, and a
+// generic (flat) load counts against both the vector-memory and the LDS
+// counters, so every LDS wait would also drain all outstanding HBM loads;
+// casting to the global address space keeps the two counters apart.
+typedef const __attribute__((address_space(1))) f4 *gf4_cptr;
+typedef __attribute__((address_space(1))) f4 *gf4_ptr;
+typedef const __attribute__((address_space(1))) float *gf_cptr;
+typedef __attribute__((address_space(1))) float *gf_ptr;
+typedef const __attribute__((address_space(1))) uint8_t *gu8_cptr;
+
+__device__ __forceinline__ f4 ldg4(const float *p)
+{
+    return *(gf4_cptr)p;
+}
+
+__device__ __forceinline__ void stg4(float *p, f4 v)
+{
+    *(gf4_ptr)p = v;
+}
+
+__device__ __forceinline__ float ldg(const float *p)
+{
+    return *(gf_cptr)p;
+}
+
+__device__ __forceinline__ void stg(float *p, float v)
+{
+    *(gf_ptr)p = v;
+}
+
+// Device-coherent accessors for data handed between workgroups of one
+// launch. The XCDs' L2 caches are not coherent with each other, so a plain
+// store may sit in one XCD's L2 while another XCD reads stale memory, and an
+// agent-scope fence would write back and invalidate the whole L2. Relaxed
+// atomics at agent scope carry the device-scope cache bits instead: the store
+// goes through to the coherence point and the load reads from it.
+__device__ __forceinline__ void st_dev(float *p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float ld_dev(const float *p)
+{
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 __device__ __forceinline__ f4 mfma(float a, float b, f4 c)
 {
@@ -118,7 +183,7 @@ __device__ __forceinline__ bool allowed(const Params &p, int row, int64_t t)
         return false;
     const int query = row / p.group;
     if (p.mask)
-        return p.mask[(int64_t)query * p.mask_stride + t] != 0;
+        return ((gu8_cptr)p.mask)[(int64_t)query * p.mask_stride + t] != 0;
     if (!p.causal)
         return true;
     const int64_t kp = p.first_key + t;

@@ -1,47 +1,51 @@
 // LDS-tiled prefill / canvas attention for gfx950.
 //
-// One workgroup of NWV waves owns 16*NWV flat (query, head) rows of one KV
-// head, 16 rows per wave; Q^T stays in registers as MFMA B operands (NWV = 4
-// at head dim 256, one wave per SIMD with the whole register file; 8 below). The K and V
-// tiles of 32 keys are staged once per workgroup in double-buffered LDS and
-// read by all 8 waves (K rows padded by 16 bytes so the 16 rows of an A
-// operand fall in distinct banks). Per tile each wave runs the score chain,
-// the online softmax and the P.V chain of the canonical arithmetic
-// (attention_device.hpp); at each 256-key chunk boundary it merges the chunk
-// into its running (M, L, Acc). Tiles wholly masked for the workgroup are
-// never loaded; tiles wholly masked for a wave are skipped by that wave.
+// One workgroup of 8 waves (two per SIMD) owns 128 flat (query, head) rows of
+// one KV head, one 16-row MFMA unit per wave. Q^T (MFMA B operands) and the
+// chunk state O stay in registers. K and V tiles of 32 keys are copied
+// HBM -> LDS by global_load_lds_dwordx4 (no register staging), double
+// buffered. K rows are stored with their 16-byte chunks XOR-swizzled by
+// (key & 7), so the 16 key rows of an MFMA A operand hit distinct banks
+// without padding the rows.
+//
+// Per tile each wave runs the score chain, online softmax and P.V chain of
+// the canonical arithmetic (attention_device.hpp). The merges are rare (every
+// 8 and every 128 tiles), so their accumulators live in memory rather than
+// registers: the span accumulator in the row's own output slot, the running
+// total across spans in the workspace; the last merge writes the normalised
+// output. Tiles wholly masked for the workgroup are never loaded; tiles
+// wholly masked for a wave are skipped by that wave.
 //
 // split != 0: the workgroup computes the single chunk c_lo + blockIdx.z and
-// writes its partial for combine_kernel (used when one pass over the keys
-// leaves too few workgroups to fill the chip).
+// writes its chunk partial for the combine kernels.
 #include "attention_device.hpp"
 
 namespace pcl {
 
-template <int DK> struct TiledShape {
-    static constexpr int waves = DK > 128 ? 4 : 8;
-    static constexpr int threads = 64 * waves;
-    static constexpr int rows = kRows * waves;
-};
+constexpr int kTiledWaves = 8;
+constexpr int kTiledRows = kTiledWaves * kRows; // 128
 
 template <int DK> struct TiledLds {
-    static constexpr int KLD = DK + 4;
-    static constexpr int kFloats = kTile * KLD;
-    static constexpr int vFloats = kTile * DK;
-    static constexpr int stage = kFloats + vFloats;
+    static constexpr int tileFloats = kTile * DK;
+    static constexpr int stage = 2 * tileFloats; // K then V
     static constexpr size_t bytes = 2 * stage * sizeof(float);
 };
 
-template <int DK>
-__global__ __launch_bounds__(TiledShape<DK>::threads) void tiled_kernel(Params p, int split)
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+typedef const __attribute__((address_space(1))) void *gbl_ptr_t;
+
+__device__ __forceinline__ void dma16(const float *g, float *l)
 {
-    using L = TiledLds<DK>;
-    constexpr int NT = TiledShape<DK>::threads;
-    constexpr int kTiledRows = TiledShape<DK>::rows;
-    constexpr int KLD = L::KLD;
-    constexpr int NU = DK / 32; // score chain steps
-    constexpr int NQ = DK / 64; // 64-dim output groups
-    constexpr int NL = kTile * (DK / 4) / NT; // float4 per thread per tile
+    __builtin_amdgcn_global_load_lds((gbl_ptr_t)g, (lds_ptr_t)l, 16, 0, 0);
+}
+
+template <int DK>
+__global__ __launch_bounds__(512) void tiled_kernel(Params p, int split)
+{
+    using LD = TiledLds<DK>;
+    constexpr int NU = DK / 32;                         // score chain steps
+    constexpr int NQ = DK / 64;                         // 64-dim output groups
+    constexpr int NI = kTile * DK / 256 / kTiledWaves;  // DMA pieces per wave per array
     extern __shared__ float lds[];
 
     const int tid = threadIdx.x;
@@ -49,11 +53,20 @@ __global__ __launch_bounds__(TiledShape<DK>::threads) void tiled_kernel(Params p
     const int w = tid >> 6;
     const int col = lane & 15;
     const int g = lane >> 4;
-    const int qb = gridDim.x - 1 - blockIdx.x; // longest causal blocks first
-    const int kvl = blockIdx.y;
+    // Blocks cycle over the KV heads first (the dispatcher deals consecutive
+    // blocks to the 8 XCDs, so each XCD's L2 serves one head's K/V), and the
+    // query blocks run last-to-first (longest causal blocks first).
+    const int nqb = gridDim.x / p.nkv;
+    const int kvl = blockIdx.x % p.nkv;
+    const int qb = nqb - 1 - (int)(blockIdx.x / p.nkv);
     const int kh = p.kh_first + kvl;
     const int fa = qb * kTiledRows;
     const int row = fa + w * kRows + col;
+    const bool rin = row < p.nrows;
+    const int query = rin ? row / p.group : 0;
+    const int head = kh * p.group + (rin ? row % p.group : 0);
+    // rows that are written (others are computed and dropped)
+    const bool rout = rin && head >= p.h_lo && head < p.h_hi;
 
     // Key range the workgroup can see.
     int64_t k_lo = 0, k_hi = p.nkeys;
@@ -76,89 +89,140 @@ __global__ __launch_bounds__(TiledShape<DK>::threads) void tiled_kernel(Params p
     // Q^T B operands: q[u][jj] = Q[row][32u + 8g + jj] * q_scale.
     float q[NU][8];
     {
-        const bool rin = row < p.nrows;
-        const int query = rin ? row / p.group : 0;
-        const int h = kh * p.group + (rin ? row % p.group : 0);
-        const float *qp = p.q + (int64_t)query * p.q_stride + (int64_t)h * p.dim;
+        const float *qp = p.q + (int64_t)query * p.q_stride + (int64_t)head * p.dim;
 #pragma unroll
         for (int u = 0; u < NU; ++u)
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 const int d = 32 * u + 8 * g + 4 * hh;
-                f4 v = {0.f, 0.f, 0.f, 0.f};
-                if (rin && d < p.dim)
-                    v = *(const f4 *)(qp + d) * p.q_scale;
+                const f4 x = ldg4(qp + (d < p.dim ? d : 0)) * p.q_scale;
+                const f4 v = (rin && d < p.dim) ? x : f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     q[u][4 * hh + j] = v[j];
             }
     }
 
-    float m = kNegInf, l = 0.f;
-    float M = kNegInf, Lsum = 0.f;
-    f4 O[NQ][4], Acc[NQ][4];
+    // chunk state (m, l, O) in registers; span (M1, L1) and total (M2, L2)
+    // scalars in registers, their vectors in memory
+    float m = kNegInf, l = 0.f, M1 = kNegInf, L1 = 0.f, M2 = kNegInf, L2 = 0.f;
+    f4 O[NQ][4];
 #pragma unroll
     for (int a = 0; a < NQ; ++a)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < 4; ++j)
             O[a][j] = f4{0.f, 0.f, 0.f, 0.f};
-            Acc[a][j] = f4{0.f, 0.f, 0.f, 0.f};
-        }
-    bool processed = false;
+    bool processed = false; // this wave computed a tile of the current chunk
     bool bad = false;
+    float *acc1 = p.out + (int64_t)query * p.o_stride + (int64_t)(head - p.h_base) * p.dim;
+    float *acc2 = p.ws_o ? p.ws_o + ((int64_t)kvl * p.nrows_pad + row) * p.dk : nullptr;
 
-    f4 kr[NL], vr[NL];
-    auto load_tile = [&](int t) {
+    // HBM -> LDS copy of tile t into stage `buf` (K swizzled, V plain).
+    auto load_tile = [&](int t, int buf) {
+        float *ks = lds + buf * LD::stage;
+        float *vs = ks + LD::tileFloats;
+        const int64_t klast = p.nkeys - 1;
 #pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            const int idx = tid + NT * i;
-            const int key = idx / (DK / 4);
-            const int d = (idx % (DK / 4)) * 4;
+        for (int i = 0; i < NI; ++i) {
+            const int j = w * NI + i;          // 1 KiB piece of the tile
+            const int f = 256 * j + 4 * lane;  // float offset of this lane's 16 bytes
+            const int key = f / DK;
+            const int pos = (f % DK) / 4;      // 16-byte chunk slot in the row
             const int64_t kt = (int64_t)t * kTile + key;
-            const bool in = kt < p.nkeys && d < p.dim;
-            const int64_t ks = in ? kt : 0;
-            kr[i] = in ? *(const f4 *)(key_row(p, ks) + (int64_t)kh * p.dim + d)
-                       : f4{0.f, 0.f, 0.f, 0.f};
-            vr[i] = in ? *(const f4 *)(value_row(p, ks) + (int64_t)kh * p.dim + d)
-                       : f4{0.f, 0.f, 0.f, 0.f};
+            const int64_t kc = kt < klast ? kt : klast;
+            const int64_t off = (int64_t)kh * p.dim;
+            dma16(key_row(p, kc) + off + 4 * (pos ^ (key & 7)), ks + 256 * j);
+            dma16(value_row(p, kc) + off + 4 * pos, vs + 256 * j);
         }
     };
-    auto store_tile = [&](int buf) {
-        float *ks = lds + buf * L::stage;
-        float *vs = ks + L::kFloats;
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            const int idx = tid + NT * i;
-            const int key = idx / (DK / 4);
-            const int d = (idx % (DK / 4)) * 4;
-            *(f4 *)(ks + key * KLD + d) = kr[i];
-            *(f4 *)(vs + key * DK + d) = vr[i];
+
+    // Chunk merge into the span, and at a span end the span merge into the
+    // total; `last` also normalises into the output.
+    auto flush = [&](bool chunk, bool span_end, bool last) {
+        const bool first1 = M1 == kNegInf;
+        MergeFactors f1 = {M1, 1.f, 0.f};
+        if (chunk) {
+            f1 = merge_factors(M1, m);
+            L1 = merge_value(L1, l, f1);
+            M1 = f1.m;
         }
-    };
-    auto merge_chunk = [&]() {
-        const MergeFactors f = merge_factors(M, m);
-        Lsum = merge_value(Lsum, l, f);
+        const bool add2 = (span_end || last) && M1 != kNegInf;
+        const bool first2 = M2 == kNegInf;
+        MergeFactors f2 = {M2, 1.f, 0.f};
+        if (add2) {
+            f2 = merge_factors(M2, M1);
+            L2 = merge_value(L2, L1, f2);
+            M2 = f2.m;
+        }
+        bool nonfinite = false;
+        if (rout) {
 #pragma unroll
-        for (int a = 0; a < NQ; ++a)
+            for (int a = 0; a < NQ; ++a)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+                for (int i = 0; i < 4; ++i) {
+                    const int d = 64 * a + 16 * g + 4 * i;
+                    if (d >= p.dim)
+                        continue;
+                    f4 s1 = f4{0.f, 0.f, 0.f, 0.f};
+                    if (!first1)
+                        s1 = ldg4(acc1 + d);
+                    if (chunk) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    Acc[a][j][i] = merge_value(Acc[a][j][i], O[a][j][i], f);
-        M = f.m;
+                        for (int j = 0; j < 4; ++j)
+                            s1[j] = merge_value(s1[j], O[a][j][i], f1);
+                    }
+                    if (!(span_end || last)) {
+                        stg4(acc1 + d, s1);
+                        continue;
+                    }
+                    f4 s2 = f4{0.f, 0.f, 0.f, 0.f};
+                    if (!first2)
+                        s2 = ldg4(acc2 + d);
+                    if (add2) {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            s2[j] = merge_value(s2[j], s1[j], f2);
+                    }
+                    if (last) {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            s2[j] = s2[j] / L2;
+                            nonfinite |= !is_finite(s2[j]);
+                        }
+                        stg4(acc1 + d, s2);
+                    } else {
+                        stg4(acc2 + d, s2);
+                    }
+                }
+        }
+        if (nonfinite)
+            atomicOr(p.err, kErrOutput);
+        if (chunk) {
+            m = kNegInf;
+            l = 0.f;
+#pragma unroll
+            for (int a = 0; a < NQ; ++a)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    O[a][j] = f4{0.f, 0.f, 0.f, 0.f};
+        }
+        if (span_end || last) {
+            M1 = kNegInf;
+            L1 = 0.f;
+        }
     };
 
     if (t_lo < t_hi) {
-        load_tile(t_lo);
-        store_tile(0);
+        load_tile(t_lo, 0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
     __syncthreads();
     for (int t = t_lo; t < t_hi; ++t) {
         const int buf = (t - t_lo) & 1;
         if (t + 1 < t_hi)
-            load_tile(t + 1);
-        const float *ks = lds + buf * L::stage;
-        const float *vs = ks + L::kFloats;
+            load_tile(t + 1, buf ^ 1);
+        const float *ks = lds + buf * LD::stage;
+        const float *vs = ks + LD::tileFloats;
 
         bool ok[2][4];
         bool any = false;
@@ -170,23 +234,24 @@ __global__ __launch_bounds__(TiledShape<DK>::threads) void tiled_kernel(Params p
                 any |= ok[b][r];
             }
         if (__any(any)) {
-            f4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+            f4 acc[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
             for (int u = 0; u < NU; ++u) {
-                const int d = 32 * u + 8 * g;
                 f4 ka[2][2];
 #pragma unroll
                 for (int b = 0; b < 2; ++b)
 #pragma unroll
-                    for (int hh = 0; hh < 2; ++hh)
-                        ka[b][hh] = *(const f4 *)(ks + (16 * b + col) * KLD + d + 4 * hh);
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const int c4 = 8 * u + 2 * g + hh;
+                        ka[b][hh] = *(const f4 *)(ks + (16 * b + col) * DK + 4 * (c4 ^ (col & 7)));
+                    }
 #pragma unroll
                 for (int jj = 0; jj < 8; ++jj)
 #pragma unroll
                     for (int b = 0; b < 2; ++b)
                         acc[b] = mfma(ka[b][jj >> 2][jj & 3], q[u][jj], acc[b]);
             }
-            float s[2][4];
+            float s[2][4], pr[2][4];
 #pragma unroll
             for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -196,7 +261,6 @@ __global__ __launch_bounds__(TiledShape<DK>::threads) void tiled_kernel(Params p
             const float mn = fmaxf(m, tile_max(s, ok));
             const float ms = safe_max(mn);
             const float alpha = fexp(m - ms);
-            float pr[2][4];
             const float rs = tile_probs(s, ok, ms, pr);
             l = __builtin_fmaf(l, alpha, rs);
             m = mn;
@@ -220,57 +284,32 @@ __global__ __launch_bounds__(TiledShape<DK>::threads) void tiled_kernel(Params p
         }
 
         if (t + 1 < t_hi)
-            store_tile(buf ^ 1);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
 
-        if (!split && (((t + 1) % kTilesPerChunk) == 0 || t + 1 == t_hi)) {
-            if (processed) {
-                merge_chunk();
-                m = kNegInf;
-                l = 0.f;
-#pragma unroll
-                for (int a = 0; a < NQ; ++a)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        O[a][j] = f4{0.f, 0.f, 0.f, 0.f};
+        if (!split) {
+            const bool last = t + 1 == t_hi;
+            const bool chunk_end = ((t + 1) % kTilesPerChunk) == 0 || last;
+            const bool span_end = ((t + 1) % kSpanTiles) == 0;
+            if ((chunk_end && processed) || span_end || last)
+                flush(chunk_end && processed, span_end, last);
+            if (chunk_end)
                 processed = false;
-            }
         }
     }
     if (bad)
         atomicOr(p.err, kErrScore);
-    if (row >= p.nrows)
-        return;
-
-    // O[a][j][i] / Acc[a][j][i] hold dim 64a + 16g + 4i + j of `row`.
-    if (split) {
-        const int64_t slot = ((int64_t)kvl * p.nrows_pad + row) * p.nch + blockIdx.z;
-        float *wo = p.ws_o + slot * p.dk;
-#pragma unroll
-        for (int a = 0; a < NQ; ++a)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int d = 64 * a + 16 * g + 4 * i;
-                if (d >= p.dim)
-                    continue;
-                f4 v;
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    v[j] = O[a][j][i];
-                *(f4 *)(wo + d) = v;
-            }
-        if (g == 0) {
-            p.ws_ml[2 * slot] = m;
-            p.ws_ml[2 * slot + 1] = l;
-        }
+    if (!split) {
+        if (t_lo >= t_hi) // no key at all: 0/0, flagged like any non-finite output
+            flush(false, false, true);
         return;
     }
-    const int query = row / p.group;
-    const int h = kh * p.group + row % p.group;
-    if (h < p.h_lo || h >= p.h_hi)
+
+    // O[a][j][i] holds dim 64a + 16g + 4i + j of `row`.
+    if (!rin)
         return;
-    float *o = p.out + (int64_t)query * p.o_stride + (int64_t)(h - p.h_base) * p.dim;
-    bool nonfinite = false;
+    const int64_t slot = ((int64_t)kvl * p.nrows_pad + row) * p.nch + blockIdx.z;
+    float *wo = p.ws_o + slot * p.dk;
 #pragma unroll
     for (int a = 0; a < NQ; ++a)
 #pragma unroll
@@ -280,14 +319,14 @@ __global__ __launch_bounds__(TiledShape<DK>::threads) void tiled_kernel(Params p
                 continue;
             f4 v;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                v[j] = Acc[a][j][i] / Lsum;
-                nonfinite |= !is_finite(v[j]);
-            }
-            *(f4 *)(o + d) = v;
+            for (int j = 0; j < 4; ++j)
+                v[j] = O[a][j][i];
+            stg4(wo + d, v);
         }
-    if (nonfinite)
-        atomicOr(p.err, kErrOutput);
+    if (g == 0) {
+        stg(p.ws_ml + 2 * slot, m);
+        stg(p.ws_ml + 2 * slot + 1, l);
+    }
 }
 
 template <int DK> static hipError_t launch_tiled_dk(const Params &p, int split, hipStream_t stream)
@@ -301,15 +340,15 @@ template <int DK> static hipError_t launch_tiled_dk(const Params &p, int split, 
             return e;
         configured = true;
     }
-    constexpr int rows = TiledShape<DK>::rows;
-    const dim3 grid((p.nrows + rows - 1) / rows, p.nkv, split ? p.nch : 1);
-    tiled_kernel<DK><<<grid, TiledShape<DK>::threads, TiledLds<DK>::bytes, stream>>>(p, split);
+    const int nqb = (p.nrows + kTiledRows - 1) / kTiledRows;
+    const dim3 grid(nqb * p.nkv, 1, split ? p.nch : 1);
+    tiled_kernel<DK><<<grid, 64 * kTiledWaves, TiledLds<DK>::bytes, stream>>>(p, split);
     return hipGetLastError();
 }
 
-int tiled_rows(int dk)
+int tiled_rows(int)
 {
-    return dk > 128 ? TiledShape<256>::rows : TiledShape<128>::rows;
+    return kTiledRows;
 }
 
 hipError_t launch_tiled(const Params &p, int split, hipStream_t stream)
