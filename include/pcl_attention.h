@@ -102,6 +102,8 @@ enum pcl_kernel {
     PCL_KERNEL_SPLIT_KV = 1,    /* split-KV flash decode + ordered combine */
     PCL_KERNEL_TILED = 2,       /* LDS-tiled prefill, one pass over the keys */
     PCL_KERNEL_TILED_SPLIT = 3, /* LDS-tiled prefill, one key chunk per block */
+    PCL_KERNEL_PIPE_KV = 4,     /* pipelined split-KV decode (score/value wave
+                                   pairs, head dim <= 256) + ordered combine */
 };
 
 /* Attention of nq query positions over keys [0, n0+n1): keys 0..n0-1 come

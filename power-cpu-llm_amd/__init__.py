@@ -27,9 +27,9 @@ LIB_PATH = os.path.join(HERE, "libpcl_attention.so")
 OK, INVALID_SHAPE, INVALID_PARAMETER, NON_FINITE_VALUE = 0, 1, 2, 3
 ERROR_NAMES = {INVALID_SHAPE: "InvalidShape", INVALID_PARAMETER: "InvalidParameter",
                NON_FINITE_VALUE: "NonFiniteValue"}
-KERNEL_AUTO, KERNEL_SPLIT_KV, KERNEL_TILED, KERNEL_TILED_SPLIT = 0, 1, 2, 3
+KERNEL_AUTO, KERNEL_SPLIT_KV, KERNEL_TILED, KERNEL_TILED_SPLIT, KERNEL_PIPE_KV = 0, 1, 2, 3, 4
 KERNEL_NAMES = {KERNEL_SPLIT_KV: "split_kv", KERNEL_TILED: "tiled",
-                KERNEL_TILED_SPLIT: "tiled_split"}
+                KERNEL_TILED_SPLIT: "tiled_split", KERNEL_PIPE_KV: "pipe_kv"}
 
 # Every symbol include/pcl_attention.h declares.
 EXPORTS = (

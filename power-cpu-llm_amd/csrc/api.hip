@@ -13,6 +13,7 @@
 namespace pcl {
 hipError_t launch_split_kv(const Params &p, hipStream_t stream);
 hipError_t launch_combine(const Params &p, hipStream_t stream);
+hipError_t launch_pipe_kv(const Params &p, hipStream_t stream);
 hipError_t launch_tiled(const Params &p, int split, hipStream_t stream);
 int tiled_rows(int dk);
 } // namespace pcl
@@ -25,8 +26,6 @@ struct pcl_context {
     bool own_stream = false;
     void *ws = nullptr;
     size_t ws_bytes = 0;
-    int *cnt = nullptr; // arrival counters of the split-KV combine (always zero at rest)
-    size_t cnt_ints = 0;
     int *err = nullptr;
     // Staging buffers of the host-pointer entries (grow-only).
     void *stage[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
@@ -37,6 +36,8 @@ namespace {
 
 constexpr int kMaxDim = 512;
 constexpr int kTiledMaxDk = 256;
+constexpr int kPipeMaxDk = 256;
+constexpr int64_t kPipeMinBlocks = 512;
 
 void report(const char *what, hipError_t e)
 {
@@ -83,8 +84,16 @@ int choose_kernel(int requested, int dk, int64_t nrows, int64_t nkv, int64_t nch
         return dk <= kTiledMaxDk ? requested : PCL_KERNEL_SPLIT_KV;
     if (requested == PCL_KERNEL_SPLIT_KV)
         return requested;
-    if (dk > kTiledMaxDk || nrows < 64)
-        return PCL_KERNEL_SPLIT_KV;
+    if (requested == PCL_KERNEL_PIPE_KV)
+        return dk <= kPipeMaxDk ? requested : PCL_KERNEL_SPLIT_KV;
+    if (dk > kTiledMaxDk || nrows < 64) {
+        // decode: the pipelined wave pairs stream long caches fastest; short
+        // launches (few workgroups, so latency-bound) and head dims above 256
+        // take the four-phase kernel with DK/64 waves per chunk
+        const int64_t units = (nrows + pcl::kRows - 1) / pcl::kRows;
+        return dk <= kPipeMaxDk && nch * nkv * units >= kPipeMinBlocks ? PCL_KERNEL_PIPE_KV
+                                                                       : PCL_KERNEL_SPLIT_KV;
+    }
     const int64_t rows = pcl::tiled_rows(dk);
     const int64_t blocks = (nrows + rows - 1) / rows * nkv;
     if (blocks >= 128 || nch <= 1)
@@ -101,6 +110,8 @@ int make_plan(const pcl_attention_desc &d, int64_t h_lo, int64_t h_hi, int64_t h
         d.dim % 16 != 0 || d.dim > kMaxDim || d.nq < 0 || d.n0 < 0 || d.n1 < 0 ||
         d.kh_first < 0 || d.kh_first > d.kh_end || d.kh_end > d.kvheads || d.window < 0)
         return PCL_INVALID_SHAPE;
+    if (d.kernel < PCL_KERNEL_AUTO || d.kernel > PCL_KERNEL_PIPE_KV)
+        return PCL_INVALID_PARAMETER;
     const int64_t group = d.qheads / d.kvheads;
     const int64_t nkeys = d.n0 + d.n1;
     const int64_t nkv = d.kh_end - d.kh_first;
@@ -178,7 +189,8 @@ int make_plan(const pcl_attention_desc &d, int64_t h_lo, int64_t h_hi, int64_t h
     p.s_lo = (int)s_lo;
     p.nspan = (int)(s_hi - s_lo);
     const bool partials = plan->kernel == PCL_KERNEL_TILED_SPLIT ||
-                          (plan->kernel == PCL_KERNEL_SPLIT_KV && nch > 1);
+                          ((plan->kernel == PCL_KERNEL_SPLIT_KV ||
+                            plan->kernel == PCL_KERNEL_PIPE_KV) && nch > 1);
     plan->ws_floats = 0;
     if (partials) {
         plan->ws_floats = (size_t)nkv * p.nrows_pad * nch * (dk + 2);
@@ -210,37 +222,12 @@ int ensure_workspace(pcl_context *ctx, size_t bytes)
     return PCL_OK;
 }
 
-int ensure_counters(pcl_context *ctx, size_t n)
-{
-    if (n <= ctx->cnt_ints)
-        return PCL_OK;
-    if (ctx->cnt) {
-        (void)hipStreamSynchronize(ctx->stream);
-        (void)hipFree(ctx->cnt);
-        ctx->cnt = nullptr;
-        ctx->cnt_ints = 0;
-    }
-    hipError_t e = hipMalloc(&ctx->cnt, n * sizeof(int));
-    if (e == hipSuccess)
-        e = hipMemsetAsync(ctx->cnt, 0, n * sizeof(int), ctx->stream);
-    if (e != hipSuccess) {
-        report("counter allocation", e);
-        return PCL_NON_FINITE_VALUE;
-    }
-    ctx->cnt_ints = n;
-    return PCL_OK;
-}
-
 int run_plan(pcl_context *ctx, Plan &plan)
 {
     if (plan.empty)
         return PCL_OK;
     Params &p = plan.p;
     p.err = ctx->err;
-    // The split-KV kernel can merge its chunks itself (p.cnt, arrival
-    // counters), but on gfx950 the two combine kernels are faster at the
-    // sizes measured, so the counters stay unused (p.cnt = nullptr).
-    (void)ensure_counters;
     if (plan.ws_floats) {
         const int rc = ensure_workspace(ctx, plan.ws_floats * sizeof(float));
         if (rc != PCL_OK)
@@ -258,6 +245,11 @@ int run_plan(pcl_context *ctx, Plan &plan)
     switch (plan.kernel) {
     case PCL_KERNEL_SPLIT_KV:
         e = pcl::launch_split_kv(p, ctx->stream);
+        if (e == hipSuccess && p.ws_o)
+            e = pcl::launch_combine(p, ctx->stream);
+        break;
+    case PCL_KERNEL_PIPE_KV:
+        e = pcl::launch_pipe_kv(p, ctx->stream);
         if (e == hipSuccess && p.ws_o)
             e = pcl::launch_combine(p, ctx->stream);
         break;
@@ -447,8 +439,6 @@ void pcl_context_destroy(pcl_context *ctx)
             (void)hipFree(ctx->stage[i]);
     if (ctx->ws)
         (void)hipFree(ctx->ws);
-    if (ctx->cnt)
-        (void)hipFree(ctx->cnt);
     if (ctx->err)
         (void)hipFree(ctx->err);
     if (ctx->own_stream && ctx->stream)

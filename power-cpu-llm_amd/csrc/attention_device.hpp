@@ -97,9 +97,6 @@ struct Params {
     int s_lo;      // first span of the launch (absolute span index)
     int nspan;     // spans of the launch
     int dk;        // padded head dim of the launch
-    // arrival counters of the in-kernel combine, [nkv][units][nspan] then
-    // [nkv][units]; zero between launches (the last arrival resets each)
-    int *cnt;
     int *err;
 };
 
@@ -131,22 +128,6 @@ __device__ __forceinline__ float ldg(const float *p)
 __device__ __forceinline__ void stg(float *p, float v)
 {
     *(gf_ptr)p = v;
-}
-
-// Device-coherent accessors for data handed between workgroups of one
-// launch. The XCDs' L2 caches are not coherent with each other, so a plain
-// store may sit in one XCD's L2 while another XCD reads stale memory, and an
-// agent-scope fence would write back and invalidate the whole L2. Relaxed
-// atomics at agent scope carry the device-scope cache bits instead: the store
-// goes through to the coherence point and the load reads from it.
-__device__ __forceinline__ void st_dev(float *p, float v)
-{
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ float ld_dev(const float *p)
-{
-    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ f4 mfma(float a, float b, f4 c)
@@ -248,6 +229,27 @@ __device__ __forceinline__ MergeFactors merge_factors(float M, float m)
 __device__ __forceinline__ float merge_value(float acc, float o, const MergeFactors &f)
 {
     return __builtin_fmaf(acc, f.a, o * f.b);
+}
+
+// Merge state of four consecutive dims of one row (the per-element merge
+// above, with the shared M and L kept once).
+struct Merged4 {
+    float M, L;
+    f4 acc;
+};
+
+// Branch-free: an empty part (m = -inf, l = 0, O = +0) leaves the state
+// bit-unchanged through the formulas (a = 1 and b = 0, or a = b = 0 on an
+// empty state), so the factors of consecutive merges, which depend only on
+// the running maxima, can be computed ahead of the fma chain.
+__device__ __forceinline__ void merge_into4(Merged4 &s, float m, float l, f4 o)
+{
+    const MergeFactors f = merge_factors(s.M, m);
+    s.L = merge_value(s.L, l, f);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        s.acc[j] = merge_value(s.acc[j], o[j], f);
+    s.M = f.m;
 }
 
 // True when any allowed score of the lane is not finite.

@@ -1,0 +1,314 @@
+// Pipelined split-KV decode for gfx950: a score wave and a value wave per
+// (256-key chunk, 16-row unit).
+//
+// Workgroup = 2 waves. The score wave streams K (two 16-key blocks in
+// flight), runs the canonical score chain and online softmax of each tile
+// (attention_device.hpp) and hands the tile's probabilities, alpha and row
+// sum to the value wave through a double-buffered LDS slot. The value wave
+// streams V (one tile in flight, as two halves) and runs the P.V chain one
+// tile behind. One barrier per tile keeps the pair in step; both HBM streams
+// stay busy through every compute step, and the two waves' MFMA work is
+// balanced (128 MFMAs each per tile at head dim 256).
+//
+// Output: for a launch of a single chunk, the output itself; otherwise the
+// chunk partial (m, l, O) for the combine kernel (split_kv.hip).
+#include "attention_device.hpp"
+
+namespace pcl {
+
+// LDS hand-over between the score wave and the value wave.
+struct PipeLds {
+    float p[2][8][64];    // probabilities, [slot][4b + r][lane]
+    float alpha[2][kRows];
+    float rs[2][kRows];
+    int any[2];
+    float m[kRows];       // chunk maximum
+};
+
+template <int DK, bool FULL>
+__device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, int c, PipeLds &s)
+{
+    constexpr int NU = DK / 32; // score chain steps
+    const int lane = threadIdx.x & 63;
+    const int col = lane & 15;
+    const int g = lane >> 4;
+    const int kh = p.kh_first + kvl;
+    const int row = unit * kRows + col;
+    const int64_t cbase = (int64_t)c * kChunk;
+    const int64_t klast = p.nkeys - 1;
+    const int64_t hoff = (int64_t)kh * p.dim;
+
+    float q[NU][8];
+    {
+        const bool rin = row < p.nrows;
+        const int query = rin ? row / p.group : 0;
+        const int h = kh * p.group + (rin ? row % p.group : 0);
+        const float *qp = p.q + (int64_t)query * p.q_stride + (int64_t)h * p.dim;
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int d = 32 * u + 8 * g + 4 * hh;
+                const bool din = FULL || d < p.dim;
+                const f4 x = ldg4(qp + (din ? d : 0)) * p.q_scale;
+                const f4 v = (rin && din) ? x : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    q[u][4 * hh + j] = v[j];
+            }
+    }
+    f4 kb[2][NU][2];
+    auto load_k = [&](int t, int b) {
+        const int64_t key = cbase + t * kTile + 16 * b + col;
+        const float *kp = key_row(p, key < klast ? key : klast) + hoff;
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int d = 32 * u + 8 * g + 4 * h;
+                const bool din = FULL || d < p.dim;
+                const f4 x = ldg4(kp + (din ? d : 0));
+                kb[b][u][h] = din ? x : f4{0.f, 0.f, 0.f, 0.f};
+            }
+    };
+    load_k(0, 0);
+    load_k(0, 1);
+    float m = kNegInf;
+    bool bad = false;
+#pragma unroll
+    for (int t = 0; t < kTilesPerChunk; ++t) {
+        bool ok[2][4];
+        bool any = false;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                ok[b][r] = allowed(p, row, cbase + t * kTile + 16 * b + 4 * g + r);
+                any |= ok[b][r];
+            }
+        const bool tile_any = __any(any);
+        f4 acc[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (tile_any) {
+#pragma unroll
+                for (int u = 0; u < NU; ++u)
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj)
+                        acc[b] = mfma(kb[b][u][jj >> 2][jj & 3], q[u][jj], acc[b]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (t + 1 < kTilesPerChunk)
+                load_k(t + 1, b); // this block's registers are free again
+        }
+        float pr[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        float alpha = 1.f, rs = 0.f;
+        if (tile_any) {
+            float sc[2][4];
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    sc[b][r] = acc[b][r];
+            bad |= bad_scores(sc, ok);
+            const float mn = fmaxf(m, tile_max(sc, ok));
+            const float ms = safe_max(mn);
+            alpha = fexp(m - ms);
+            rs = tile_probs(sc, ok, ms, pr);
+            m = mn;
+        } else {
+            // nothing allowed for the unit: alpha = exp(m - safe(m)), rs = 0
+            alpha = fexp(m - safe_max(m));
+        }
+        const int slot = t & 1;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                s.p[slot][4 * b + r][lane] = pr[b][r];
+        if (g == 0) {
+            s.alpha[slot][col] = alpha;
+            s.rs[slot][col] = rs;
+        }
+        if (lane == 0)
+            s.any[slot] = tile_any;
+        __syncthreads(); // tile t handed over
+    }
+    if (g == 0)
+        s.m[col] = m;
+    if (bad)
+        atomicOr(p.err, kErrScore);
+    __syncthreads(); // chunk maximum handed over
+}
+
+// Output modes of the pipelined kernel.
+enum PipeMode { kDirect = 0, kPartial = 1 };
+
+template <int DK, int MODE, bool FULL>
+__device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, int c, PipeLds &s)
+{
+    constexpr int NQ = DK / 64; // 64-dim output groups
+    const int lane = threadIdx.x & 63;
+    const int col = lane & 15;
+    const int g = lane >> 4;
+    const int kh = p.kh_first + kvl;
+    const int row = unit * kRows + col;
+    const int64_t cbase = (int64_t)c * kChunk;
+    const int64_t klast = p.nkeys - 1;
+    const int64_t hoff = (int64_t)kh * p.dim;
+
+    const int dv = 4 * col; // + 64a
+    f4 vv[2][4][NQ];        // [half][slice in half][64-dim group]
+    auto load_v = [&](int t, int half) {
+#pragma unroll
+        for (int sl = 0; sl < 4; ++sl) {
+            const int br = 4 * half + sl;
+            const int64_t key = cbase + t * kTile + 16 * (br >> 2) + 4 * g + (br & 3);
+            const float *vp = value_row(p, key < klast ? key : klast) + hoff;
+#pragma unroll
+            for (int a = 0; a < NQ; ++a) {
+                const int d = 64 * a + dv;
+                const bool din = FULL || d < p.dim;
+                const f4 x = ldg4(vp + (din ? d : 0));
+                vv[half][sl][a] = din ? x : f4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    };
+    load_v(0, 0);
+    load_v(0, 1);
+    float l = 0.f;
+    f4 O[NQ][4];
+#pragma unroll
+    for (int a = 0; a < NQ; ++a)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            O[a][j] = f4{0.f, 0.f, 0.f, 0.f};
+    __syncthreads(); // tile 0 handed over
+#pragma unroll
+    for (int t = 0; t < kTilesPerChunk; ++t) {
+        const int slot = t & 1;
+        const float a_t = s.alpha[slot][col];
+        l = __builtin_fmaf(l, a_t, s.rs[slot][col]);
+        const bool tile_any = s.any[slot];
+        if (tile_any) {
+#pragma unroll
+            for (int a = 0; a < NQ; ++a)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    O[a][j] = O[a][j] * a_t;
+        }
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (tile_any) {
+#pragma unroll
+                for (int sl = 0; sl < 4; ++sl) {
+                    const float pb = s.p[slot][4 * half + sl][lane];
+#pragma unroll
+                    for (int a = 0; a < NQ; ++a)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            O[a][j] = mfma(vv[half][sl][a][j], pb, O[a][j]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (t + 1 < kTilesPerChunk)
+                load_v(t + 1, half);
+        }
+        __syncthreads(); // tile t + 1 handed over (the last one: the chunk maximum)
+    }
+    const float m = s.m[col];
+
+    // O[a][j][i] is dim 64a + 16g + 4i + j of row `row`.
+    if (row >= p.nrows)
+        return;
+    if (MODE == kDirect) { // the launch's only chunk: final output
+        const int query = row / p.group;
+        const int h = kh * p.group + row % p.group;
+        if (h < p.h_lo || h >= p.h_hi)
+            return;
+        float *o = p.out + (int64_t)query * p.o_stride + (int64_t)(h - p.h_base) * p.dim;
+        bool nonfinite = false;
+#pragma unroll
+        for (int a = 0; a < NQ; ++a)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = 64 * a + 16 * g + 4 * i;
+                if (d >= p.dim)
+                    continue;
+                f4 v;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    v[j] = O[a][j][i] / l;
+                    nonfinite |= !is_finite(v[j]);
+                }
+                stg4(o + d, v);
+            }
+        if (nonfinite)
+            atomicOr(p.err, kErrOutput);
+        return;
+    }
+    { // chunk partial for the combine kernel
+        const int64_t slot = ((int64_t)kvl * p.nrows_pad + row) * p.nch + blockIdx.x;
+        float *wo = p.ws_o + slot * p.dk;
+#pragma unroll
+        for (int a = 0; a < NQ; ++a)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = 64 * a + 16 * g + 4 * i;
+                if (d >= p.dim)
+                    continue;
+                f4 v;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    v[j] = O[a][j][i];
+                stg4(wo + d, v);
+            }
+        if (g == 0) {
+            stg(p.ws_ml + 2 * slot, m);
+            stg(p.ws_ml + 2 * slot + 1, l);
+        }
+        return;
+    }
+}
+
+// FULL: the head dim equals the padded head dim (no dim clamping).
+template <int DK, int MODE, bool FULL>
+__global__ __launch_bounds__(128, 2) void pipe_kv_kernel(Params p)
+{
+    __shared__ PipeLds s;
+    const int c = p.c_lo + blockIdx.x;
+    const int unit = blockIdx.y % p.units;
+    const int kvl = blockIdx.y / p.units;
+    if (threadIdx.x < 64)
+        score_wave<DK, FULL>(p, unit, kvl, c, s);
+    else
+        value_wave<DK, MODE, FULL>(p, unit, kvl, c, s);
+}
+
+template <int MODE, bool FULL> hipError_t launch_mode(const Params &p, hipStream_t stream)
+{
+    const dim3 grid(p.nch, p.nkv * p.units);
+    switch (p.dk) {
+    case 64: pipe_kv_kernel<64, MODE, FULL><<<grid, 128, 0, stream>>>(p); break;
+    case 128: pipe_kv_kernel<128, MODE, FULL><<<grid, 128, 0, stream>>>(p); break;
+    case 256: pipe_kv_kernel<256, MODE, FULL><<<grid, 128, 0, stream>>>(p); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <bool FULL> hipError_t launch_full(const Params &p, hipStream_t stream)
+{
+    return p.ws_o == nullptr ? launch_mode<kDirect, FULL>(p, stream)
+                             : launch_mode<kPartial, FULL>(p, stream);
+}
+
+// Direct output for a single chunk, chunk partials otherwise.
+hipError_t launch_pipe_kv(const Params &p, hipStream_t stream)
+{
+    return p.dim == p.dk ? launch_full<true>(p, stream) : launch_full<false>(p, stream);
+}
+
+} // namespace pcl

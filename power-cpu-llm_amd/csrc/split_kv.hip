@@ -13,11 +13,14 @@
 //   phase 3  wave w streams V for dims [64w, 64w+64) through the MFMA P.V
 //            chain over the chunk's tiles in order, VD tiles of V in flight.
 // With more than one chunk the workgroup writes its chunk partial (m, l, O)
-// and counts itself in; the last workgroup of a span merges the span's
-// chunks, and the last span of a unit merges the spans and writes the output,
-// both in ascending order (the ordered merges of attention_device.hpp). The
-// counters reset themselves, so the workspace needs no clearing between
-// launches. A launch of a single chunk writes the output directly.
+// for the combine kernel; a launch of a single chunk writes the output
+// directly.
+//
+// The combine (also used by the pipelined and tiled split kernels) runs both
+// levels of the ordered merge of attention_device.hpp in one launch: span
+// lanes merge the chunks of their spans, one batch of loads per span, and the
+// span partials are folded in ascending order from registers of the same
+// wave.
 #include "attention_device.hpp"
 
 namespace pcl {
@@ -53,22 +56,7 @@ __device__ __forceinline__ void merge_into(Merged &s, float m, float l, float o)
     s.M = f.m;
 }
 
-template <bool DEV> __device__ __forceinline__ float ld_part(const float *p)
-{
-    return DEV ? ld_dev(p) : ldg(p);
-}
-
-template <bool DEV> __device__ __forceinline__ void st_part(float *p, float v)
-{
-    if (DEV)
-        st_dev(p, v);
-    else
-        stg(p, v);
-}
-
-// Chunks [c0, c1) (launch-local indices) of one element, in order. DEV: the
-// partials were written by other workgroups of this launch.
-template <bool DEV>
+// Chunks [c0, c1) (launch-local indices) of one element, in order.
 __device__ __forceinline__ Merged merge_span_chunks(const float *ml, const float *o, int dk,
                                                     int c0, int c1)
 {
@@ -76,9 +64,9 @@ __device__ __forceinline__ Merged merge_span_chunks(const float *ml, const float
 #pragma unroll
     for (int i = 0; i < kSpanChunks; ++i) {
         const int cc = c0 + i < c1 ? c0 + i : c0;
-        mv[i] = ld_part<DEV>(ml + 2 * cc);
-        lv[i] = ld_part<DEV>(ml + 2 * cc + 1);
-        ov[i] = ld_part<DEV>(o + (int64_t)cc * dk);
+        mv[i] = ldg(ml + 2 * cc);
+        lv[i] = ldg(ml + 2 * cc + 1);
+        ov[i] = ldg(o + (int64_t)cc * dk);
     }
     Merged s = {kNegInf, 0.f, 0.f};
 #pragma unroll
@@ -89,7 +77,6 @@ __device__ __forceinline__ Merged merge_span_chunks(const float *ml, const float
 }
 
 // Spans [0, nspan) of one element, in order.
-template <bool DEV>
 __device__ __forceinline__ Merged merge_spans(const float *ml, const float *o, int dk, int nspan)
 {
     Merged s = {kNegInf, 0.f, 0.f};
@@ -99,9 +86,9 @@ __device__ __forceinline__ Merged merge_spans(const float *ml, const float *o, i
 #pragma unroll
         for (int i = 0; i < B; ++i) {
             const int ss = s0 + i < nspan ? s0 + i : s0;
-            mv[i] = ld_part<DEV>(ml + 2 * ss);
-            lv[i] = ld_part<DEV>(ml + 2 * ss + 1);
-            ov[i] = ld_part<DEV>(o + (int64_t)ss * dk);
+            mv[i] = ldg(ml + 2 * ss);
+            lv[i] = ldg(ml + 2 * ss + 1);
+            ov[i] = ldg(o + (int64_t)ss * dk);
         }
 #pragma unroll
         for (int i = 0; i < B; ++i)
@@ -153,7 +140,6 @@ __global__ __launch_bounds__(DK, SplitCfg<DK>::waves_per_eu) void split_kv_kerne
     __shared__ float rs_lds[kTilesPerChunk][kRows];
     __shared__ float p_lds[kTilesPerChunk][8][64];
     __shared__ int any_lds[kTilesPerChunk];
-    __shared__ int last_lds;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -360,7 +346,6 @@ __global__ __launch_bounds__(DK, SplitCfg<DK>::waves_per_eu) void split_kv_kerne
             atomicOr(p.err, kErrOutput);
         return;
     }
-    const bool fused = p.cnt != nullptr; // merged in this kernel, not by the combine kernels
     if (row < p.nrows) {
         const int64_t slot = ((int64_t)kvl * p.nrows_pad + row) * p.nch + blockIdx.x;
         float *wo = p.ws_o + slot * p.dk;
@@ -369,105 +354,17 @@ __global__ __launch_bounds__(DK, SplitCfg<DK>::waves_per_eu) void split_kv_kerne
             const int d = 64 * w + 16 * g + 4 * i;
             if (d >= p.dim)
                 continue;
+            f4 v;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                if (fused)
-                    st_dev(wo + d + j, O[j][i]);
-                else
-                    stg(wo + d + j, O[j][i]);
-            }
+            for (int j = 0; j < 4; ++j)
+                v[j] = O[j][i];
+            stg4(wo + d, v);
         }
         if (w == 0 && g == 0) {
-            if (fused) {
-                st_dev(p.ws_ml + 2 * slot, m);
-                st_dev(p.ws_ml + 2 * slot + 1, l);
-            } else {
-                stg(p.ws_ml + 2 * slot, m);
-                stg(p.ws_ml + 2 * slot + 1, l);
-            }
+            stg(p.ws_ml + 2 * slot, m);
+            stg(p.ws_ml + 2 * slot + 1, l);
         }
     }
-    if (!fused)
-        return; // the combine kernels merge the partials
-
-    // ---- the last workgroup of a span merges it -------------------------
-    const int sl = (c / kSpanChunks) - p.s_lo;
-    int c0, c1;
-    span_chunks(p, sl, &c0, &c1);
-    // this workgroup's device-scope stores are complete before it counts in
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __syncthreads();
-    if (tid == 0) {
-        int *cs = p.cnt + ((int64_t)kvl * p.units + unit) * p.nspan + sl;
-        const int old = atomicAdd(cs, 1);
-        last_lds = old == c1 - c0 - 1;
-        if (last_lds)
-            atomicExch(cs, 0);
-    }
-    __syncthreads();
-    if (!last_lds)
-        return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    const int nreal = min(kRows, p.nrows - row0);
-    const bool single = p.nspan == 1;
-    bool nonfinite = false;
-    for (int e = tid; e < nreal * p.dim; e += DK) {
-        const int r = row0 + e / p.dim;
-        const int d = e % p.dim;
-        const int64_t slot0 = ((int64_t)kvl * p.nrows_pad + r) * p.nch;
-        const Merged sm = merge_span_chunks<true>(p.ws_ml + 2 * slot0,
-                                                  p.ws_o + slot0 * p.dk + d, p.dk, c0, c1);
-        if (single) {
-            float *o = out_ptr(p, kh, r);
-            if (o) {
-                const float v = finish(sm, true);
-                stg(o + d, v);
-                nonfinite |= !is_finite(v);
-            }
-        } else {
-            const int64_t s2 = ((int64_t)kvl * p.nrows_pad + r) * p.nspan + sl;
-            st_dev(p.ws2_o + s2 * p.dk + d, sm.acc);
-            if (d == 0) {
-                st_dev(p.ws2_ml + 2 * s2, sm.M);
-                st_dev(p.ws2_ml + 2 * s2 + 1, sm.L);
-            }
-        }
-    }
-    if (single) {
-        if (nonfinite)
-            atomicOr(p.err, kErrOutput);
-        return;
-    }
-
-    // ---- the last span of the unit merges the spans -----------------------
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __syncthreads();
-    if (tid == 0) {
-        int *ct = p.cnt + (int64_t)p.nkv * p.units * p.nspan + (int64_t)kvl * p.units + unit;
-        const int old = atomicAdd(ct, 1);
-        last_lds = old == p.nspan - 1;
-        if (last_lds)
-            atomicExch(ct, 0);
-    }
-    __syncthreads();
-    if (!last_lds)
-        return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    for (int e = tid; e < nreal * p.dim; e += DK) {
-        const int r = row0 + e / p.dim;
-        const int d = e % p.dim;
-        float *o = out_ptr(p, kh, r);
-        if (!o)
-            continue;
-        const int64_t s0 = ((int64_t)kvl * p.nrows_pad + r) * p.nspan;
-        const Merged st =
-            merge_spans<true>(p.ws2_ml + 2 * s0, p.ws2_o + s0 * p.dk + d, p.dk, p.nspan);
-        const float v = finish(st, false);
-        stg(o + d, v);
-        nonfinite |= !is_finite(v);
-    }
-    if (nonfinite)
-        atomicOr(p.err, kErrOutput);
 }
 
 // Level 1 of the combine: the chunks of one span, for one (row, dim) per
@@ -488,7 +385,7 @@ __global__ __launch_bounds__(256) void combine_span_kernel(Params p)
     span_chunks(p, sl, &c0, &c1);
     const int64_t slot0 = ((int64_t)kvl * p.nrows_pad + row) * p.nch;
     const Merged sm =
-        merge_span_chunks<false>(p.ws_ml + 2 * slot0, p.ws_o + slot0 * p.dk + d, p.dk, c0, c1);
+        merge_span_chunks(p.ws_ml + 2 * slot0, p.ws_o + slot0 * p.dk + d, p.dk, c0, c1);
     if (p.nspan == 1) {
         const float v = finish(sm, true);
         stg(o + d, v);
@@ -518,7 +415,7 @@ __global__ __launch_bounds__(256) void combine_final_kernel(Params p)
         return;
     const int64_t slot0 = ((int64_t)kvl * p.nrows_pad + row) * p.nspan;
     const Merged st =
-        merge_spans<false>(p.ws2_ml + 2 * slot0, p.ws2_o + slot0 * p.dk + d, p.dk, p.nspan);
+        merge_spans(p.ws2_ml + 2 * slot0, p.ws2_o + slot0 * p.dk + d, p.dk, p.nspan);
     const float v = finish(st, false);
     stg(o + d, v);
     if (!is_finite(v))
@@ -538,8 +435,115 @@ hipError_t launch_split_kv(const Params &p, hipStream_t stream)
     return hipGetLastError();
 }
 
+// Both levels of the combine in one launch, one wave per workgroup (small
+// workgroups spread the partial loads over many CUs). The wave holds
+// G = 64 / SP element groups (four consecutive dims of one row) x SP span
+// lanes: span lane s merges the chunks of span s for its element group (one
+// batch of loads), then every lane folds the group's span partials, gathered
+// by cross-lane reads, in ascending order. The values are those of the two
+// kernels above, which serve launches of more than 64 spans.
+constexpr int kCombineMaxSpans = 64;
+
+typedef float f2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f2 ldg2(const float *p)
+{
+    return *(const __attribute__((address_space(1))) f2 *)p;
+}
+
+// Chunks [c0, c1) of the element group (slot0: the row's first chunk slot).
+__device__ __forceinline__ Merged4 merge_chunks4(const Params &p, int64_t slot0, int d, int c0,
+                                                 int c1)
+{
+    f2 ml[kSpanChunks];
+    f4 ov[kSpanChunks];
+#pragma unroll
+    for (int i = 0; i < kSpanChunks; ++i) {
+        const int64_t cc = slot0 + (c0 + i < c1 ? c0 + i : c0);
+        ml[i] = ldg2(p.ws_ml + 2 * cc);
+        ov[i] = ldg4(p.ws_o + cc * p.dk + d);
+    }
+    Merged4 s = {kNegInf, 0.f, f4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int i = 0; i < kSpanChunks; ++i) {
+        // chunks past the span merge as empty parts (no-ops)
+        const bool in = c0 + i < c1;
+        merge_into4(s, in ? ml[i].x : kNegInf, in ? ml[i].y : 0.f,
+                    in ? ov[i] : f4{0.f, 0.f, 0.f, 0.f});
+    }
+    return s;
+}
+
+__global__ __launch_bounds__(64) void combine_kernel(Params p, int span_lanes)
+{
+    const int lane = threadIdx.x;
+    const int G = 64 / span_lanes;
+    const int gi = lane / span_lanes;
+    const int sl = lane % span_lanes;
+    const int q4 = p.dim / 4;
+    const int e = blockIdx.x * G + gi; // element group within the KV head
+    const int kvl = blockIdx.y;
+    const bool valid = e < p.nrows * q4;
+    const int row = valid ? e / q4 : 0;
+    const int d = valid ? 4 * (e % q4) : 0;
+    float *o = valid ? out_ptr(p, p.kh_first + kvl, row) : nullptr;
+    const int64_t slot0 = ((int64_t)kvl * p.nrows_pad + row) * p.nch;
+    bool nonfinite = false;
+    f4 v;
+    if (p.nspan == 1) {
+        // one span: merged into the empty total (exact), then normalised
+        if (!o)
+            return;
+        const Merged4 s = merge_chunks4(p, slot0, d, 0, p.nch);
+        const MergeFactors f = merge_factors(kNegInf, s.M);
+        const float L = merge_value(0.f, s.L, f);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            v[j] = merge_value(0.f, s.acc[j], f) / L;
+    } else {
+        Merged4 s = {kNegInf, 0.f, f4{0.f, 0.f, 0.f, 0.f}};
+        if (o && sl < p.nspan) {
+            int c0, c1;
+            span_chunks(p, sl, &c0, &c1);
+            s = merge_chunks4(p, slot0, d, c0, c1);
+        }
+        Merged4 st = {kNegInf, 0.f, f4{0.f, 0.f, 0.f, 0.f}};
+        const int base = gi * span_lanes;
+#pragma unroll 8
+        for (int t = 0; t < p.nspan; ++t) {
+            f4 acc;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[j] = __shfl(s.acc[j], base + t);
+            merge_into4(st, __shfl(s.M, base + t), __shfl(s.L, base + t), acc);
+        }
+        if (!o || sl != 0)
+            return;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            v[j] = st.acc[j] / st.L;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        nonfinite |= !is_finite(v[j]);
+    stg4(o + d, v);
+    if (nonfinite)
+        atomicOr(p.err, kErrOutput);
+}
+
 hipError_t launch_combine(const Params &p, hipStream_t stream)
 {
+    if (p.nspan <= kCombineMaxSpans && (int64_t)p.nrows * (p.dim / 4) < ((int64_t)1 << 31)) {
+        int lanes = 1;
+        while (lanes < p.nspan)
+            lanes *= 2;
+        const int G = 64 / lanes;
+        const int64_t groups = (int64_t)p.nrows * (p.dim / 4);
+        const unsigned bx = (unsigned)((groups + G - 1) / G);
+        combine_kernel<<<dim3(bx, p.nkv), 64, 0, stream>>>(p, lanes);
+        return hipGetLastError();
+    }
+    // very long launches: span partials through the workspace, two kernels
     const int64_t n = (int64_t)p.nrows * p.dim;
     const unsigned bx = (unsigned)((n + 255) / 256);
     combine_span_kernel<<<dim3(bx, p.nspan, p.nkv), 256, 0, stream>>>(p);

@@ -84,10 +84,18 @@ def test_descriptor_validation_on_the_host(pcl):
                          kvheads=8, dim=256, kh_first=0, kh_end=8, causal=1, first_query=32767,
                          out=16, o_stride=16 * 256)
     lib = pcl.load()
-    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_SPLIT_KV
+    # a long cache streams through the pipelined kernel
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
     assert lib.pcl_attention_workspace_bytes(ctypes.byref(d)) > 0
-    d.window = 1024
+    d.window = 1024  # five chunks per head: the four-phase kernel
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_SPLIT_KV
+    d.kernel = pcl.KERNEL_PIPE_KV  # forced choices are kept where the kernel exists
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
+    d.dim, d.q_stride, d.o_stride = 512, 16 * 512, 16 * 512
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_SPLIT_KV
+    d.kernel = 5  # no such kernel
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == -1
+    d.kernel, d.dim, d.q_stride, d.o_stride = 0, 256, 16 * 256, 16 * 256
     d.dim = 24
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == -1
     d.dim, d.nq, d.first_query, d.window, d.n0 = 256, 4096, 0, 0, 4096

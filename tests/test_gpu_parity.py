@@ -268,12 +268,12 @@ def test_every_kernel_gives_identical_bits(torch, ctx, oracle, case):
     k = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
     v = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
     outs = {}
-    for kernel in (1, 2, 3):
+    for kernel in (1, 2, 3, 4):
         outs[kernel], err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel, causal,
                                      window, 0, fq)
         assert err == 0
-    assert np.array_equal(bits(outs[1]), bits(outs[2]))
-    assert np.array_equal(bits(outs[1]), bits(outs[3]))
+    for kernel in (2, 3, 4):
+        assert np.array_equal(bits(outs[1]), bits(outs[kernel])), kernel
     for i in sorted({0, nq // 2, nq - 1}):
         m = oracle.encoder_mask(0, nkeys, fq + i, window or None) if causal else None
         ok, want = oracle.heads(q[i], k, v, qheads, kvh, dim, nkeys, m)
@@ -293,7 +293,7 @@ def test_explicit_masks_segments_scale_and_kv_ranges_keep_bits(torch, ctx):
     scale = np.float32(1.0 / 16.0)
     base, err = run_desc(torch, ctx, prescale(q, dim), k, v, qheads, kvh, dim, 1, 1, 300, 0, fq)
     assert err == 0
-    for kernel in (1, 2, 3):
+    for kernel in (1, 2, 3, 4):
         # explicit byte masks equal the descriptor's causal window
         got, err = run_desc(torch, ctx, prescale(q, dim), k, v, qheads, kvh, dim, kernel,
                             mask=mask)
@@ -342,7 +342,7 @@ def test_device_error_flags(torch, ctx):
     bad_k[10, 1, 5] = np.nan
     bad_v = v.copy()
     bad_v[20, 0, 3] = np.inf
-    for kernel in (1, 2, 3):
+    for kernel in (1, 2, 3, 4):
         _, err = run_desc(torch, ctx, q, bad_k, v, qheads, kvh, dim, kernel)
         assert err & 1
         _, err = run_desc(torch, ctx, q, k, bad_v, qheads, kvh, dim, kernel)
@@ -365,14 +365,22 @@ def decode_config(torch, ctx, oracle, qheads, kvh, dim, nkeys, window, seed, uni
     v = gpu_normals(torch, seed + 2, (nkeys, kvh, dim))
     if unit_k:
         k = k / k.norm(dim=-1, keepdim=True)
-    out = torch.empty((1, qheads, dim), device="cuda:0")
-    d = ctx.desc(q=q.data_ptr(), q_stride=qheads * dim, nq=1, k0=k.data_ptr(), v0=v.data_ptr(),
-                 n0=nkeys, qheads=qheads, kvheads=kvh, dim=dim, kh_first=0, kh_end=kvh,
-                 causal=1, window=window, first_key=0, first_query=nkeys - 1,
-                 out=out.data_ptr(), o_stride=qheads * dim, kernel=0)
-    ctx.launch(d)
-    assert ctx.sync() == 0
-    got = out.cpu().numpy().reshape(-1)
+    outs = {}
+    # the automatic choice, then both split-KV kernels (the pipelined one up to
+    # head dim 256): all bitwise equal
+    for kernel in (0, 1, 4) if dim <= 256 else (0, 1):
+        out = torch.full((1, qheads, dim), float("nan"), device="cuda:0")
+        d = ctx.desc(q=q.data_ptr(), q_stride=qheads * dim, nq=1, k0=k.data_ptr(),
+                     v0=v.data_ptr(), n0=nkeys, qheads=qheads, kvheads=kvh, dim=dim, kh_first=0,
+                     kh_end=kvh, causal=1, window=window, first_key=0, first_query=nkeys - 1,
+                     out=out.data_ptr(), o_stride=qheads * dim, kernel=kernel)
+        ctx.reserve(ctx.workspace_bytes(d))
+        ctx.launch(d)
+        assert ctx.sync() == 0
+        outs[kernel] = out.cpu().numpy().reshape(-1)
+    for kernel in outs:
+        assert np.array_equal(bits(outs[kernel]), bits(outs[0])), kernel
+    got = outs[0]
     qn, kn, vn = (x.cpu().numpy().reshape(-1) for x in (q, k, v))
     ok, want = oracle.threaded(qn, 1, kn, vn, qheads, kvh, dim, nkeys, True, 0, nkeys - 1,
                                window, threads=THREADS)
