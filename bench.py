@@ -177,6 +177,9 @@ def main():
     ap.add_argument("--workload", default=None, help="time only this workload")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run a plain 256 MiB device copy (the reference point for "
+                         "HBM byte counters under rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the attention path runs on a single MI355X here "
@@ -187,6 +190,13 @@ def main():
     pcl = load_package()
     pcl.load()
     ctx = pcl.Context(0, torch.cuda.current_stream().cuda_stream)
+    if args.copy_calibration:
+        src = torch.ones(64 << 20, device="cuda:0", dtype=torch.float32)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     names = [args.workload] if args.workload else list(WORKLOADS)
     results = {}
