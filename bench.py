@@ -52,6 +52,20 @@ WORKLOADS = {
 HEADLINE = "decode_32k"
 
 
+def traffic_bytes(name):
+    """HBM bytes per launch of the workload's streaming kernel(s), from the
+    committed rocprofv3 counter summary (profiles/hbm_traffic_counters.md: a
+    line `traffic_bytes <workload> <bytes>`), or None when not measured."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_counters.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        f = line.split()
+        if len(f) == 3 and f[0] == "traffic_bytes" and f[1] == name:
+            return int(f[2])
+    return None
+
+
 def allowed_pairs(nq, nkeys, causal, window, first_query):
     """Allowed (query, key) pairs of one head (first_key = 0)."""
     if not causal:
@@ -94,11 +108,11 @@ def make_inputs(torch, name, seed):
     return q.contiguous(), k.contiguous(), v.contiguous()
 
 
-def desc_for(ctx, name, q, k, v, out, k_canvas=None, v_canvas=None):
+def desc_for(ctx, name, q, k, v, out, k_canvas=None, v_canvas=None, kernel=0):
     qh, kvh, dim, nq, nkeys, causal, window, fq, kind, _ = WORKLOADS[name]
     kw = dict(q=q.data_ptr(), q_stride=qh * dim, nq=nq, qheads=qh, kvheads=kvh, dim=dim,
               kh_first=0, kh_end=kvh, causal=int(causal), window=window, first_key=0,
-              first_query=fq, out=out.data_ptr(), o_stride=qh * dim, kernel=0)
+              first_query=fq, out=out.data_ptr(), o_stride=qh * dim, kernel=kernel)
     if k_canvas is not None:
         n0 = nkeys - nq
         kw.update(k0=k.data_ptr(), v0=v.data_ptr(), n0=n0, k1=k_canvas.data_ptr(),
@@ -108,21 +122,36 @@ def desc_for(ctx, name, q, k, v, out, k_canvas=None, v_canvas=None):
     return ctx.desc(**kw)
 
 
-def time_workload(torch, pcl, ctx, name, steps, warmup, seed=0):
-    """Per-launch time (ms) from HIP events on the launch stream."""
+# Each timed launch reads a different input set, and one cycle through the sets
+# touches at least this many bytes: more than twice the MI355X's 256 MB
+# last-level cache, so no launch finds its K/V there (a model's layers each
+# have their own cache; re-reading one small set would measure the cache).
+CYCLE_BYTES = 2 << 30
+MAX_SETS = 64
+
+
+def time_workload(torch, pcl, ctx, name, steps, warmup, seed=0, kernel=0):
+    """Per-launch time (ms) from HIP events on the launch stream, and the
+    per-kernel-role times from the library's own event spans."""
     qh, kvh, dim, nq, nkeys, causal, window, fq, kind, _ = WORKLOADS[name]
-    q, k, v = make_inputs(torch, name, seed)
-    out = torch.empty((nq, qh, dim), device="cuda:0", dtype=torch.float32)
-    kc = vc = None
-    if kind == "canvas":
-        # canvas K/V live apart from the fixed prompt prefix (two segments)
-        kc, vc = k[nkeys - nq:].clone(), v[nkeys - nq:].clone()
-        k, v = k[:nkeys - nq].contiguous(), v[:nkeys - nq].contiguous()
-    d = desc_for(ctx, name, q, k, v, out, kc, vc)
-    ctx.reserve(ctx.workspace_bytes(d))
-    kernel = pcl.KERNEL_NAMES.get(ctx.resolve_kernel(d), "?")
-    for _ in range(warmup):
-        ctx.launch(d)
+    set_bytes = 4 * (2 * nkeys * kvh * dim + 2 * nq * qh * dim)
+    nsets = max(2, min(MAX_SETS, -(-CYCLE_BYTES // set_bytes)))
+    sets = []
+    for i in range(nsets):
+        q, k, v = make_inputs(torch, name, seed + 1000 * i)
+        out = torch.empty((nq, qh, dim), device="cuda:0", dtype=torch.float32)
+        kc = vc = None
+        if kind == "canvas":
+            # canvas K/V live apart from the fixed prompt prefix (two segments)
+            kc, vc = k[nkeys - nq:].clone(), v[nkeys - nq:].clone()
+            k, v = k[:nkeys - nq].contiguous(), v[:nkeys - nq].contiguous()
+        d = desc_for(ctx, name, q, k, v, out, kc, vc, kernel)
+        sets.append(({"q": q, "k": k, "v": v, "out": out, "kc": kc, "vc": vc}, d))
+    d0 = sets[0][1]
+    ctx.reserve(ctx.workspace_bytes(d0))
+    kernel = pcl.KERNEL_NAMES.get(ctx.resolve_kernel(d0), "?")
+    for i in range(max(warmup, nsets)):
+        ctx.launch(sets[i % nsets][1])
     torch.cuda.synchronize()
     if ctx.sync() != 0:
         raise RuntimeError("device error flag set for %s" % name)
@@ -130,8 +159,8 @@ def time_workload(torch, pcl, ctx, name, steps, warmup, seed=0):
     stop = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record()
-    for _ in range(steps):
-        ctx.launch(d)
+    for i in range(steps):
+        ctx.launch(sets[i % nsets][1])
     stop.record()
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
@@ -139,8 +168,16 @@ def time_workload(torch, pcl, ctx, name, steps, warmup, seed=0):
     err = ctx.sync()
     if err:
         raise RuntimeError("device error flag %d for %s" % (err, name))
-    host = {"q": q, "k": k, "v": v, "out": out, "kc": kc, "vc": vc}
-    return ev, wall, kernel, host
+    # the same launches again with the library's per-kernel event spans
+    ctx.set_timing(True)
+    for i in range(steps):
+        ctx.launch(sets[i % nsets][1])
+    (ms_stream, ms_comb), (n_stream, n_comb) = ctx.timing()
+    ctx.set_timing(False)
+    roles = {"stream_ms": ms_stream / max(n_stream, 1),
+             "combine_ms": ms_comb / n_comb if n_comb else 0.0}
+    host = sets[(steps - 1) % nsets][0]
+    return ev, wall, kernel, host, roles, nsets
 
 
 def cpu_baseline(name, host, threads, budget_s=20.0):
@@ -176,6 +213,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default=None, help="time only this workload")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernel", type=int, default=0,
+                    help="pcl_kernel choice for every workload (0 = the library's choice)")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 256 MiB device copy (the reference point for "
@@ -203,10 +242,12 @@ def main():
     hosts = {}
     for name in names:
         steps = args.steps if name == HEADLINE else max(5, args.steps // 5)
-        ev, wall, kernel, host = time_workload(torch, pcl, ctx, name, steps, args.warmup)
+        ev, wall, kernel, host, roles, nsets = time_workload(torch, pcl, ctx, name, steps,
+                                                             args.warmup, kernel=args.kernel)
         flops, bytes_, pairs = work(name)
         kind = WORKLOADS[name][8]
-        r = {"ms": ev, "wall_ms": wall, "kernel": kernel, "steps": steps,
+        r = {"ms": ev, "wall_ms": wall, "kernel": kernel, "steps": steps, "input_sets": nsets,
+             "stream_kernel_ms": roles["stream_ms"], "combine_ms": roles["combine_ms"],
              "algorithmic_bytes": bytes_, "algorithmic_flops": flops}
         r["GB/s"] = bytes_ / (ev * 1e-3) / 1e9
         r["TFLOP/s"] = flops / (ev * 1e-3) / 1e12
@@ -220,8 +261,9 @@ def main():
         else:
             del host
         torch.cuda.empty_cache()
-        print("# %s: %.4f ms (%s) %.1f GB/s %.2f TFLOP/s" % (name, ev, kernel, r["GB/s"],
-                                                             r["TFLOP/s"]), file=sys.stderr)
+        print("# %s: %.4f ms (%s; stream %.4f + combine %.4f ms) %.1f GB/s %.2f TFLOP/s"
+              % (name, ev, kernel, roles["stream_ms"], roles["combine_ms"], r["GB/s"],
+                 r["TFLOP/s"]), file=sys.stderr)
 
     head = args.workload or HEADLINE
     hr = results[head]
@@ -238,14 +280,21 @@ def main():
                          % (runs, head, med),
                "gpu_vs_oracle_maxabs": maxerr}
     qh, kvh, dim, nq, nkeys, causal, window, fq, _, _ = WORKLOADS[head]
+    # roofline of the dominant kernel(s): the launches that stream K/V, timed by
+    # the library's event spans (the ordered combine is excluded)
+    stream_s = hr["stream_kernel_ms"] * 1e-3
     if kind == "decode":
         value, unit, metric = hr["GB/s"], "GB/s", "decode-attn HBM GB/s at 32K KV"
-        roof = {"bound": "hbm", "achieved": hr["GB/s"], "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": hr["GB/s"] / HBM_PEAK_GBS, "traffic": None}
+        ach = hr["algorithmic_bytes"] / stream_s / 1e9
+        roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": ach / HBM_PEAK_GBS, "traffic": traffic_bytes(head)}
     else:
         value, unit, metric = hr["TFLOP/s"], "TFLOP/s", "prefill attn TFLOP/s"
-        roof = {"bound": "mfma", "achieved": hr["TFLOP/s"], "peak": FP32_MFMA_PEAK_TFS,
-                "unit": "TFLOP/s", "frac": hr["TFLOP/s"] / FP32_MFMA_PEAK_TFS, "traffic": None}
+        ach = hr["algorithmic_flops"] / stream_s / 1e12
+        roof = {"bound": "mfma", "achieved": ach, "peak": FP32_MFMA_PEAK_TFS,
+                "unit": "TFLOP/s", "frac": ach / FP32_MFMA_PEAK_TFS,
+                "traffic": traffic_bytes(head)}
+    roof["kernel"] = hr["kernel"]
     line = {
         "metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": hr["steps"],
         "warmup": args.warmup, "ms_per_step": hr["ms"], "higher_is_better": True,

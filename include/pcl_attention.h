@@ -104,6 +104,8 @@ enum pcl_kernel {
     PCL_KERNEL_TILED_SPLIT = 3, /* LDS-tiled prefill, one key chunk per block */
     PCL_KERNEL_PIPE_KV = 4,     /* pipelined split-KV decode (score/value wave
                                    pairs, head dim <= 256) + ordered combine */
+    PCL_KERNEL_TWO_PASS = 5,    /* split-KV decode as a K-streaming pass and a
+                                   V-streaming pass + ordered combine */
 };
 
 /* Attention of nq query positions over keys [0, n0+n1): keys 0..n0-1 come
@@ -163,6 +165,17 @@ int pcl_context_reserve(pcl_context *ctx, size_t bytes);
 int pcl_context_sync(pcl_context *ctx, int *device_error);
 /* Kernel the descriptor resolves to under PCL_KERNEL_AUTO. */
 int pcl_attention_resolve_kernel(const pcl_attention_desc *desc);
+
+/* Per-kernel timing, the device-side counterpart of the engine's stage
+ * timers (stats::Span, src/engine/stats.rs:9-64). While enabled, every launch
+ * records HIP events on the context's stream around the kernels that stream
+ * K/V (role 0: split-KV, pipelined, two-pass or tiled kernels) and around the
+ * ordered combine (role 1). pcl_context_timing waits for the stream, adds the
+ * elapsed times of the recorded launches to ms[role] and their number to
+ * launches[role], and forgets them. Enabling costs two event records per role
+ * per launch; leave it off in production. */
+int pcl_context_set_timing(pcl_context *ctx, int enable);
+int pcl_context_timing(pcl_context *ctx, double *ms, int64_t *launches);
 
 /* Library identification (for loaders). */
 const char *pcl_version(void);

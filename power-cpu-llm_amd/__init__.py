@@ -27,9 +27,11 @@ LIB_PATH = os.path.join(HERE, "libpcl_attention.so")
 OK, INVALID_SHAPE, INVALID_PARAMETER, NON_FINITE_VALUE = 0, 1, 2, 3
 ERROR_NAMES = {INVALID_SHAPE: "InvalidShape", INVALID_PARAMETER: "InvalidParameter",
                NON_FINITE_VALUE: "NonFiniteValue"}
-KERNEL_AUTO, KERNEL_SPLIT_KV, KERNEL_TILED, KERNEL_TILED_SPLIT, KERNEL_PIPE_KV = 0, 1, 2, 3, 4
+(KERNEL_AUTO, KERNEL_SPLIT_KV, KERNEL_TILED, KERNEL_TILED_SPLIT, KERNEL_PIPE_KV,
+ KERNEL_TWO_PASS) = 0, 1, 2, 3, 4, 5
 KERNEL_NAMES = {KERNEL_SPLIT_KV: "split_kv", KERNEL_TILED: "tiled",
-                KERNEL_TILED_SPLIT: "tiled_split", KERNEL_PIPE_KV: "pipe_kv"}
+                KERNEL_TILED_SPLIT: "tiled_split", KERNEL_PIPE_KV: "pipe_kv",
+                KERNEL_TWO_PASS: "two_pass"}
 
 # Every symbol include/pcl_attention.h declares.
 EXPORTS = (
@@ -46,6 +48,8 @@ EXPORTS = (
     "pcl_context_reserve",
     "pcl_context_sync",
     "pcl_attention_resolve_kernel",
+    "pcl_context_set_timing",
+    "pcl_context_timing",
     "pcl_version",
 )
 
@@ -132,6 +136,11 @@ def load():
     lib.pcl_context_sync.argtypes = [vp, ctypes.POINTER(ctypes.c_int)]
     lib.pcl_attention_resolve_kernel.restype = ctypes.c_int
     lib.pcl_attention_resolve_kernel.argtypes = [ctypes.POINTER(PclDesc)]
+    lib.pcl_context_set_timing.restype = ctypes.c_int
+    lib.pcl_context_set_timing.argtypes = [vp, ctypes.c_int]
+    lib.pcl_context_timing.restype = ctypes.c_int
+    lib.pcl_context_timing.argtypes = [vp, ctypes.POINTER(ctypes.c_double),
+                                       ctypes.POINTER(ctypes.c_int64)]
     lib.pcl_version.restype = ctypes.c_char_p
     lib.pcl_version.argtypes = []
     _lib = lib
@@ -306,6 +315,21 @@ class Context:
 
     def resolve_kernel(self, desc):
         return self.lib.pcl_attention_resolve_kernel(ctypes.byref(desc))
+
+    def set_timing(self, enable):
+        rc = self.lib.pcl_context_set_timing(self.handle, int(bool(enable)))
+        if rc != OK:
+            raise AttentionError(rc)
+
+    def timing(self):
+        """Wait; returns ((stream_ms, combine_ms), (stream_launches,
+        combine_launches)) accumulated since the last call."""
+        ms = (ctypes.c_double * 2)(0.0, 0.0)
+        n = (ctypes.c_int64 * 2)(0, 0)
+        rc = self.lib.pcl_context_timing(self.handle, ms, n)
+        if rc != OK:
+            raise AttentionError(rc)
+        return (ms[0], ms[1]), (n[0], n[1])
 
     def sync(self):
         """Wait; returns the device error flag (cleared)."""

@@ -11,7 +11,8 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libpcl_attention.so")
-SOURCES = ["csrc/split_kv.hip", "csrc/pipe_kv.hip", "csrc/tiled.hip", "csrc/api.hip"]
+SOURCES = ["csrc/split_kv.hip", "csrc/pipe_kv.hip", "csrc/two_pass.hip", "csrc/tiled.hip",
+           "csrc/api.hip"]
 HEADERS = ["csrc/attention_device.hpp", os.path.join(ROOT, "include", "pcl_attention.h")]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -15,10 +15,18 @@ hipError_t launch_split_kv(const Params &p, hipStream_t stream);
 hipError_t launch_combine(const Params &p, hipStream_t stream);
 hipError_t launch_pipe_kv(const Params &p, hipStream_t stream);
 hipError_t launch_tiled(const Params &p, int split, hipStream_t stream);
+hipError_t launch_two_pass(const Params &p, hipStream_t stream);
 int tiled_rows(int dk);
+int rec_floats();
 } // namespace pcl
 
 using pcl::Params;
+
+// Event pair of one timed kernel role in one launch.
+struct TimedSpan {
+    hipEvent_t start, stop;
+    int role;
+};
 
 struct pcl_context {
     int device = 0;
@@ -30,6 +38,10 @@ struct pcl_context {
     // Staging buffers of the host-pointer entries (grow-only).
     void *stage[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
     size_t stage_bytes[5] = {0, 0, 0, 0, 0};
+    // per-kernel timing: recorded spans and a pool of free events
+    bool timing = false;
+    std::vector<TimedSpan> spans;
+    std::vector<hipEvent_t> free_events;
 };
 
 namespace {
@@ -37,7 +49,11 @@ namespace {
 constexpr int kMaxDim = 512;
 constexpr int kTiledMaxDk = 256;
 constexpr int kPipeMaxDk = 256;
-constexpr int64_t kPipeMinBlocks = 512;
+// Decode launches of at least this many (chunk, unit, KV head) items are
+// bandwidth-bound and take a streaming kernel (pipelined up to head dim 256,
+// two passes above); shorter ones are latency-bound and take the four-phase
+// kernel.
+constexpr int64_t kStreamMinItems = 256;
 
 void report(const char *what, hipError_t e)
 {
@@ -59,7 +75,8 @@ struct Plan {
     Params p;
     int kernel = PCL_KERNEL_SPLIT_KV;
     size_t ws_floats = 0;
-    bool empty = false; // nothing to compute
+    size_t rec_floats = 0; // two-pass tile records (after the partials)
+    bool empty = false;    // nothing to compute
 };
 
 // Visible key chunks of the whole launch (descriptor masks only narrow it).
@@ -86,13 +103,16 @@ int choose_kernel(int requested, int dk, int64_t nrows, int64_t nkv, int64_t nch
         return requested;
     if (requested == PCL_KERNEL_PIPE_KV)
         return dk <= kPipeMaxDk ? requested : PCL_KERNEL_SPLIT_KV;
+    if (requested == PCL_KERNEL_TWO_PASS)
+        return requested;
     if (dk > kTiledMaxDk || nrows < 64) {
-        // decode: the pipelined wave pairs stream long caches fastest; short
-        // launches (few workgroups, so latency-bound) and head dims above 256
-        // take the four-phase kernel with DK/64 waves per chunk
+        // decode: long caches take a streaming kernel; short launches (few
+        // workgroups, so latency-bound) take the four-phase kernel with DK/64
+        // waves per chunk
         const int64_t units = (nrows + pcl::kRows - 1) / pcl::kRows;
-        return dk <= kPipeMaxDk && nch * nkv * units >= kPipeMinBlocks ? PCL_KERNEL_PIPE_KV
-                                                                       : PCL_KERNEL_SPLIT_KV;
+        if (nch * nkv * units < kStreamMinItems)
+            return PCL_KERNEL_SPLIT_KV;
+        return dk <= kPipeMaxDk ? PCL_KERNEL_PIPE_KV : PCL_KERNEL_TWO_PASS;
     }
     const int64_t rows = pcl::tiled_rows(dk);
     const int64_t blocks = (nrows + rows - 1) / rows * nkv;
@@ -110,7 +130,7 @@ int make_plan(const pcl_attention_desc &d, int64_t h_lo, int64_t h_hi, int64_t h
         d.dim % 16 != 0 || d.dim > kMaxDim || d.nq < 0 || d.n0 < 0 || d.n1 < 0 ||
         d.kh_first < 0 || d.kh_first > d.kh_end || d.kh_end > d.kvheads || d.window < 0)
         return PCL_INVALID_SHAPE;
-    if (d.kernel < PCL_KERNEL_AUTO || d.kernel > PCL_KERNEL_PIPE_KV)
+    if (d.kernel < PCL_KERNEL_AUTO || d.kernel > PCL_KERNEL_TWO_PASS)
         return PCL_INVALID_PARAMETER;
     const int64_t group = d.qheads / d.kvheads;
     const int64_t nkeys = d.n0 + d.n1;
@@ -190,7 +210,8 @@ int make_plan(const pcl_attention_desc &d, int64_t h_lo, int64_t h_hi, int64_t h
     p.nspan = (int)(s_hi - s_lo);
     const bool partials = plan->kernel == PCL_KERNEL_TILED_SPLIT ||
                           ((plan->kernel == PCL_KERNEL_SPLIT_KV ||
-                            plan->kernel == PCL_KERNEL_PIPE_KV) && nch > 1);
+                            plan->kernel == PCL_KERNEL_PIPE_KV ||
+                            plan->kernel == PCL_KERNEL_TWO_PASS) && nch > 1);
     plan->ws_floats = 0;
     if (partials) {
         plan->ws_floats = (size_t)nkv * p.nrows_pad * nch * (dk + 2);
@@ -199,6 +220,10 @@ int make_plan(const pcl_attention_desc &d, int64_t h_lo, int64_t h_hi, int64_t h
     } else if (plan->kernel == PCL_KERNEL_TILED && p.nspan > 1) {
         // the tiled kernel's running totals across spans
         plan->ws_floats = (size_t)nkv * p.nrows_pad * dk;
+    }
+    if (plan->kernel == PCL_KERNEL_TWO_PASS) {
+        plan->rec_floats = (size_t)nkv * p.units * nch * pcl::rec_floats();
+        plan->ws_floats = round_up((int64_t)plan->ws_floats, 4) + plan->rec_floats;
     }
     return PCL_OK;
 }
@@ -222,6 +247,46 @@ int ensure_workspace(pcl_context *ctx, size_t bytes)
     return PCL_OK;
 }
 
+hipEvent_t take_event(pcl_context *ctx)
+{
+    if (!ctx->free_events.empty()) {
+        hipEvent_t e = ctx->free_events.back();
+        ctx->free_events.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess)
+        return nullptr;
+    return e;
+}
+
+// Opens a timed span of `role` on the context's stream (no-op when timing is
+// off); close_span records its end.
+int open_span(pcl_context *ctx, int role)
+{
+    if (!ctx->timing)
+        return -1;
+    TimedSpan t;
+    t.start = take_event(ctx);
+    t.stop = take_event(ctx);
+    t.role = role;
+    if (!t.start || !t.stop || hipEventRecord(t.start, ctx->stream) != hipSuccess) {
+        if (t.start)
+            ctx->free_events.push_back(t.start);
+        if (t.stop)
+            ctx->free_events.push_back(t.stop);
+        return -1;
+    }
+    ctx->spans.push_back(t);
+    return (int)ctx->spans.size() - 1;
+}
+
+void close_span(pcl_context *ctx, int idx)
+{
+    if (idx >= 0)
+        (void)hipEventRecord(ctx->spans[idx].stop, ctx->stream);
+}
+
 int run_plan(pcl_context *ctx, Plan &plan)
 {
     if (plan.empty)
@@ -232,37 +297,50 @@ int run_plan(pcl_context *ctx, Plan &plan)
         const int rc = ensure_workspace(ctx, plan.ws_floats * sizeof(float));
         if (rc != PCL_OK)
             return rc;
-        const size_t o_floats = (size_t)p.nkv * p.nrows_pad * p.nch * p.dk;
-        const size_t ml_floats = (size_t)p.nkv * p.nrows_pad * p.nch * 2;
-        p.ws_o = static_cast<float *>(ctx->ws);
-        p.ws_ml = p.ws_o + o_floats;
-        if (p.nspan > 1) {
-            p.ws2_o = p.ws_ml + ml_floats;
-            p.ws2_ml = p.ws2_o + (size_t)p.nkv * p.nrows_pad * p.nspan * p.dk;
+        float *ws = static_cast<float *>(ctx->ws);
+        if (plan.ws_floats > plan.rec_floats) {
+            const size_t o_floats = (size_t)p.nkv * p.nrows_pad * p.nch * p.dk;
+            const size_t ml_floats = (size_t)p.nkv * p.nrows_pad * p.nch * 2;
+            p.ws_o = ws;
+            p.ws_ml = p.ws_o + o_floats;
+            if (p.nspan > 1) {
+                p.ws2_o = p.ws_ml + ml_floats;
+                p.ws2_ml = p.ws2_o + (size_t)p.nkv * p.nrows_pad * p.nspan * p.dk;
+            }
         }
+        if (plan.rec_floats)
+            p.ws_rec = ws + (plan.ws_floats - plan.rec_floats);
     }
     hipError_t e = hipSuccess;
+    const bool combine = plan.kernel == PCL_KERNEL_TILED_SPLIT ||
+                         ((plan.kernel == PCL_KERNEL_SPLIT_KV || plan.kernel == PCL_KERNEL_PIPE_KV ||
+                           plan.kernel == PCL_KERNEL_TWO_PASS) &&
+                          p.ws_o);
+    int span = open_span(ctx, 0);
     switch (plan.kernel) {
     case PCL_KERNEL_SPLIT_KV:
         e = pcl::launch_split_kv(p, ctx->stream);
-        if (e == hipSuccess && p.ws_o)
-            e = pcl::launch_combine(p, ctx->stream);
         break;
     case PCL_KERNEL_PIPE_KV:
         e = pcl::launch_pipe_kv(p, ctx->stream);
-        if (e == hipSuccess && p.ws_o)
-            e = pcl::launch_combine(p, ctx->stream);
+        break;
+    case PCL_KERNEL_TWO_PASS:
+        e = pcl::launch_two_pass(p, ctx->stream);
         break;
     case PCL_KERNEL_TILED:
         e = pcl::launch_tiled(p, 0, ctx->stream);
         break;
     case PCL_KERNEL_TILED_SPLIT:
         e = pcl::launch_tiled(p, 1, ctx->stream);
-        if (e == hipSuccess)
-            e = pcl::launch_combine(p, ctx->stream);
         break;
     default:
         return PCL_INVALID_SHAPE;
+    }
+    close_span(ctx, span);
+    if (e == hipSuccess && combine) {
+        span = open_span(ctx, 1);
+        e = pcl::launch_combine(p, ctx->stream);
+        close_span(ctx, span);
     }
     if (e != hipSuccess) {
         report("kernel launch", e);
@@ -434,6 +512,12 @@ void pcl_context_destroy(pcl_context *ctx)
     (void)hipSetDevice(ctx->device);
     if (ctx->stream)
         (void)hipStreamSynchronize(ctx->stream);
+    for (const TimedSpan &t : ctx->spans) {
+        (void)hipEventDestroy(t.start);
+        (void)hipEventDestroy(t.stop);
+    }
+    for (hipEvent_t e : ctx->free_events)
+        (void)hipEventDestroy(e);
     for (int i = 0; i < 5; ++i)
         if (ctx->stage[i])
             (void)hipFree(ctx->stage[i]);
@@ -498,6 +582,39 @@ int pcl_attention_launch(pcl_context *ctx, const pcl_attention_desc *desc)
         return rc;
     (void)hipSetDevice(ctx->device);
     return run_plan(ctx, plan);
+}
+
+int pcl_context_set_timing(pcl_context *ctx, int enable)
+{
+    if (!ctx)
+        return PCL_INVALID_SHAPE;
+    ctx->timing = enable != 0;
+    return PCL_OK;
+}
+
+int pcl_context_timing(pcl_context *ctx, double *ms, int64_t *launches)
+{
+    if (!ctx || !ms || !launches)
+        return PCL_INVALID_SHAPE;
+    (void)hipSetDevice(ctx->device);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    for (const TimedSpan &t : ctx->spans) {
+        float x = 0.f;
+        if (e == hipSuccess)
+            e = hipEventElapsedTime(&x, t.start, t.stop);
+        if (e == hipSuccess) {
+            ms[t.role] += x;
+            launches[t.role] += 1;
+        }
+        ctx->free_events.push_back(t.start);
+        ctx->free_events.push_back(t.stop);
+    }
+    ctx->spans.clear();
+    if (e != hipSuccess) {
+        report("timing", e);
+        return PCL_NON_FINITE_VALUE;
+    }
+    return PCL_OK;
 }
 
 int pcl_context_sync(pcl_context *ctx, int *device_error)

@@ -97,6 +97,8 @@ struct Params {
     int s_lo;      // first span of the launch (absolute span index)
     int nspan;     // spans of the launch
     int dk;        // padded head dim of the launch
+    // tile records of the two-pass decode: [nkv][units][nch][kRecFloats]
+    float *ws_rec;
     int *err;
 };
 
@@ -113,6 +115,13 @@ typedef const __attribute__((address_space(1))) uint8_t *gu8_cptr;
 __device__ __forceinline__ f4 ldg4(const float *p)
 {
     return *(gf4_cptr)p;
+}
+
+// Streaming load for data read exactly once (decode K/V): the nontemporal
+// hint keeps it from displacing reused lines; the HBM stream runs faster.
+__device__ __forceinline__ f4 ldg4_stream(const float *p)
+{
+    return __builtin_nontemporal_load((gf4_cptr)p);
 }
 
 __device__ __forceinline__ void stg4(float *p, f4 v)

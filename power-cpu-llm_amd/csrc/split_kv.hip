@@ -56,48 +56,6 @@ __device__ __forceinline__ void merge_into(Merged &s, float m, float l, float o)
     s.M = f.m;
 }
 
-// Chunks [c0, c1) (launch-local indices) of one element, in order.
-__device__ __forceinline__ Merged merge_span_chunks(const float *ml, const float *o, int dk,
-                                                    int c0, int c1)
-{
-    float mv[kSpanChunks], lv[kSpanChunks], ov[kSpanChunks];
-#pragma unroll
-    for (int i = 0; i < kSpanChunks; ++i) {
-        const int cc = c0 + i < c1 ? c0 + i : c0;
-        mv[i] = ldg(ml + 2 * cc);
-        lv[i] = ldg(ml + 2 * cc + 1);
-        ov[i] = ldg(o + (int64_t)cc * dk);
-    }
-    Merged s = {kNegInf, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < kSpanChunks; ++i)
-        if (c0 + i < c1)
-            merge_into(s, mv[i], lv[i], ov[i]);
-    return s;
-}
-
-// Spans [0, nspan) of one element, in order.
-__device__ __forceinline__ Merged merge_spans(const float *ml, const float *o, int dk, int nspan)
-{
-    Merged s = {kNegInf, 0.f, 0.f};
-    constexpr int B = 8; // spans requested per batch
-    for (int s0 = 0; s0 < nspan; s0 += B) {
-        float mv[B], lv[B], ov[B];
-#pragma unroll
-        for (int i = 0; i < B; ++i) {
-            const int ss = s0 + i < nspan ? s0 + i : s0;
-            mv[i] = ldg(ml + 2 * ss);
-            lv[i] = ldg(ml + 2 * ss + 1);
-            ov[i] = ldg(o + (int64_t)ss * dk);
-        }
-#pragma unroll
-        for (int i = 0; i < B; ++i)
-            if (s0 + i < nspan)
-                merge_into(s, mv[i], lv[i], ov[i]);
-    }
-    return s;
-}
-
 // Launch-local chunk range of span `sl`.
 __device__ __forceinline__ void span_chunks(const Params &p, int sl, int *c0, int *c1)
 {
@@ -113,17 +71,6 @@ __device__ __forceinline__ float *out_ptr(const Params &p, int kh, int row)
     if (h < p.h_lo || h >= p.h_hi)
         return nullptr;
     return p.out + (int64_t)query * p.o_stride + (int64_t)(h - p.h_base) * p.dim;
-}
-
-// Final value of a merged element: merged into the empty total when there is
-// only one span (exact), then normalised.
-__device__ __forceinline__ float finish(const Merged &s, bool single_span)
-{
-    if (single_span) {
-        const MergeFactors f = merge_factors(kNegInf, s.M);
-        return merge_value(0.f, s.acc, f) / merge_value(0.f, s.L, f);
-    }
-    return s.acc / s.L;
 }
 
 template <int DK>
@@ -182,7 +129,7 @@ __global__ __launch_bounds__(DK, SplitCfg<DK>::waves_per_eu) void split_kv_kerne
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const int d = 32 * u + 8 * g + 4 * h;
-                const f4 x = ld4(kp + (d < p.dim ? d : 0));
+                const f4 x = ldg4_stream(kp + (d < p.dim ? d : 0));
                 kb[u][h] = d < p.dim ? x : zero4();
             }
     };
@@ -216,7 +163,7 @@ __global__ __launch_bounds__(DK, SplitCfg<DK>::waves_per_eu) void split_kv_kerne
             for (int r = 0; r < 4; ++r) {
                 const int64_t key = cbase + t * kTile + 16 * b + 4 * g + r;
                 const int64_t kc = key < klast ? key : klast;
-                dst[4 * b + r] = ld4(value_row(p, kc) + (int64_t)kh * p.dim + dvc);
+                dst[4 * b + r] = ldg4_stream(value_row(p, kc) + (int64_t)kh * p.dim + dvc);
             }
     };
 
@@ -367,58 +314,106 @@ __global__ __launch_bounds__(DK, SplitCfg<DK>::waves_per_eu) void split_kv_kerne
     }
 }
 
-// Level 1 of the combine: the chunks of one span, for one (row, dim) per
-// thread. With a single span the result is final.
-__global__ __launch_bounds__(256) void combine_span_kernel(Params p)
+// Two-level combine for launches of many spans, one wave per 256 output dims
+// of one row, so every load is a contiguous KiB of one partial.
+// Level 1: wave ((kv, row), span, piece) merges the span's chunks in order;
+// with a single span it writes the output, else the span partial.
+__global__ __launch_bounds__(64) void combine_level1_kernel(Params p)
 {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (int64_t)p.nrows * p.dim)
-        return;
-    const int kvl = blockIdx.z;
+    const int lane = threadIdx.x;
+    const int piece = blockIdx.z;
     const int sl = blockIdx.y;
-    const int row = (int)(idx / p.dim);
-    const int d = (int)(idx % p.dim);
-    float *o = out_ptr(p, p.kh_first + kvl, row);
-    if (!o)
-        return;
+    const int kvl = blockIdx.x / p.nrows;
+    const int row = blockIdx.x % p.nrows;
+    const int d = 256 * piece + 4 * lane;
+    const bool din = d < p.dim;
     int c0, c1;
     span_chunks(p, sl, &c0, &c1);
     const int64_t slot0 = ((int64_t)kvl * p.nrows_pad + row) * p.nch;
-    const Merged sm =
-        merge_span_chunks(p.ws_ml + 2 * slot0, p.ws_o + slot0 * p.dk + d, p.dk, c0, c1);
+    float mv[kSpanChunks], lv[kSpanChunks];
+    f4 ov[kSpanChunks];
+#pragma unroll
+    for (int i = 0; i < kSpanChunks; ++i) {
+        const int64_t cc = slot0 + (c0 + i < c1 ? c0 + i : c0);
+        mv[i] = ldg(p.ws_ml + 2 * cc);
+        lv[i] = ldg(p.ws_ml + 2 * cc + 1);
+        ov[i] = ldg4(p.ws_o + cc * p.dk + (din ? d : 0));
+    }
+    Merged4 s = {kNegInf, 0.f, zero4()};
+#pragma unroll
+    for (int i = 0; i < kSpanChunks; ++i) {
+        // chunks past the span merge as empty parts (no-ops)
+        const bool in = c0 + i < c1;
+        merge_into4(s, in ? mv[i] : kNegInf, in ? lv[i] : 0.f, in ? ov[i] : zero4());
+    }
     if (p.nspan == 1) {
-        const float v = finish(sm, true);
-        stg(o + d, v);
-        if (!is_finite(v))
+        float *o = out_ptr(p, p.kh_first + kvl, row);
+        if (!o || !din)
+            return;
+        // one span: merged into the empty total (exact), then normalised
+        const MergeFactors f = merge_factors(kNegInf, s.M);
+        const float L = merge_value(0.f, s.L, f);
+        f4 v;
+        bool nonfinite = false;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[j] = merge_value(0.f, s.acc[j], f) / L;
+            nonfinite |= !is_finite(v[j]);
+        }
+        stg4(o + d, v);
+        if (nonfinite)
             atomicOr(p.err, kErrOutput);
         return;
     }
     const int64_t slot = ((int64_t)kvl * p.nrows_pad + row) * p.nspan + sl;
-    stg(p.ws2_o + slot * p.dk + d, sm.acc);
-    if (d == 0) {
-        stg(p.ws2_ml + 2 * slot, sm.M);
-        stg(p.ws2_ml + 2 * slot + 1, sm.L);
+    if (din)
+        stg4(p.ws2_o + slot * p.dk + d, s.acc);
+    if (lane == 0 && piece == 0) {
+        stg(p.ws2_ml + 2 * slot, s.M);
+        stg(p.ws2_ml + 2 * slot + 1, s.L);
     }
 }
 
-// Level 2 of the combine: the spans, in ascending order.
-__global__ __launch_bounds__(256) void combine_final_kernel(Params p)
+// Level 2: wave ((kv, row), piece) merges the span partials in order.
+__global__ __launch_bounds__(64) void combine_level2_kernel(Params p)
 {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (int64_t)p.nrows * p.dim)
-        return;
-    const int kvl = blockIdx.z;
-    const int row = (int)(idx / p.dim);
-    const int d = (int)(idx % p.dim);
+    const int lane = threadIdx.x;
+    const int piece = blockIdx.z;
+    const int kvl = blockIdx.x / p.nrows;
+    const int row = blockIdx.x % p.nrows;
+    const int d = 256 * piece + 4 * lane;
+    const bool din = d < p.dim;
     float *o = out_ptr(p, p.kh_first + kvl, row);
-    if (!o)
+    if (!o || !din)
         return;
     const int64_t slot0 = ((int64_t)kvl * p.nrows_pad + row) * p.nspan;
-    const Merged st =
-        merge_spans(p.ws2_ml + 2 * slot0, p.ws2_o + slot0 * p.dk + d, p.dk, p.nspan);
-    const float v = finish(st, false);
-    stg(o + d, v);
-    if (!is_finite(v))
+    Merged4 s = {kNegInf, 0.f, zero4()};
+    constexpr int B = 32; // spans requested per batch
+    for (int s0 = 0; s0 < p.nspan; s0 += B) {
+        float mv[B], lv[B];
+        f4 ov[B];
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            const int64_t ss = slot0 + (s0 + i < p.nspan ? s0 + i : s0);
+            mv[i] = ldg(p.ws2_ml + 2 * ss);
+            lv[i] = ldg(p.ws2_ml + 2 * ss + 1);
+            ov[i] = ldg4(p.ws2_o + ss * p.dk + d);
+        }
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            const bool in = s0 + i < p.nspan;
+            merge_into4(s, in ? mv[i] : kNegInf, in ? lv[i] : 0.f, in ? ov[i] : zero4());
+        }
+    }
+    f4 v;
+    bool nonfinite = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        v[j] = s.acc[j] / s.L;
+        nonfinite |= !is_finite(v[j]);
+    }
+    stg4(o + d, v);
+    if (nonfinite)
         atomicOr(p.err, kErrOutput);
 }
 
@@ -440,9 +435,11 @@ hipError_t launch_split_kv(const Params &p, hipStream_t stream)
 // G = 64 / SP element groups (four consecutive dims of one row) x SP span
 // lanes: span lane s merges the chunks of span s for its element group (one
 // batch of loads), then every lane folds the group's span partials, gathered
-// by cross-lane reads, in ascending order. The values are those of the two
-// kernels above, which serve launches of more than 64 spans.
-constexpr int kCombineMaxSpans = 64;
+// by cross-lane reads, in ascending order. The values are those of the
+// two-level kernels above, which serve launches of more spans: their loads
+// are whole KiB of one partial, while here a wave's loads scatter over span
+// lanes, which costs more than the second launch once spans are many.
+constexpr int kCombineMaxSpans = 8;
 
 typedef float f2 __attribute__((ext_vector_type(2)));
 
@@ -543,14 +540,14 @@ hipError_t launch_combine(const Params &p, hipStream_t stream)
         combine_kernel<<<dim3(bx, p.nkv), 64, 0, stream>>>(p, lanes);
         return hipGetLastError();
     }
-    // very long launches: span partials through the workspace, two kernels
-    const int64_t n = (int64_t)p.nrows * p.dim;
-    const unsigned bx = (unsigned)((n + 255) / 256);
-    combine_span_kernel<<<dim3(bx, p.nspan, p.nkv), 256, 0, stream>>>(p);
+    // many spans: span partials through the workspace, two launches
+    const unsigned pieces = (unsigned)((p.dim + 255) / 256);
+    const unsigned rows = (unsigned)(p.nkv * p.nrows);
+    combine_level1_kernel<<<dim3(rows, p.nspan, pieces), 64, 0, stream>>>(p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.nspan == 1)
         return e;
-    combine_final_kernel<<<dim3(bx, 1, p.nkv), 256, 0, stream>>>(p);
+    combine_level2_kernel<<<dim3(rows, 1, pieces), 64, 0, stream>>>(p);
     return hipGetLastError();
 }
 

@@ -268,11 +268,11 @@ def test_every_kernel_gives_identical_bits(torch, ctx, oracle, case):
     k = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
     v = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
     outs = {}
-    for kernel in (1, 2, 3, 4):
+    for kernel in (1, 2, 3, 4, 5):
         outs[kernel], err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel, causal,
                                      window, 0, fq)
         assert err == 0
-    for kernel in (2, 3, 4):
+    for kernel in (2, 3, 4, 5):
         assert np.array_equal(bits(outs[1]), bits(outs[kernel])), kernel
     for i in sorted({0, nq // 2, nq - 1}):
         m = oracle.encoder_mask(0, nkeys, fq + i, window or None) if causal else None
@@ -293,7 +293,7 @@ def test_explicit_masks_segments_scale_and_kv_ranges_keep_bits(torch, ctx):
     scale = np.float32(1.0 / 16.0)
     base, err = run_desc(torch, ctx, prescale(q, dim), k, v, qheads, kvh, dim, 1, 1, 300, 0, fq)
     assert err == 0
-    for kernel in (1, 2, 3, 4):
+    for kernel in (1, 2, 3, 4, 5):
         # explicit byte masks equal the descriptor's causal window
         got, err = run_desc(torch, ctx, prescale(q, dim), k, v, qheads, kvh, dim, kernel,
                             mask=mask)
@@ -313,6 +313,36 @@ def test_explicit_masks_segments_scale_and_kv_ranges_keep_bits(torch, ctx):
         group = qheads // kvh
         assert err == 0 and np.array_equal(bits(got), bits(base[:, 3 * group * dim:
                                                                 6 * group * dim]))
+
+
+def test_long_launch_combines_agree_across_kernels(torch, ctx, oracle):
+    """More than 8 spans of 4096 keys: the split kernels' two-level combine
+    and the tiled kernel's in-kernel merges give the same bits."""
+    qheads, kvh, dim, nq, nkeys = 16, 8, 256, 64, 36000
+    fq = nkeys - nq
+    q = gpu_normals(torch, 0x5EED0777, (nq, qheads, dim)) * (1.0 / 16.0)
+    k = gpu_normals(torch, 0x5EED0778, (nkeys, kvh, dim))
+    v = gpu_normals(torch, 0x5EED0779, (nkeys, kvh, dim))
+    outs = {}
+    for kernel in (1, 2, 3, 4, 5):
+        out = torch.full((nq, qheads, dim), float("nan"), device="cuda:0")
+        d = ctx.desc(q=q.data_ptr(), q_stride=qheads * dim, nq=nq, k0=k.data_ptr(),
+                     v0=v.data_ptr(), n0=nkeys, qheads=qheads, kvheads=kvh, dim=dim, kh_first=0,
+                     kh_end=kvh, causal=1, window=0, first_key=0, first_query=fq,
+                     out=out.data_ptr(), o_stride=qheads * dim, kernel=kernel)
+        ctx.reserve(ctx.workspace_bytes(d))
+        ctx.launch(d)
+        assert ctx.sync() == 0
+        outs[kernel] = out.cpu().numpy()
+    for kernel in (2, 3, 4, 5):
+        assert np.array_equal(bits(outs[1]), bits(outs[kernel])), kernel
+    qn, kn, vn = (x.cpu().numpy().reshape(-1) for x in (q, k, v))
+    for i in (0, nq - 1):
+        m = oracle.encoder_mask(0, nkeys, fq + i, None)
+        ok, want = oracle.heads(qn[i * qheads * dim:(i + 1) * qheads * dim], kn, vn, qheads,
+                                kvh, dim, nkeys, m)
+        assert ok
+        assert_parity(outs[1][i], want, dim)
 
 
 def test_masked_suffix_does_not_change_results(torch, ctx):
@@ -342,7 +372,7 @@ def test_device_error_flags(torch, ctx):
     bad_k[10, 1, 5] = np.nan
     bad_v = v.copy()
     bad_v[20, 0, 3] = np.inf
-    for kernel in (1, 2, 3, 4):
+    for kernel in (1, 2, 3, 4, 5):
         _, err = run_desc(torch, ctx, q, bad_k, v, qheads, kvh, dim, kernel)
         assert err & 1
         _, err = run_desc(torch, ctx, q, k, bad_v, qheads, kvh, dim, kernel)
@@ -366,9 +396,9 @@ def decode_config(torch, ctx, oracle, qheads, kvh, dim, nkeys, window, seed, uni
     if unit_k:
         k = k / k.norm(dim=-1, keepdim=True)
     outs = {}
-    # the automatic choice, then both split-KV kernels (the pipelined one up to
+    # the automatic choice, then every split-KV kernel (the pipelined one up to
     # head dim 256): all bitwise equal
-    for kernel in (0, 1, 4) if dim <= 256 else (0, 1):
+    for kernel in (0, 1, 4, 5) if dim <= 256 else (0, 1, 5):
         out = torch.full((1, qheads, dim), float("nan"), device="cuda:0")
         d = ctx.desc(q=q.data_ptr(), q_stride=qheads * dim, nq=1, k0=k.data_ptr(),
                      v0=v.data_ptr(), n0=nkeys, qheads=qheads, kvheads=kvh, dim=dim, kh_first=0,
