@@ -230,10 +230,11 @@ def main():
     pcl.load()
     ctx = pcl.Context(0, torch.cuda.current_stream().cuda_stream)
     if args.copy_calibration:
+        # a plain elementwise copy kernel of known size: reads and writes 256 MiB
         src = torch.ones(64 << 20, device="cuda:0", dtype=torch.float32)
         dst = torch.empty_like(src)
         for _ in range(3):
-            dst.copy_(src)
+            torch.mul(src, 1.0, out=dst)
         torch.cuda.synchronize()
         del src, dst
 

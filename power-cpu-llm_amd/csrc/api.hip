@@ -48,11 +48,10 @@ namespace {
 
 constexpr int kMaxDim = 512;
 constexpr int kTiledMaxDk = 256;
-constexpr int kPipeMaxDk = 256;
+constexpr int kPipeMaxDk = 512;
 // Decode launches of at least this many (chunk, unit, KV head) items are
-// bandwidth-bound and take a streaming kernel (pipelined up to head dim 256,
-// two passes above); shorter ones are latency-bound and take the four-phase
-// kernel.
+// bandwidth-bound and take the pipelined kernel; shorter ones are
+// latency-bound and take the four-phase kernel.
 constexpr int64_t kStreamMinItems = 256;
 
 void report(const char *what, hipError_t e)
@@ -112,7 +111,7 @@ int choose_kernel(int requested, int dk, int64_t nrows, int64_t nkv, int64_t nch
         const int64_t units = (nrows + pcl::kRows - 1) / pcl::kRows;
         if (nch * nkv * units < kStreamMinItems)
             return PCL_KERNEL_SPLIT_KV;
-        return dk <= kPipeMaxDk ? PCL_KERNEL_PIPE_KV : PCL_KERNEL_TWO_PASS;
+        return PCL_KERNEL_PIPE_KV;
     }
     const int64_t rows = pcl::tiled_rows(dk);
     const int64_t blocks = (nrows + rows - 1) / rows * nkv;

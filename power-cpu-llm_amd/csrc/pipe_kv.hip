@@ -1,12 +1,14 @@
-// Pipelined split-KV decode for gfx950: a score wave and a value wave per
+// Pipelined split-KV decode for gfx950: a score wave and value waves per
 // (256-key chunk, 16-row unit).
 //
-// Workgroup = 2 waves. The score wave streams K, runs the canonical score
-// chain and online softmax of each tile (attention_device.hpp) and hands the
-// tile's probabilities, alpha and row sum to the value wave through a
-// double-buffered LDS slot. The value wave streams V and runs the P.V chain
-// one tile behind. One barrier per tile keeps the pair in step, and the two
-// waves' MFMA work is balanced (128 MFMAs each per tile at head dim 256).
+// Workgroup = 1 score wave + one value wave per 256 output dims. The score
+// wave streams K, runs the canonical score chain and online softmax of each
+// tile (attention_device.hpp) and hands the tile's probabilities, alpha and
+// row sum to the value waves through a double-buffered LDS slot. The value
+// waves stream V and run the P.V chain one tile behind. One barrier per tile
+// keeps the workgroup in step; at head dim 256 the score and value waves'
+// MFMA work is balanced (128 MFMAs each per tile). At head dim 512 the score
+// wave reads Q^T from LDS so its registers can hold the 32 KiB K block.
 //
 // Each wave keeps exactly one 16-key block of K or V in flight, loading the
 // next block into the same registers as soon as its MFMAs have consumed them.
@@ -22,19 +24,36 @@
 
 namespace pcl {
 
-// LDS hand-over between the score wave and the value wave.
-struct PipeLds {
+// Value waves per workgroup: one per 256 output dims.
+template <int DK> constexpr int pipe_value_waves()
+{
+    return DK > 256 ? DK / 256 : 1;
+}
+
+// Head dims above 256 keep Q^T in LDS (the score wave's registers hold the K
+// block in flight); padded rows avoid bank conflicts.
+template <int DK> constexpr bool pipe_q_lds()
+{
+    return DK > 256;
+}
+
+// LDS hand-over between the score wave and the value waves.
+template <int DK> struct PipeLds {
     float p[2][8][64];    // probabilities, [slot][4b + r][lane]
     float alpha[2][kRows];
     float rs[2][kRows];
     int any[2];
     float m[kRows];       // chunk maximum
+    float q[pipe_q_lds<DK>() ? kRows * (DK + 4) : 1];
 };
 
 template <int DK, bool FULL>
-__device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, int c, PipeLds &s)
+__device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, int c,
+                                           PipeLds<DK> &s)
 {
     constexpr int NU = DK / 32; // score chain steps
+    constexpr bool QLDS = pipe_q_lds<DK>();
+    constexpr int QLD = DK + 4;
     const int lane = threadIdx.x & 63;
     const int col = lane & 15;
     const int g = lane >> 4;
@@ -44,8 +63,24 @@ __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, i
     const int64_t klast = p.nkeys - 1;
     const int64_t hoff = (int64_t)kh * p.dim;
 
-    float q[NU][8];
-    {
+    // Q^T B operands: Q[row][32u + 8g + jj] * q_scale (0 for padding rows).
+    float q[QLDS ? 1 : NU][8];
+    if constexpr (QLDS) {
+        for (int i = lane; i < kRows * (DK / 4); i += 64) {
+            const int r = i / (DK / 4);
+            const int d = (i % (DK / 4)) * 4;
+            const int f = unit * kRows + r;
+            f4 v = f4{0.f, 0.f, 0.f, 0.f};
+            if (f < p.nrows && d < p.dim) {
+                const int qq = f / p.group;
+                const int hh = kh * p.group + f % p.group;
+                v = ldg4(p.q + (int64_t)qq * p.q_stride + (int64_t)hh * p.dim + d) * p.q_scale;
+            }
+            *(f4 *)(s.q + r * QLD + d) = v;
+        }
+        // only this wave reads them; its LDS operations complete in order
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    } else {
         const bool rin = row < p.nrows;
         const int query = rin ? row / p.group : 0;
         const int h = kh * p.group + (rin ? row % p.group : 0);
@@ -98,10 +133,25 @@ __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, i
             __builtin_amdgcn_sched_barrier(0);
             if (tile_any) {
 #pragma unroll
-                for (int u = 0; u < NU; ++u)
+                for (int u = 0; u < NU; ++u) {
+                    float qv[8];
+                    if constexpr (QLDS) {
+                        const f4 qa0 = *(const f4 *)(s.q + col * QLD + 32 * u + 8 * g);
+                        const f4 qa1 = *(const f4 *)(s.q + col * QLD + 32 * u + 8 * g + 4);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            qv[j] = qa0[j];
+                            qv[4 + j] = qa1[j];
+                        }
+                    } else {
+#pragma unroll
+                        for (int jj = 0; jj < 8; ++jj)
+                            qv[jj] = q[u][jj];
+                    }
 #pragma unroll
                     for (int jj = 0; jj < 8; ++jj)
-                        acc[b] = mfma(kb[u][jj >> 2][jj & 3], q[u][jj], acc[b]);
+                        acc[b] = mfma(kb[u][jj >> 2][jj & 3], qv[jj], acc[b]);
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
             // the next block into the registers just consumed
@@ -154,9 +204,11 @@ __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, i
 enum PipeMode { kDirect = 0, kPartial = 1 };
 
 template <int DK, int MODE, bool FULL>
-__device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, int c, PipeLds &s)
+__device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, int c,
+                                           PipeLds<DK> &s)
 {
-    constexpr int NQ = DK / 64; // 64-dim output groups
+    constexpr int NQ = DK > 256 ? 4 : DK / 64; // 64-dim output groups of this wave
+    const int d0 = 256 * ((int)(threadIdx.x >> 6) - 1); // the wave's first output dim
     const int lane = threadIdx.x & 63;
     const int col = lane & 15;
     const int g = lane >> 4;
@@ -166,7 +218,7 @@ __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, i
     const int64_t klast = p.nkeys - 1;
     const int64_t hoff = (int64_t)kh * p.dim;
 
-    const int dv = 4 * col; // + 64a
+    const int dv = d0 + 4 * col; // + 64a
     f4 vv[4][NQ];           // the half tile in flight: [slice][64-dim group]
     auto load_v = [&](int t, int half) {
 #pragma unroll
@@ -244,7 +296,7 @@ __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, i
         for (int a = 0; a < NQ; ++a)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int d = 64 * a + 16 * g + 4 * i;
+                const int d = d0 + 64 * a + 16 * g + 4 * i;
                 if (d >= p.dim)
                     continue;
                 f4 v;
@@ -266,7 +318,7 @@ __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, i
         for (int a = 0; a < NQ; ++a)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int d = 64 * a + 16 * g + 4 * i;
+                const int d = d0 + 64 * a + 16 * g + 4 * i;
                 if (d >= p.dim)
                     continue;
                 f4 v;
@@ -275,7 +327,7 @@ __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, i
                     v[j] = O[a][j][i];
                 stg4(wo + d, v);
             }
-        if (g == 0) {
+        if (g == 0 && d0 == 0) {
             stg(p.ws_ml + 2 * slot, m);
             stg(p.ws_ml + 2 * slot + 1, l);
         }
@@ -285,9 +337,9 @@ __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, i
 
 // FULL: the head dim equals the padded head dim (no dim clamping).
 template <int DK, int MODE, bool FULL>
-__global__ __launch_bounds__(128, 2) void pipe_kv_kernel(Params p)
+__global__ __launch_bounds__(64 * (1 + pipe_value_waves<DK>()), 2) void pipe_kv_kernel(Params p)
 {
-    __shared__ PipeLds s;
+    __shared__ PipeLds<DK> s;
     const int c = p.c_lo + blockIdx.x;
     const int unit = blockIdx.y % p.units;
     const int kvl = blockIdx.y / p.units;
@@ -304,6 +356,7 @@ template <int MODE, bool FULL> hipError_t launch_mode(const Params &p, hipStream
     case 64: pipe_kv_kernel<64, MODE, FULL><<<grid, 128, 0, stream>>>(p); break;
     case 128: pipe_kv_kernel<128, MODE, FULL><<<grid, 128, 0, stream>>>(p); break;
     case 256: pipe_kv_kernel<256, MODE, FULL><<<grid, 128, 0, stream>>>(p); break;
+    case 512: pipe_kv_kernel<512, MODE, FULL><<<grid, 192, 0, stream>>>(p); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -88,8 +88,8 @@ def test_descriptor_validation_on_the_host(pcl):
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
     assert lib.pcl_attention_workspace_bytes(ctypes.byref(d)) > 0
     d.dim, d.q_stride, d.o_stride = 512, 16 * 512, 16 * 512
-    # above head dim 256: the K pass and the V pass
-    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_TWO_PASS
+    # also at head dim 512 (one score wave, two value waves)
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
     d.dim, d.q_stride, d.o_stride = 256, 16 * 256, 16 * 256
     d.window = 1024  # five chunks per head: the four-phase kernel
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_SPLIT_KV
@@ -99,7 +99,7 @@ def test_descriptor_validation_on_the_host(pcl):
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_TWO_PASS
     d.kernel = pcl.KERNEL_PIPE_KV
     d.dim, d.q_stride, d.o_stride = 512, 16 * 512, 16 * 512
-    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_SPLIT_KV
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
     d.kernel = 6  # no such kernel
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == -1
     d.kernel, d.dim, d.q_stride, d.o_stride = 0, 256, 16 * 256, 16 * 256

@@ -396,9 +396,8 @@ def decode_config(torch, ctx, oracle, qheads, kvh, dim, nkeys, window, seed, uni
     if unit_k:
         k = k / k.norm(dim=-1, keepdim=True)
     outs = {}
-    # the automatic choice, then every split-KV kernel (the pipelined one up to
-    # head dim 256): all bitwise equal
-    for kernel in (0, 1, 4, 5) if dim <= 256 else (0, 1, 5):
+    # the automatic choice, then every split-KV kernel: all bitwise equal
+    for kernel in (0, 1, 4, 5):
         out = torch.full((1, qheads, dim), float("nan"), device="cuda:0")
         d = ctx.desc(q=q.data_ptr(), q_stride=qheads * dim, nq=1, k0=k.data_ptr(),
                      v0=v.data_ptr(), n0=nkeys, qheads=qheads, kvheads=kvh, dim=dim, kh_first=0,
