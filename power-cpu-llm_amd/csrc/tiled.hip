@@ -39,8 +39,30 @@ __device__ __forceinline__ void dma16(const float *g, float *l)
     __builtin_amdgcn_global_load_lds((gbl_ptr_t)g, (lds_ptr_t)l, 16, 0, 0);
 }
 
+// True when every row in [row_lo, row_hi] may attend every key of tile t
+// (no explicit mask; the tile inside the keys and inside every row's causal
+// window).
+__device__ __forceinline__ bool tile_whole(const Params &p, int row_lo, int row_hi, int t)
+{
+    if (p.mask || row_lo > row_hi)
+        return false;
+    const int64_t k0 = (int64_t)t * kTile;
+    if (k0 + kTile > p.nkeys)
+        return false;
+    if (!p.causal)
+        return true;
+    const int64_t kmin = p.first_key + k0;
+    const int64_t kmax = kmin + kTile - 1;
+    const int64_t qlo = p.first_query + row_lo / p.group;
+    const int64_t qhi = p.first_query + row_hi / p.group;
+    return kmax <= qlo && (p.window == 0 || qhi - kmin < p.window);
+}
+
+// One workgroup per CU (its K/V stages fill the LDS), so two waves per SIMD:
+// each wave may hold 256 VGPRs, which the operand double-buffering below uses.
 template <int DK>
-__global__ __launch_bounds__(512) void tiled_kernel(Params p, int split)
+__global__ __launch_bounds__(512, 2) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void tiled_kernel(Params p, int split)
 {
     using LD = TiledLds<DK>;
     constexpr int NU = DK / 32;                         // score chain steps
@@ -62,6 +84,9 @@ __global__ __launch_bounds__(512) void tiled_kernel(Params p, int split)
     const int kh = p.kh_first + kvl;
     const int fa = qb * kTiledRows;
     const int row = fa + w * kRows + col;
+    // the wave's real rows
+    const int wrow_lo = fa + w * kRows;
+    const int wrow_hi = min(wrow_lo + kRows, p.nrows) - 1;
     const bool rin = row < p.nrows;
     const int query = rin ? row / p.group : 0;
     const int head = kh * p.group + (rin ? row % p.group : 0);
@@ -224,33 +249,61 @@ __global__ __launch_bounds__(512) void tiled_kernel(Params p, int split)
         const float *ks = lds + buf * LD::stage;
         const float *vs = ks + LD::tileFloats;
 
+        // Masks. Without an explicit mask, a tile that every row of the wave
+        // sees whole needs no per-key test (padding rows may then count as
+        // allowed: their columns never reach a real row's state).
         bool ok[2][4];
         bool any = false;
+        if (tile_whole(p, wrow_lo, wrow_hi, t)) {
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+            for (int b = 0; b < 2; ++b)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                ok[b][r] = allowed(p, row, (int64_t)t * kTile + 16 * b + 4 * g + r);
-                any |= ok[b][r];
-            }
+                for (int r = 0; r < 4; ++r)
+                    ok[b][r] = true;
+            any = true;
+        } else {
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    ok[b][r] = allowed(p, row, (int64_t)t * kTile + 16 * b + 4 * g + r);
+                    any |= ok[b][r];
+                }
+        }
         if (__any(any)) {
+            // score chain, the next u-step's K operands read ahead of the MFMAs
             f4 acc[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-            for (int u = 0; u < NU; ++u) {
-                f4 ka[2][2];
+            f4 ka[2][2][2]; // [u parity][b][hh]
+            auto read_k = [&](int u, int sl) {
 #pragma unroll
                 for (int b = 0; b < 2; ++b)
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh) {
                         const int c4 = 8 * u + 2 * g + hh;
-                        ka[b][hh] = *(const f4 *)(ks + (16 * b + col) * DK + 4 * (c4 ^ (col & 7)));
+                        ka[sl][b][hh] =
+                            *(const f4 *)(ks + (16 * b + col) * DK + 4 * (c4 ^ (col & 7)));
                     }
+            };
+            read_k(0, 0);
+#pragma unroll
+            for (int u = 0; u < NU; ++u) {
+                if (u + 1 < NU)
+                    read_k(u + 1, (u + 1) & 1);
 #pragma unroll
                 for (int jj = 0; jj < 8; ++jj)
 #pragma unroll
                     for (int b = 0; b < 2; ++b)
-                        acc[b] = mfma(ka[b][jj >> 2][jj & 3], q[u][jj], acc[b]);
+                        acc[b] = mfma(ka[u & 1][b][jj >> 2][jj & 3], q[u][jj], acc[b]);
             }
+            // the first V operands are read while the softmax runs
+            f4 vb[2][4]; // [half-group parity][r]
+            auto read_v = [&](int hg, int sl) { // half-group hg = 2a + b
+                const int a = hg >> 1, b = hg & 1;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    vb[sl][r] = *(const f4 *)(vs + (16 * b + 4 * g + r) * DK + 64 * a + 4 * col);
+            };
+            read_v(0, 0);
             float s[2][4], pr[2][4];
 #pragma unroll
             for (int b = 0; b < 2; ++b)
@@ -265,20 +318,20 @@ __global__ __launch_bounds__(512) void tiled_kernel(Params p, int split)
             l = __builtin_fmaf(l, alpha, rs);
             m = mn;
 #pragma unroll
-            for (int a = 0; a < NQ; ++a) {
+            for (int hg = 0; hg < 2 * NQ; ++hg) {
+                const int a = hg >> 1, b = hg & 1;
+                if (hg + 1 < 2 * NQ)
+                    read_v(hg + 1, (hg + 1) & 1);
+                if (b == 0) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    O[a][j] = O[a][j] * alpha;
+                    for (int j = 0; j < 4; ++j)
+                        O[a][j] = O[a][j] * alpha;
+                }
 #pragma unroll
-                for (int b = 0; b < 2; ++b)
+                for (int r = 0; r < 4; ++r)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const f4 v = *(const f4 *)(vs + (16 * b + 4 * g + r) * DK + 64 * a +
-                                                   4 * col);
-#pragma unroll
-                        for (int j = 0; j < 4; ++j)
-                            O[a][j] = mfma(v[j], pr[b][r], O[a][j]);
-                    }
+                    for (int j = 0; j < 4; ++j)
+                        O[a][j] = mfma(vb[hg & 1][r][j], pr[b][r], O[a][j]);
             }
             processed = true;
         }
