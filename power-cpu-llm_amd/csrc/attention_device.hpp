@@ -181,6 +181,40 @@ __device__ __forceinline__ bool allowed(const Params &p, int row, int64_t t)
     return kp <= qp && (p.window == 0 || qp - kp < p.window);
 }
 
+// Butterflies across the four 16-lane groups: each lane combined with lane ^
+// 16 or lane ^ 32. The gfx950 permlane swaps exchange 16-lane rows (32-lane
+// halves) between two registers in a few cycles, where a shuffle goes
+// through the LDS unit; given the same value twice, their two results hold
+// every lane's own value and its partner's, and max and + are commutative,
+// so the results equal x op shfl_xor(x, k) bit for bit.
+__device__ __forceinline__ float max_xor16(float x)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                    false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float max_xor32(float x)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                    false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float add_xor16(float x)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                    false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float add_xor32(float x)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                    false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Max of a tile's allowed scores for the lane's row (column lane%16): the
 // lane's eight values, then across the four lane groups.
 __device__ __forceinline__ float tile_max(const float s[2][4], const bool ok[2][4])
@@ -191,8 +225,8 @@ __device__ __forceinline__ float tile_max(const float s[2][4], const bool ok[2][
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             m = ok[b][r] ? fmaxf(m, s[b][r]) : m;
-    m = fmaxf(m, __shfl_xor(m, 16));
-    m = fmaxf(m, __shfl_xor(m, 32));
+    m = max_xor16(m);
+    m = max_xor32(m);
     return m;
 }
 
@@ -209,8 +243,8 @@ __device__ __forceinline__ float tile_probs(const float s[2][4], const bool ok[2
     const float x0 = (p[0][0] + p[0][1]) + (p[0][2] + p[0][3]);
     const float x1 = (p[1][0] + p[1][1]) + (p[1][2] + p[1][3]);
     float x = x0 + x1;
-    x = x + __shfl_xor(x, 16);
-    x = x + __shfl_xor(x, 32);
+    x = add_xor16(x);
+    x = add_xor32(x);
     return x;
 }
 

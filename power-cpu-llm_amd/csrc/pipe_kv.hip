@@ -98,21 +98,27 @@ __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, i
                     q[u][4 * hh + j] = v[j];
             }
     }
-    f4 kb[NU][2]; // the block in flight
-    auto load_k = [&](int t, int b) {
+    // The K piece in flight: 16 keys x PD dims (a whole 16-key block up to
+    // head dim 256, half a block at 512, so a workgroup keeps ~the same bytes
+    // in flight at every head dim).
+    constexpr int PD = DK > 256 ? 256 : DK;
+    constexpr int PU = PD / 32; // u-steps per piece
+    constexpr int PB = DK / PD; // pieces per 16-key block
+    f4 kb[PU][2];
+    auto load_k = [&](int t, int b, int pc) {
         const int64_t key = cbase + t * kTile + 16 * b + col;
         const float *kp = key_row(p, key < klast ? key : klast) + hoff;
 #pragma unroll
-        for (int u = 0; u < NU; ++u)
+        for (int uu = 0; uu < PU; ++uu)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const int d = 32 * u + 8 * g + 4 * h;
+                const int d = 32 * (pc * PU + uu) + 8 * g + 4 * h;
                 const bool din = FULL || d < p.dim;
                 const f4 x = ldg4_stream(kp + (din ? d : 0));
-                kb[u][h] = din ? x : f4{0.f, 0.f, 0.f, 0.f};
+                kb[uu][h] = din ? x : f4{0.f, 0.f, 0.f, 0.f};
             }
     };
-    load_k(0, 0);
+    load_k(0, 0, 0);
     float m = kNegInf;
     bool bad = false;
 #pragma unroll
@@ -129,37 +135,42 @@ __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, i
         const bool tile_any = __any(any);
         f4 acc[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            __builtin_amdgcn_sched_barrier(0);
-            if (tile_any) {
+        for (int b = 0; b < 2; ++b)
 #pragma unroll
-                for (int u = 0; u < NU; ++u) {
-                    float qv[8];
-                    if constexpr (QLDS) {
-                        const f4 qa0 = *(const f4 *)(s.q + col * QLD + 32 * u + 8 * g);
-                        const f4 qa1 = *(const f4 *)(s.q + col * QLD + 32 * u + 8 * g + 4);
+            for (int pc = 0; pc < PB; ++pc) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (tile_any) {
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            qv[j] = qa0[j];
-                            qv[4 + j] = qa1[j];
+                    for (int uu = 0; uu < PU; ++uu) {
+                        const int u = pc * PU + uu;
+                        float qv[8];
+                        if constexpr (QLDS) {
+                            const f4 qa0 = *(const f4 *)(s.q + col * QLD + 32 * u + 8 * g);
+                            const f4 qa1 = *(const f4 *)(s.q + col * QLD + 32 * u + 8 * g + 4);
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) {
+                                qv[j] = qa0[j];
+                                qv[4 + j] = qa1[j];
+                            }
+                        } else {
+#pragma unroll
+                            for (int jj = 0; jj < 8; ++jj)
+                                qv[jj] = q[u][jj];
                         }
-                    } else {
 #pragma unroll
                         for (int jj = 0; jj < 8; ++jj)
-                            qv[jj] = q[u][jj];
+                            acc[b] = mfma(kb[uu][jj >> 2][jj & 3], qv[jj], acc[b]);
                     }
-#pragma unroll
-                    for (int jj = 0; jj < 8; ++jj)
-                        acc[b] = mfma(kb[u][jj >> 2][jj & 3], qv[jj], acc[b]);
                 }
+                __builtin_amdgcn_sched_barrier(0);
+                // the next piece into the registers just consumed
+                if (pc + 1 < PB)
+                    load_k(t, b, pc + 1);
+                else if (b == 0)
+                    load_k(t, 1, 0);
+                else if (t + 1 < kTilesPerChunk)
+                    load_k(t + 1, 0, 0);
             }
-            __builtin_amdgcn_sched_barrier(0);
-            // the next block into the registers just consumed
-            if (b == 0)
-                load_k(t, 1);
-            else if (t + 1 < kTilesPerChunk)
-                load_k(t + 1, 0);
-        }
         float pr[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
         float alpha = 1.f, rs = 0.f;
         if (tile_any) {
