@@ -17,7 +17,9 @@
  *   2. checked wrappers with the reference wrappers' validation and error
  *      codes;
  *   3. a device-resident entry (device pointers, descriptor masks, two KV
- *      segments, asynchronous on a caller-visible stream).
+ *      segments, asynchronous on a caller-visible stream);
+ *   4. a device-resident layer cache whose rows the entry of 3 reads in
+ *      place.
  */
 #ifndef PCL_ATTENTION_H
 #define PCL_ATTENTION_H
@@ -69,6 +71,8 @@ enum pcl_status {
     PCL_INVALID_SHAPE = 1,
     PCL_INVALID_PARAMETER = 2,
     PCL_NON_FINITE_VALUE = 3,
+    /* engine::Error::ResourceLimit: a cache's position or byte limit */
+    PCL_RESOURCE_LIMIT = 4,
 };
 
 /* attention_with (src/kernels/quantized/int8.rs:596-663) over this backend:
@@ -176,6 +180,80 @@ int pcl_attention_resolve_kernel(const pcl_attention_desc *desc);
  * per launch; leave it off in production. */
 int pcl_context_set_timing(pcl_context *ctx, int enable);
 int pcl_context_timing(pcl_context *ctx, double *ms, int64_t *launches);
+
+/* ---- 4. device-resident layer cache ----------------------------------------
+ *
+ * The engine's LayerCache (src/engine/attention.rs:244-311) with its K/V rows
+ * in HBM: token-major [tokens][kvheads][dim] f32, the retained rows
+ * contiguous, so attention reads them in place (no staging copy, unlike
+ * stage(), attention.rs:562-581). All copies run on the context's stream. */
+typedef struct pcl_kv_cache pcl_kv_cache;
+
+/* Undo record of one uncommitted step (PendingKv, attention.rs:263-266);
+ * lengths in tokens. */
+typedef struct pcl_kv_pending {
+    int64_t old_len;
+    int64_t old_total;
+} pcl_kv_pending;
+
+/* new_cache (attention.rs:484-505): rows of kvheads x dim floats, positions
+ * up to `context`, window 0 for a global layer (a sliding layer keeps
+ * window - 1 tokens, retained_count, attention.rs:1166-1168), max_bytes
+ * bounding the retained plus appended K+V bytes of a step. PCL_RESOURCE_LIMIT
+ * when max_bytes is below one token's K+V. */
+int pcl_kv_cache_create(pcl_context *ctx, int64_t kvheads, int64_t dim, int64_t context,
+                        int64_t window, size_t max_bytes, pcl_kv_cache **out);
+void pcl_kv_cache_destroy(pcl_kv_cache *cache);
+/* LayerCache::total_tokens / retained_tokens (attention.rs:268-273). */
+int64_t pcl_kv_cache_total_tokens(const pcl_kv_cache *cache);
+int64_t pcl_kv_cache_retained_tokens(const pcl_kv_cache *cache);
+/* The retained rows (LayerCache::keys / values, attention.rs:274-279) as device
+ * pointers, their count and the absolute position of the first. Valid until
+ * the next append, keep, rollback or commit. */
+int pcl_kv_cache_view(const pcl_kv_cache *cache, const float **keys, const float **values,
+                      int64_t *rows, int64_t *first_position);
+/* Copy retained rows [first, first + rows) of K and V into keys / values
+ * (host or device memory, [rows][kvheads][dim] each) and wait for the copy:
+ * the host-side read of LayerCache::keys / values. */
+int pcl_kv_cache_read(const pcl_kv_cache *cache, int64_t first, int64_t rows, float *keys,
+                      float *values);
+/* One uncommitted step of n tokens (encode_in_place's append,
+ * attention.rs:949-1080): checks total + n <= context and the byte limit
+ * (check_stage, attention.rs:545-558), copies the device rows keys/values
+ * ([n][kvheads][dim]) after the retained rows, advances the total and fills
+ * *pending. On an error the cache is unchanged. */
+int pcl_kv_cache_append(pcl_kv_cache *cache, const float *keys, const float *values, int64_t n,
+                        pcl_kv_pending *pending);
+/* LayerCache::rollback / keep / commit (attention.rs:280-310): undo the step;
+ * keep only its first `tokens` positions; apply window retention (the dead
+ * prefix is dropped once it is at least half the rows). */
+int pcl_kv_cache_rollback(pcl_kv_cache *cache, const pcl_kv_pending *pending);
+int pcl_kv_cache_keep(pcl_kv_cache *cache, const pcl_kv_pending *pending, int64_t tokens);
+int pcl_kv_cache_commit(pcl_kv_cache *cache);
+/* Key/value fields of an attention descriptor over the cache; the caller sets
+ * the query, output and head fields. Encoder pass (after append, before
+ * commit): the retained rows including the step, causal with the cache's
+ * window, first_key = position of the first retained row, first_query =
+ * pending->old_total (encode_in_place's view, attention.rs:978-987). Decoder
+ * pass (DiffusionGemma canvas, decode_routed, attention.rs:1156-1163): the
+ * retained rows then n canvas rows as a second segment, no mask, first_query =
+ * the cache total; the cache is not changed. */
+int pcl_kv_cache_encoder_desc(const pcl_kv_cache *cache, const pcl_kv_pending *pending,
+                              pcl_attention_desc *desc);
+int pcl_kv_cache_decoder_desc(const pcl_kv_cache *cache, const float *canvas_keys,
+                              const float *canvas_values, int64_t n, pcl_attention_desc *desc);
+/* Shared-K/V layer step (encode_shared_in_place, attention.rs:1086-1145): the
+ * layer stores no K/V and attends over its source layer's rows of the same
+ * uncommitted step. shared_desc checks cache total == source_pending->old_total
+ * and source total == cache total + n, and fills the key/value fields: the
+ * source's retained rows, causal with this cache's window, first_key =
+ * source_pending->old_total - the rows the source retained before its step,
+ * first_query = the cache total. advance records *pending and moves the
+ * total to total + n (keep / rollback / commit apply as for any step). */
+int pcl_kv_cache_shared_desc(const pcl_kv_cache *cache, const pcl_kv_cache *source,
+                             const pcl_kv_pending *source_pending, int64_t n,
+                             pcl_attention_desc *desc);
+int pcl_kv_cache_advance(pcl_kv_cache *cache, int64_t n, pcl_kv_pending *pending);
 
 /* Library identification (for loaders). */
 const char *pcl_version(void);

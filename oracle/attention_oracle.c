@@ -256,6 +256,120 @@ size_t oracle_retained_count(size_t count, size_t window, int has_window)
     return count < keep ? count : keep;
 }
 
+/* ---- layer cache ------------------------------------------------------- */
+
+/* new_cache (src/engine/attention.rs:484-505). */
+int oracle_cache_init(oracle_layer_cache *c, size_t kv_heads, size_t head_dim, size_t context,
+                      size_t window, int has_window, size_t max_bytes)
+{
+    memset(c, 0, sizeof(*c));
+    if (kv_heads == 0 || head_dim == 0 || kv_heads > SIZE_MAX / head_dim)
+        return ORACLE_INVALID_SHAPE;
+    const size_t width = kv_heads * head_dim;
+    if (width > SIZE_MAX / (2 * sizeof(float)))
+        return ORACLE_RESOURCE_LIMIT;
+    if (max_bytes < width * 2 * sizeof(float))
+        return ORACLE_RESOURCE_LIMIT;
+    c->width = width;
+    c->context = context;
+    c->window = window;
+    c->has_window = has_window;
+    c->max_bytes = max_bytes;
+    return ORACLE_OK;
+}
+
+void oracle_cache_free(oracle_layer_cache *c)
+{
+    free(c->keys);
+    free(c->values);
+    c->keys = c->values = NULL;
+    c->len = c->cap = 0;
+}
+
+/* retained_tokens (attention.rs:271-273). */
+size_t oracle_cache_retained(const oracle_layer_cache *c)
+{
+    return (c->len - c->start) / c->width;
+}
+
+/* try_reserve: room for `extra` more floats after len. */
+static int oracle_cache_reserve(oracle_layer_cache *c, size_t extra)
+{
+    if (c->len + extra <= c->cap)
+        return ORACLE_OK;
+    const size_t cap = c->len + extra;
+    float *k = realloc(c->keys, cap * sizeof(float));
+    if (!k)
+        return ORACLE_RESOURCE_LIMIT;
+    c->keys = k;
+    float *v = realloc(c->values, cap * sizeof(float));
+    if (!v)
+        return ORACLE_RESOURCE_LIMIT;
+    c->values = v;
+    c->cap = cap;
+    return ORACLE_OK;
+}
+
+/* check_stage's limits (attention.rs:542-559) and encode_in_place's append
+ * (attention.rs:956-980, 1070-1073). */
+int oracle_cache_append(oracle_layer_cache *c, const float *keys, const float *values, size_t n,
+                        size_t *old_len, size_t *old_total)
+{
+    if (n == 0)
+        return ORACLE_INVALID_SHAPE; /* "hidden-state rows" */
+    if (c->total > SIZE_MAX - n || c->total + n > c->context)
+        return ORACLE_RESOURCE_LIMIT;
+    const size_t next_position = c->total + n;
+    const size_t count = oracle_cache_retained(c) + n;
+    if (count > SIZE_MAX / c->width)
+        return ORACLE_RESOURCE_LIMIT;
+    const size_t cells = count * c->width;
+    if (cells > SIZE_MAX / (2 * sizeof(float)) || cells * 2 * sizeof(float) > c->max_bytes)
+        return ORACLE_RESOURCE_LIMIT;
+    *old_len = c->len;
+    *old_total = c->total;
+    const size_t extra = cells - (c->len - c->start);
+    if (oracle_cache_reserve(c, extra) != ORACLE_OK)
+        return ORACLE_RESOURCE_LIMIT;
+    memcpy(c->keys + c->len, keys, n * c->width * sizeof(float));
+    memcpy(c->values + c->len, values, n * c->width * sizeof(float));
+    c->len += n * c->width;
+    c->total = next_position;
+    return ORACLE_OK;
+}
+
+/* LayerCache::rollback (attention.rs:280-285). */
+void oracle_cache_rollback(oracle_layer_cache *c, size_t old_len, size_t old_total)
+{
+    if (old_len < c->len)
+        c->len = old_len;
+    c->total = old_total;
+}
+
+/* LayerCache::keep (attention.rs:286-296). */
+void oracle_cache_keep(oracle_layer_cache *c, size_t old_len, size_t old_total, size_t tokens)
+{
+    const size_t len = old_len + tokens * c->width;
+    if (len < c->len)
+        c->len = len;
+    c->total = old_total + tokens;
+}
+
+/* LayerCache::commit (attention.rs:297-310): window retention, then the dead
+ * prefix drained once it is at least half the buffer. */
+void oracle_cache_commit(oracle_layer_cache *c)
+{
+    const size_t count = (c->len - c->start) / c->width;
+    const size_t keep = oracle_retained_count(count, c->window, c->has_window);
+    c->start += (count - keep) * c->width;
+    if (c->start > 0 && c->start * 2 >= c->len) {
+        memmove(c->keys, c->keys + c->start, (c->len - c->start) * sizeof(float));
+        memmove(c->values, c->values + c->start, (c->len - c->start) * sizeof(float));
+        c->len -= c->start;
+        c->start = 0;
+    }
+}
+
 /* ---- threaded CPU baseline (the engine's decomposition) ---------------- */
 
 struct job {

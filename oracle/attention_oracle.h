@@ -82,6 +82,41 @@ int oracle_encoder_mask(size_t first_key, size_t count, size_t query, size_t win
 /* a10 — retained_count (src/engine/attention.rs:1166-1168). */
 size_t oracle_retained_count(size_t count, size_t window, int has_window);
 
+/* Layer cache — LayerCache (src/engine/attention.rs:244-311) with the
+ * K/V half of encode_in_place (attention.rs:949-1080): token-major f32
+ * rows, lengths and `start` in floats as the engine keeps them. */
+enum { ORACLE_RESOURCE_LIMIT = 4 }; /* engine::Error::ResourceLimit */
+typedef struct oracle_layer_cache {
+    size_t width;      /* kv_heads * head_dim */
+    size_t context;    /* ModelSpec::context */
+    size_t window;     /* sliding window when has_window */
+    int has_window;
+    size_t max_bytes;  /* bound of one staged K+V pair */
+    size_t total;      /* positions processed */
+    size_t start;      /* first retained float */
+    size_t len;        /* floats in keys / values */
+    size_t cap;        /* floats allocated */
+    float *keys, *values;
+} oracle_layer_cache;
+
+/* new_cache (attention.rs:484-505). ORACLE_RESOURCE_LIMIT when max_bytes is
+ * below one token's K+V. */
+int oracle_cache_init(oracle_layer_cache *c, size_t kv_heads, size_t head_dim, size_t context,
+                      size_t window, int has_window, size_t max_bytes);
+void oracle_cache_free(oracle_layer_cache *c);
+/* retained_tokens (attention.rs:271-273). */
+size_t oracle_cache_retained(const oracle_layer_cache *c);
+/* encode_in_place's K/V step: check_stage's position and byte limits
+ * (attention.rs:542-559), then the rows appended after the retained ones and
+ * total = next position; fills the PendingKv record (old_len in floats). On
+ * an error the cache is unchanged. */
+int oracle_cache_append(oracle_layer_cache *c, const float *keys, const float *values, size_t n,
+                        size_t *old_len, size_t *old_total);
+/* rollback / keep / commit (attention.rs:280-310). */
+void oracle_cache_rollback(oracle_layer_cache *c, size_t old_len, size_t old_total);
+void oracle_cache_keep(oracle_layer_cache *c, size_t old_len, size_t old_total, size_t tokens);
+void oracle_cache_commit(oracle_layer_cache *c);
+
 /* CPU baseline: the exact (a1) or binary32 (a3) path threaded as the engine
  * threads it (src/engine/attention.rs:755-836): one query's heads split
  * into ceil(qheads/split) ranges with split = clamp(workers/queries, 1,

@@ -136,3 +136,85 @@ def threaded(query, nq, keys, values, qheads, kvheads, dim, nkeys, causal, first
                                        kvheads, dim, nkeys, int(causal), first_key, first_query,
                                        window, _f(out))
     return bool(ok), out
+
+
+class _CacheStruct(ctypes.Structure):
+    _fields_ = [("width", ctypes.c_size_t), ("context", ctypes.c_size_t),
+                ("window", ctypes.c_size_t), ("has_window", ctypes.c_int),
+                ("max_bytes", ctypes.c_size_t), ("total", ctypes.c_size_t),
+                ("start", ctypes.c_size_t), ("len", ctypes.c_size_t), ("cap", ctypes.c_size_t),
+                ("keys", ctypes.POINTER(ctypes.c_float)),
+                ("values", ctypes.POINTER(ctypes.c_float))]
+
+
+def _cache_lib():
+    lib = load()
+    if not getattr(lib, "_cache_bound", False):
+        cp, sz = ctypes.POINTER(_CacheStruct), ctypes.c_size_t
+        fp, szp = ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_size_t)
+        for name, res, args in (
+                ("oracle_cache_init", ctypes.c_int, [cp, sz, sz, sz, sz, ctypes.c_int, sz]),
+                ("oracle_cache_free", None, [cp]),
+                ("oracle_cache_retained", sz, [cp]),
+                ("oracle_cache_append", ctypes.c_int, [cp, fp, fp, sz, szp, szp]),
+                ("oracle_cache_rollback", None, [cp, sz, sz]),
+                ("oracle_cache_keep", None, [cp, sz, sz, sz]),
+                ("oracle_cache_commit", None, [cp])):
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        lib._cache_bound = True
+    return lib
+
+
+class OracleCache:
+    """The LayerCache restatement (oracle_cache_*). Pending records are
+    (old_len, old_total) with old_len in floats, as the engine keeps them."""
+
+    def __init__(self, kv_heads, head_dim, context, window, max_bytes):
+        self.lib = _cache_lib()
+        self.c = _CacheStruct()
+        self.status = self.lib.oracle_cache_init(ctypes.byref(self.c), kv_heads, head_dim,
+                                                 context, window or 0, int(window is not None),
+                                                 max_bytes)
+
+    def __del__(self):
+        try:
+            self.lib.oracle_cache_free(ctypes.byref(self.c))
+        except Exception:
+            pass
+
+    @property
+    def total(self):
+        return self.c.total
+
+    def retained(self):
+        return int(self.lib.oracle_cache_retained(ctypes.byref(self.c)))
+
+    def first_position(self):
+        return self.c.total - self.retained()
+
+    def rows(self):
+        """(keys, values) of the retained rows, [retained][width] copies."""
+        w, s, n = self.c.width, self.c.start, self.c.len
+        if n == s:
+            return np.zeros((0, w), np.float32), np.zeros((0, w), np.float32)
+        k = np.ctypeslib.as_array(self.c.keys, shape=(n,))[s:].reshape(-1, w).copy()
+        v = np.ctypeslib.as_array(self.c.values, shape=(n,))[s:].reshape(-1, w).copy()
+        return k, v
+
+    def append(self, keys, values, n):
+        k, v = _f32(keys), _f32(values)
+        old_len, old_total = ctypes.c_size_t(), ctypes.c_size_t()
+        rc = self.lib.oracle_cache_append(ctypes.byref(self.c), _f(k), _f(v), n,
+                                          ctypes.byref(old_len), ctypes.byref(old_total))
+        return rc, (old_len.value, old_total.value)
+
+    def rollback(self, pending):
+        self.lib.oracle_cache_rollback(ctypes.byref(self.c), pending[0], pending[1])
+
+    def keep(self, pending, tokens):
+        self.lib.oracle_cache_keep(ctypes.byref(self.c), pending[0], pending[1], tokens)
+
+    def commit(self):
+        self.lib.oracle_cache_commit(ctypes.byref(self.c))

@@ -13,6 +13,9 @@ error behaviour:
   Context
       the device-resident entry: device pointers, descriptor masks, two KV
       segments, launches on a stream.
+  LayerCache
+      the engine's LayerCache (src/engine/attention.rs:244-311) with its K/V
+      rows in device memory, producing attention descriptors over them.
 
 There is no CPU fallback: without the built library every entry raises.
 """
@@ -24,9 +27,9 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libpcl_attention.so")
 
-OK, INVALID_SHAPE, INVALID_PARAMETER, NON_FINITE_VALUE = 0, 1, 2, 3
+OK, INVALID_SHAPE, INVALID_PARAMETER, NON_FINITE_VALUE, RESOURCE_LIMIT = 0, 1, 2, 3, 4
 ERROR_NAMES = {INVALID_SHAPE: "InvalidShape", INVALID_PARAMETER: "InvalidParameter",
-               NON_FINITE_VALUE: "NonFiniteValue"}
+               NON_FINITE_VALUE: "NonFiniteValue", RESOURCE_LIMIT: "ResourceLimit"}
 (KERNEL_AUTO, KERNEL_SPLIT_KV, KERNEL_TILED, KERNEL_TILED_SPLIT, KERNEL_PIPE_KV,
  KERNEL_TWO_PASS) = 0, 1, 2, 3, 4, 5
 KERNEL_NAMES = {KERNEL_SPLIT_KV: "split_kv", KERNEL_TILED: "tiled",
@@ -50,13 +53,27 @@ EXPORTS = (
     "pcl_attention_resolve_kernel",
     "pcl_context_set_timing",
     "pcl_context_timing",
+    "pcl_kv_cache_create",
+    "pcl_kv_cache_destroy",
+    "pcl_kv_cache_total_tokens",
+    "pcl_kv_cache_retained_tokens",
+    "pcl_kv_cache_view",
+    "pcl_kv_cache_read",
+    "pcl_kv_cache_append",
+    "pcl_kv_cache_rollback",
+    "pcl_kv_cache_keep",
+    "pcl_kv_cache_commit",
+    "pcl_kv_cache_encoder_desc",
+    "pcl_kv_cache_decoder_desc",
+    "pcl_kv_cache_shared_desc",
+    "pcl_kv_cache_advance",
     "pcl_version",
 )
 
 
 class AttentionError(Exception):
     """kernels::reference::Error: kind is InvalidShape, InvalidParameter or
-    NonFiniteValue."""
+    NonFiniteValue; the layer cache adds engine::Error::ResourceLimit."""
 
     def __init__(self, code):
         self.code = code
@@ -79,6 +96,11 @@ class PclDesc(ctypes.Structure):
         ("out", ctypes.c_void_p), ("o_stride", ctypes.c_int64),
         ("kernel", ctypes.c_int32),
     ]
+
+
+class PclPending(ctypes.Structure):
+    """pcl_kv_pending (PendingKv, src/engine/attention.rs:263-266), in tokens."""
+    _fields_ = [("old_len", ctypes.c_int64), ("old_total", ctypes.c_int64)]
 
 
 _lib = None
@@ -141,6 +163,29 @@ def load():
     lib.pcl_context_timing.restype = ctypes.c_int
     lib.pcl_context_timing.argtypes = [vp, ctypes.POINTER(ctypes.c_double),
                                        ctypes.POINTER(ctypes.c_int64)]
+    i64, i64p = ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)
+    pend = ctypes.POINTER(PclPending)
+    dp = ctypes.POINTER(PclDesc)
+    for name, res, args in (
+            ("pcl_kv_cache_create", ctypes.c_int, [vp, i64, i64, i64, i64, sz,
+                                                   ctypes.POINTER(vp)]),
+            ("pcl_kv_cache_destroy", None, [vp]),
+            ("pcl_kv_cache_total_tokens", i64, [vp]),
+            ("pcl_kv_cache_retained_tokens", i64, [vp]),
+            ("pcl_kv_cache_view", ctypes.c_int, [vp, ctypes.POINTER(vp), ctypes.POINTER(vp),
+                                                 i64p, i64p]),
+            ("pcl_kv_cache_read", ctypes.c_int, [vp, i64, i64, vp, vp]),
+            ("pcl_kv_cache_append", ctypes.c_int, [vp, vp, vp, i64, pend]),
+            ("pcl_kv_cache_rollback", ctypes.c_int, [vp, pend]),
+            ("pcl_kv_cache_keep", ctypes.c_int, [vp, pend, i64]),
+            ("pcl_kv_cache_commit", ctypes.c_int, [vp]),
+            ("pcl_kv_cache_encoder_desc", ctypes.c_int, [vp, pend, dp]),
+            ("pcl_kv_cache_decoder_desc", ctypes.c_int, [vp, vp, vp, i64, dp]),
+            ("pcl_kv_cache_shared_desc", ctypes.c_int, [vp, vp, pend, i64, dp]),
+            ("pcl_kv_cache_advance", ctypes.c_int, [vp, i64, pend])):
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
     lib.pcl_version.restype = ctypes.c_char_p
     lib.pcl_version.argtypes = []
     _lib = lib
@@ -338,3 +383,106 @@ class Context:
         if rc != OK:
             raise AttentionError(rc)
         return err.value
+
+
+class LayerCache:
+    """LayerCache (src/engine/attention.rs:244-311) with its K/V in device
+    memory: token-major [tokens][kv_heads][head_dim] f32 rows on the
+    context's device, copies on the context's stream. Methods keep the
+    engine's names; append() is the K/V half of encode_in_place
+    (attention.rs:949-1080) and returns the PendingKv record that rollback,
+    keep and the descriptors take. Limits raise AttentionError
+    ("ResourceLimit") as check_stage does (attention.rs:507-560)."""
+
+    def __init__(self, ctx, kv_heads, head_dim, context, window, max_bytes):
+        self.ctx = ctx
+        self.lib = ctx.lib
+        self.kv_heads, self.head_dim = int(kv_heads), int(head_dim)
+        self.handle = ctypes.c_void_p()
+        rc = self.lib.pcl_kv_cache_create(ctx.handle, self.kv_heads, self.head_dim,
+                                          int(context), int(window or 0), int(max_bytes),
+                                          ctypes.byref(self.handle))
+        if rc != OK:
+            raise AttentionError(rc)
+
+    def close(self):
+        if self.handle:
+            self.lib.pcl_kv_cache_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc):
+        if rc != OK:
+            raise AttentionError(rc)
+
+    def total_tokens(self):
+        return self.lib.pcl_kv_cache_total_tokens(self.handle)
+
+    def retained_tokens(self):
+        return self.lib.pcl_kv_cache_retained_tokens(self.handle)
+
+    def view(self):
+        """(keys_ptr, values_ptr, rows, first_position) of the retained rows."""
+        k, v = ctypes.c_void_p(), ctypes.c_void_p()
+        rows, first = ctypes.c_int64(), ctypes.c_int64()
+        self._check(self.lib.pcl_kv_cache_view(self.handle, ctypes.byref(k), ctypes.byref(v),
+                                               ctypes.byref(rows), ctypes.byref(first)))
+        return k.value or 0, v.value or 0, rows.value, first.value
+
+    def read(self, first, rows):
+        """Retained rows [first, first+rows) of K and V as host arrays."""
+        width = self.kv_heads * self.head_dim
+        keys = np.zeros(max(rows * width, 1), np.float32)
+        values = np.zeros(max(rows * width, 1), np.float32)
+        self._check(self.lib.pcl_kv_cache_read(self.handle, int(first), int(rows),
+                                               keys.ctypes.data, values.ctypes.data))
+        return keys[:rows * width], values[:rows * width]
+
+    def append(self, keys_ptr, values_ptr, n):
+        pending = PclPending()
+        self._check(self.lib.pcl_kv_cache_append(self.handle, ctypes.c_void_p(keys_ptr),
+                                                 ctypes.c_void_p(values_ptr), int(n),
+                                                 ctypes.byref(pending)))
+        return pending
+
+    def advance(self, n):
+        """A shared-K/V layer's step (encode_shared_in_place's position move)."""
+        pending = PclPending()
+        self._check(self.lib.pcl_kv_cache_advance(self.handle, int(n), ctypes.byref(pending)))
+        return pending
+
+    def rollback(self, pending):
+        self._check(self.lib.pcl_kv_cache_rollback(self.handle, ctypes.byref(pending)))
+
+    def keep(self, pending, tokens):
+        self._check(self.lib.pcl_kv_cache_keep(self.handle, ctypes.byref(pending), int(tokens)))
+
+    def commit(self):
+        self._check(self.lib.pcl_kv_cache_commit(self.handle))
+
+    def encoder_desc(self, pending, **kw):
+        """Descriptor of the encoder pass of the step `pending`; kw sets the
+        query, output and head fields."""
+        d = Context.desc(**kw)
+        self._check(self.lib.pcl_kv_cache_encoder_desc(self.handle, ctypes.byref(pending),
+                                                       ctypes.byref(d)))
+        return d
+
+    def decoder_desc(self, canvas_keys_ptr, canvas_values_ptr, n, **kw):
+        d = Context.desc(**kw)
+        self._check(self.lib.pcl_kv_cache_decoder_desc(
+            self.handle, ctypes.c_void_p(canvas_keys_ptr or None),
+            ctypes.c_void_p(canvas_values_ptr or None), int(n), ctypes.byref(d)))
+        return d
+
+    def shared_desc(self, source, source_pending, n, **kw):
+        d = Context.desc(**kw)
+        self._check(self.lib.pcl_kv_cache_shared_desc(self.handle, source.handle,
+                                                      ctypes.byref(source_pending), int(n),
+                                                      ctypes.byref(d)))
+        return d
