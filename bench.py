@@ -48,6 +48,12 @@ WORKLOADS = {
     "prefill_4k_window1024": (16, 8, 256, 4096, 4096, True, 1024, 0, "prefill", False),
     "prefill_4k": (16, 8, 256, 4096, 4096, True, 0, 0, "prefill", False),
     "canvas_256x2304": (16, 8, 256, 256, 2304, False, 0, 2048, "canvas", False),
+    # speculative verification (encode_speculative: the previous token and 7
+    # drafts, causal over the cache and themselves)
+    "verify_32k_q8": (16, 8, 256, 8, 32768, True, 0, 32760, "decode", False),
+    # one decode step through the device-resident layer cache: append the
+    # token's K/V row, attend over the 32K cache in place, roll back
+    "decode_32k_cache": (16, 8, 256, 1, 32768, True, 0, 32767, "cache", False),
 }
 HEADLINE = "decode_32k"
 
@@ -86,7 +92,7 @@ def work(name):
     # decode bytes: attended K and V rows of every KV head, plus Q and O
     if causal:
         lo = max(0, fq - window + 1) if window else 0
-        attended = min(fq, nkeys - 1) - lo + 1
+        attended = min(fq + nq - 1, nkeys - 1) - lo + 1
     else:
         attended = nkeys
     bytes_ = 4 * (2 * attended * kvh * dim + 2 * nq * qh * dim)
@@ -136,6 +142,8 @@ def time_workload(torch, pcl, ctx, name, steps, warmup, seed=0, kernel=0):
     qh, kvh, dim, nq, nkeys, causal, window, fq, kind, _ = WORKLOADS[name]
     set_bytes = 4 * (2 * nkeys * kvh * dim + 2 * nq * qh * dim)
     nsets = max(2, min(MAX_SETS, -(-CYCLE_BYTES // set_bytes)))
+    if kind == "cache":
+        return time_cache_workload(torch, pcl, ctx, name, steps, warmup, nsets, seed)
     sets = []
     for i in range(nsets):
         q, k, v = make_inputs(torch, name, seed + 1000 * i)
@@ -177,6 +185,66 @@ def time_workload(torch, pcl, ctx, name, steps, warmup, seed=0, kernel=0):
     roles = {"stream_ms": ms_stream / max(n_stream, 1),
              "combine_ms": ms_comb / n_comb if n_comb else 0.0}
     host = sets[(steps - 1) % nsets][0]
+    return ev, wall, kernel, host, roles, nsets
+
+
+def time_cache_workload(torch, pcl, ctx, name, steps, warmup, nsets, seed):
+    """Decode steps through pcl.LayerCache: per step, append one token's K/V
+    (device rows) after nkeys-1 cached rows, attend over the cache's rows in
+    place (its encoder descriptor), roll the step back. Each input set is
+    its own cache."""
+    qh, kvh, dim, nq, nkeys, causal, window, fq, kind, _ = WORKLOADS[name]
+    sets = []
+    for i in range(nsets):
+        q, k, v = make_inputs(torch, name, seed + 1000 * i)
+        cache = pcl.LayerCache(ctx, kvh, dim, nkeys + 1, window, 1 << 40)
+        cache.append(k.data_ptr(), v.data_ptr(), nkeys - 1)
+        cache.commit()
+        out = torch.empty((nq, qh, dim), device="cuda:0", dtype=torch.float32)
+        kt, vt = k[nkeys - 1:].clone(), v[nkeys - 1:].clone()
+        sets.append(({"q": q, "k": k, "v": v, "out": out, "kt": kt, "vt": vt}, cache))
+    torch.cuda.synchronize()
+
+    def step(i):
+        host, cache = sets[i % nsets]
+        pending = cache.append(host["kt"].data_ptr(), host["vt"].data_ptr(), 1)
+        d = cache.encoder_desc(pending, q=host["q"].data_ptr(), q_stride=qh * dim, nq=nq,
+                               qheads=qh, kh_first=0, kh_end=kvh, out=host["out"].data_ptr(),
+                               o_stride=qh * dim)
+        ctx.launch(d)
+        cache.rollback(pending)
+        return d
+
+    d0 = step(0)
+    ctx.reserve(ctx.workspace_bytes(d0))
+    kernel = pcl.KERNEL_NAMES.get(ctx.resolve_kernel(d0), "?")
+    for i in range(max(warmup, nsets)):
+        step(i)
+    torch.cuda.synchronize()
+    if ctx.sync() != 0:
+        raise RuntimeError("device error flag set for %s" % name)
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for i in range(steps):
+        step(i)
+    stop.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    ev = start.elapsed_time(stop) / steps
+    if ctx.sync():
+        raise RuntimeError("device error flag set for %s" % name)
+    ctx.set_timing(True)
+    for i in range(steps):
+        step(i)
+    (ms_stream, ms_comb), (n_stream, n_comb) = ctx.timing()
+    ctx.set_timing(False)
+    roles = {"stream_ms": ms_stream / max(n_stream, 1),
+             "combine_ms": ms_comb / n_comb if n_comb else 0.0}
+    host = sets[(steps - 1) % nsets][0]
+    for _, cache in sets:
+        cache.close()
     return ev, wall, kernel, host, roles, nsets
 
 
@@ -252,7 +320,7 @@ def main():
              "algorithmic_bytes": bytes_, "algorithmic_flops": flops}
         r["GB/s"] = bytes_ / (ev * 1e-3) / 1e9
         r["TFLOP/s"] = flops / (ev * 1e-3) / 1e12
-        if kind == "decode":
+        if kind in ("decode", "cache"):
             r["frac_hbm"] = r["GB/s"] / HBM_PEAK_GBS
         else:
             r["frac_mfma"] = r["TFLOP/s"] / FP32_MFMA_PEAK_TFS

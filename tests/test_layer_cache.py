@@ -376,3 +376,53 @@ def test_shared_kv_layer_attends_over_its_source_step(pcl, torch, ctx, oracle):
     assert shared.total_tokens() == 8 and source.total_tokens() == 8
     shared.close()
     source.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("nq,window", [(8, 0), (5, 0), (16, 1024), (2, 0)])
+def test_speculative_verify_over_a_long_cache(pcl, torch, ctx, oracle, nq, window):
+    # encode_speculative (text.rs:709-797): the previous token and its drafts
+    # appended to a 32K cache, causal attention of those positions over the
+    # cache and themselves, then keep(accepted) and commit; every kernel gives
+    # the same bits, within 1e-4 of the exact oracle
+    qheads, kvh, dim, cached = 16, 8, 256, 32760
+    width = kvh * dim
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(0x5EED0900 + nq)
+    k = torch.randn((cached + nq, width), generator=g, device="cuda:0")
+    v = torch.randn((cached + nq, width), generator=g, device="cuda:0")
+    q = torch.randn((nq, qheads * dim), generator=g, device="cuda:0") * (1.0 / 16.0)
+    cache = pcl.LayerCache(ctx, kvh, dim, 40000, window or None, 1 << 32)
+    cache.append(k.data_ptr(), v.data_ptr(), cached)
+    cache.commit()
+    pending = cache.append(k[cached:].data_ptr(), v[cached:].data_ptr(), nq)
+    outs = {}
+    for kernel in (0, 1, 2, 4, 5):
+        out = torch.full((nq, qheads * dim), float("nan"), device="cuda:0")
+        d = cache.encoder_desc(pending, q=q.data_ptr(), q_stride=qheads * dim, nq=nq,
+                               qheads=qheads, kh_first=0, kh_end=kvh, out=out.data_ptr(),
+                               o_stride=qheads * dim, kernel=kernel)
+        if kernel == 0:
+            assert ctx.resolve_kernel(d) in (pcl.KERNEL_SPLIT_KV, pcl.KERNEL_PIPE_KV)
+        ctx.reserve(ctx.workspace_bytes(d))
+        ctx.launch(d)
+        assert ctx.sync() == 0
+        outs[kernel] = out.cpu().numpy()
+    for kernel in outs:
+        assert np.array_equal(outs[kernel].view(np.uint32), outs[0].view(np.uint32)), kernel
+    _, _, rows, first = cache.view()
+    kn, vn = k[cached + nq - rows:].cpu().numpy(), v[cached + nq - rows:].cpu().numpy()
+    ok, want = oracle.threaded(q.cpu().numpy(), nq, kn, vn, qheads, kvh, dim, rows, True, first,
+                               cached, window, threads=8)
+    assert ok
+    got = outs[0].reshape(-1)
+    assert float(np.max(np.abs(got - want))) <= 1e-4
+    # accept the first half of the drafts: later positions are gone
+    accepted = max(1, nq // 2)
+    cache.keep(pending, accepted)
+    cache.commit()
+    assert cache.total_tokens() == cached + accepted
+    keys, _, first = read_rows(cache, width)
+    assert first == cache.total_tokens() - keys.shape[0]
+    assert np.array_equal(keys[-1], k[cached + accepted - 1].cpu().numpy())
+    cache.close()
