@@ -19,7 +19,8 @@
  *   3. a device-resident entry (device pointers, descriptor masks, two KV
  *      segments, asynchronous on a caller-visible stream);
  *   4. a device-resident layer cache whose rows the entry of 3 reads in
- *      place.
+ *      place;
+ *   5. the head transform that prepares Q, K and V rows for 3 and 4.
  */
 #ifndef PCL_ATTENTION_H
 #define PCL_ATTENTION_H
@@ -203,6 +204,7 @@ typedef struct pcl_kv_pending {
  * when max_bytes is below one token's K+V. */
 int pcl_kv_cache_create(pcl_context *ctx, int64_t kvheads, int64_t dim, int64_t context,
                         int64_t window, size_t max_bytes, pcl_kv_cache **out);
+/* Destroy caches (and head transforms) before the context they were made on. */
 void pcl_kv_cache_destroy(pcl_kv_cache *cache);
 /* LayerCache::total_tokens / retained_tokens (attention.rs:268-273). */
 int64_t pcl_kv_cache_total_tokens(const pcl_kv_cache *cache);
@@ -254,6 +256,50 @@ int pcl_kv_cache_shared_desc(const pcl_kv_cache *cache, const pcl_kv_cache *sour
                              const pcl_kv_pending *source_pending, int64_t n,
                              pcl_attention_desc *desc);
 int pcl_kv_cache_advance(pcl_kv_cache *cache, int64_t n, pcl_kv_pending *pending);
+
+/* ---- 5. head transform (the attention prologue) ----------------------------
+ *
+ * HeadTransform (src/engine/attention.rs:51-243) on the device: per head an
+ * RMS norm with a sequential f64 sum of squares (p9_ref_rms_norm,
+ * src/kernels/portable/reference.rs:11-33), the learned scale for Q and K,
+ * then NeoX rotation of pairs (j, j + dim/2) by f32 angles
+ * position * (1 / powf(base, 2j/dim)) / factor_j (p9_ref_rope,
+ * reference.rs:277-318); V is normalised without scale and not rotated.
+ * Row layouts: raw and prepared Q [n][qheads][dim], K and V [n][kvheads][dim],
+ * device pointers; token i is at position `position + i`. Launches are
+ * asynchronous on the context's stream; a non-finite input or output sets
+ * bit 2 of the context's device error flag (pcl_context_sync). */
+typedef struct pcl_head_transform pcl_head_transform;
+
+/* HeadTransform::new (attention.rs:65-101): scales [dim] and factors NULL or
+ * [dim/2] are host arrays, copied. sliding != 0: the layer needs a V
+ * projection; otherwise raw_v NULL means V = the raw K (global K-as-V,
+ * attention.rs:121-129). PCL_INVALID_SHAPE for a head geometry this backend
+ * does not run (dim 16, 32, 64, 128, 256 or 512); PCL_INVALID_PARAMETER for a
+ * non-finite or non-positive epsilon, base or factor, or a non-finite scale. */
+int pcl_head_transform_create(pcl_context *ctx, int64_t qheads, int64_t kvheads, int64_t dim,
+                              int sliding, const float *query_scale, const float *key_scale,
+                              float epsilon, float base, const float *factors,
+                              pcl_head_transform **out);
+void pcl_head_transform_destroy(pcl_head_transform *transform);
+/* HeadTransform::prepare (attention.rs:102-156) for n tokens. The rotation
+ * table is built on the host (the C library's powf and sincosf) for positions
+ * up to the largest seen so far and kept on the device; PCL_NON_FINITE_VALUE
+ * for a non-finite angle, PCL_RESOURCE_LIMIT beyond 2^24 positions. */
+int pcl_head_transform_prepare(pcl_head_transform *transform, const float *raw_q,
+                               const float *raw_k, const float *raw_v, int64_t n,
+                               int64_t position, float *q_out, float *k_out, float *v_out);
+/* prepare_query (attention.rs:223-242): the query half, for shared-K/V
+ * layers. */
+int pcl_head_transform_query(pcl_head_transform *transform, const float *raw_q, int64_t n,
+                             int64_t position, float *q_out);
+/* encode_in_place's projection tail (project_tokens, attention.rs:584-666)
+ * fused with the cache append: prepared K and V go straight into the cache's
+ * rows after the retained ones, at positions total .. total+n-1, and the
+ * prepared queries into q_out. Limits and *pending as pcl_kv_cache_append. */
+int pcl_kv_cache_append_transformed(pcl_kv_cache *cache, pcl_head_transform *transform,
+                                    const float *raw_q, const float *raw_k, const float *raw_v,
+                                    int64_t n, float *q_out, pcl_kv_pending *pending);
 
 /* Library identification (for loaders). */
 const char *pcl_version(void);

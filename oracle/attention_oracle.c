@@ -370,6 +370,102 @@ void oracle_cache_commit(oracle_layer_cache *c)
     }
 }
 
+/* ---- head transform primitives ----------------------------------------- */
+
+/* p9_ref_rms_norm (src/kernels/portable/reference.rs:11-33). */
+void oracle_rms_norm(const float *x, const float *scale, size_t n, float eps, float *out)
+{
+    double sum = 0.0;
+    for (size_t i = 0; i < n; ++i)
+        sum += (double)x[i] * (double)x[i];
+    const double inv = 1.0 / sqrt(sum / (double)n + (double)eps);
+    for (size_t i = 0; i < n; ++i) {
+        const float normed = (float)((double)x[i] * inv);
+        out[i] = scale ? normed * scale[i] : normed;
+    }
+}
+
+/* p9_ref_rope (reference.rs:277-318). */
+bool oracle_rope(const float *x, size_t heads, size_t dim, size_t position, float base,
+                 const float *factors, float *out)
+{
+    const size_t half = dim / 2;
+    for (size_t i = 0; i < half; ++i) {
+        float inv = 1.0f / powf(base, (2.0f * (float)i) / (float)dim);
+        if (factors)
+            inv /= factors[i];
+        const float angle = (float)position * inv;
+        if (!isfinite(angle))
+            return false;
+        float s, c;
+        sincosf(angle, &s, &c);
+        for (size_t h = 0; h < heads; ++h) {
+            const size_t a = h * dim + i, b = h * dim + i + half;
+            const float xa = x[a], xb = x[b];
+            out[a] = xa * c - xb * s;
+            out[b] = xb * c + xa * s;
+        }
+    }
+    return true;
+}
+
+static uint64_t fnv(uint64_t h, uint64_t v)
+{
+    return (h ^ v) * 0x100000001b3ULL;
+}
+
+static float from_bits(uint32_t b)
+{
+    float x;
+    memcpy(&x, &b, 4);
+    return x;
+}
+
+/* bits of r; a NaN generated from non-NaN inputs as the positive default NaN */
+static uint32_t digest_bits(float r, int inputs_nan)
+{
+    uint32_t b;
+    memcpy(&b, &r, 4);
+    return (!inputs_nan && isnan(r)) ? 0x7fc00000u : b;
+}
+
+/* The reference's digest inputs (src/libm/tests.rs:20-62): every 61st
+ * binary32 pattern for sincosf; for powf, xorshift64 pairs from seed
+ * 0x2545f4914f6cdd1d, random patterns at even steps and x in (0, 1e6],
+ * y in [-2, 2] at odd steps. */
+uint64_t oracle_libm_digest(int which)
+{
+    uint64_t h = 0xcbf29ce484222325ULL;
+    if (which == 1) {
+        for (uint64_t k = 0; k <= 0xffffffffULL / 61; ++k) {
+            const float x = from_bits((uint32_t)(k * 61));
+            float s, c;
+            sincosf(x, &s, &c);
+            h = fnv(fnv(h, digest_bits(s, isnan(x))), digest_bits(c, isnan(x)));
+        }
+        return h;
+    }
+    uint64_t r = 0x2545f4914f6cdd1dULL;
+    for (uint32_t k = 0; k < (1u << 22); ++k) {
+        r ^= r << 13;
+        r ^= r >> 7;
+        r ^= r << 17;
+        float x, y;
+        if (k % 2 == 0) {
+            x = from_bits((uint32_t)r);
+            y = from_bits((uint32_t)(r >> 32));
+        } else {
+            const float u1 = (float)(r >> 40) / (float)(1u << 24);
+            const float u2 = (float)((r << 24) >> 40) / (float)(1u << 24);
+            x = 1e6f * u1;
+            const float t = 4.0f * u2;
+            y = t - 2.0f;
+        }
+        h = fnv(h, digest_bits(powf(x, y), isnan(x) || isnan(y)));
+    }
+    return h;
+}
+
 /* ---- threaded CPU baseline (the engine's decomposition) ---------------- */
 
 struct job {

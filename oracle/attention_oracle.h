@@ -117,6 +117,22 @@ void oracle_cache_rollback(oracle_layer_cache *c, size_t old_len, size_t old_tot
 void oracle_cache_keep(oracle_layer_cache *c, size_t old_len, size_t old_total, size_t tokens);
 void oracle_cache_commit(oracle_layer_cache *c);
 
+/* Head transform primitives. p9_ref_rms_norm
+ * (src/kernels/portable/reference.rs:11-33): sequential f64 sum of squares,
+ * inv = 1 / sqrt(sum / n + eps) in f64, out = f32(x * inv) [* scale in f32]. */
+void oracle_rms_norm(const float *x, const float *scale, size_t n, float eps, float *out);
+/* p9_ref_rope (reference.rs:277-318): NeoX pairs (i, i + dim/2), f32
+ * frequencies 1 / powf(base, 2i/dim) [/ factor_i], f32 angles, the C
+ * library's sincosf; false on a non-finite angle. */
+bool oracle_rope(const float *x, size_t heads, size_t dim, size_t position, float base,
+                 const float *factors, float *out);
+/* FNV-1a digests of the C library's powf (which = 0) or sincosf (which = 1)
+ * over the inputs of the reference's libm digest tests
+ * (src/libm/tests.rs:20-62, 87-136); NaNs that an invalid operation
+ * generates are counted with the positive default-NaN bits of the
+ * reference's platform. */
+uint64_t oracle_libm_digest(int which);
+
 /* CPU baseline: the exact (a1) or binary32 (a3) path threaded as the engine
  * threads it (src/engine/attention.rs:755-836): one query's heads split
  * into ceil(qheads/split) ranges with split = clamp(workers/queries, 1,

@@ -218,3 +218,56 @@ class OracleCache:
 
     def commit(self):
         self.lib.oracle_cache_commit(ctypes.byref(self.c))
+
+
+def _transform_lib():
+    lib = load()
+    if not getattr(lib, "_transform_bound", False):
+        fp, sz = ctypes.POINTER(ctypes.c_float), ctypes.c_size_t
+        lib.oracle_rms_norm.restype = None
+        lib.oracle_rms_norm.argtypes = [fp, fp, sz, ctypes.c_float, fp]
+        lib.oracle_rope.restype = ctypes.c_bool
+        lib.oracle_rope.argtypes = [fp, sz, sz, sz, ctypes.c_float, fp, fp]
+        lib.oracle_libm_digest.restype = ctypes.c_uint64
+        lib.oracle_libm_digest.argtypes = [ctypes.c_int]
+        lib._transform_bound = True
+    return lib
+
+
+def rms_norm(x, scale, eps):
+    """p9_ref_rms_norm over one row."""
+    lib = _transform_lib()
+    x = _f32(x)
+    s = _f32(scale) if scale is not None else None
+    out = np.zeros(x.size, np.float32)
+    lib.oracle_rms_norm(_f(x), _f(s) if s is not None else None, x.size, eps, _f(out))
+    return out
+
+
+def rope(x, dim, position, base, factors=None):
+    """p9_ref_rope over whole heads: (ok, out)."""
+    lib = _transform_lib()
+    x = _f32(x)
+    f = _f32(factors) if factors is not None else None
+    out = np.zeros(x.size, np.float32)
+    ok = lib.oracle_rope(_f(x), x.size // dim, dim, position, base,
+                         _f(f) if f is not None else None, _f(out))
+    return bool(ok), out
+
+
+def libm_digest(which):
+    """0: powf, 1: sincosf (see oracle_libm_digest)."""
+    return int(_transform_lib().oracle_libm_digest(which))
+
+
+def head_transform(raw_q, raw_k, raw_v, qheads, kvheads, dim, position, query_scale, key_scale,
+                   eps, base, factors=None):
+    """HeadTransform::prepare (src/engine/attention.rs:102-156) for one token:
+    per-head norms, then rotation of Q and K; V = norm(raw V or raw K)."""
+    q = np.concatenate([rms_norm(h, query_scale, eps) for h in _f32(raw_q).reshape(qheads, dim)])
+    k = np.concatenate([rms_norm(h, key_scale, eps) for h in _f32(raw_k).reshape(kvheads, dim)])
+    src = raw_v if raw_v is not None else raw_k
+    v = np.concatenate([rms_norm(h, None, eps) for h in _f32(src).reshape(kvheads, dim)])
+    okq, q = rope(q, dim, position, base, factors)
+    okk, k = rope(k, dim, position, base, factors)
+    return okq and okk, q, k, v

@@ -16,11 +16,15 @@ error behaviour:
   LayerCache
       the engine's LayerCache (src/engine/attention.rs:244-311) with its K/V
       rows in device memory, producing attention descriptors over them.
+  HeadTransform
+      the engine's HeadTransform (src/engine/attention.rs:51-243): Q/K/V head
+      norms and rotary positions on the device, fused with the cache append.
 
 There is no CPU fallback: without the built library every entry raises.
 """
 import ctypes
 import os
+import weakref
 
 import numpy as np
 
@@ -67,6 +71,11 @@ EXPORTS = (
     "pcl_kv_cache_decoder_desc",
     "pcl_kv_cache_shared_desc",
     "pcl_kv_cache_advance",
+    "pcl_head_transform_create",
+    "pcl_head_transform_destroy",
+    "pcl_head_transform_prepare",
+    "pcl_head_transform_query",
+    "pcl_kv_cache_append_transformed",
     "pcl_version",
 )
 
@@ -182,7 +191,15 @@ def load():
             ("pcl_kv_cache_encoder_desc", ctypes.c_int, [vp, pend, dp]),
             ("pcl_kv_cache_decoder_desc", ctypes.c_int, [vp, vp, vp, i64, dp]),
             ("pcl_kv_cache_shared_desc", ctypes.c_int, [vp, vp, pend, i64, dp]),
-            ("pcl_kv_cache_advance", ctypes.c_int, [vp, i64, pend])):
+            ("pcl_kv_cache_advance", ctypes.c_int, [vp, i64, pend]),
+            ("pcl_head_transform_create", ctypes.c_int,
+             [vp, i64, i64, i64, ctypes.c_int, fp, fp, ctypes.c_float, ctypes.c_float, fp,
+              ctypes.POINTER(vp)]),
+            ("pcl_head_transform_destroy", None, [vp]),
+            ("pcl_head_transform_prepare", ctypes.c_int, [vp, vp, vp, vp, i64, i64, vp, vp, vp]),
+            ("pcl_head_transform_query", ctypes.c_int, [vp, vp, i64, i64, vp]),
+            ("pcl_kv_cache_append_transformed", ctypes.c_int,
+             [vp, vp, vp, vp, vp, i64, vp, pend])):
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
@@ -314,6 +331,8 @@ class Context:
     def __init__(self, device=0, stream=None):
         self.lib = load()
         self.handle = ctypes.c_void_p()
+        # caches and transforms made on this context: closed before it
+        self._children = weakref.WeakSet()
         if stream is None:
             rc = self.lib.pcl_context_create(device, ctypes.byref(self.handle))
         else:
@@ -324,6 +343,8 @@ class Context:
 
     def close(self):
         if self.handle:
+            for child in list(self._children):
+                child.close()
             self.lib.pcl_context_destroy(self.handle)
             self.handle = ctypes.c_void_p()
 
@@ -404,6 +425,7 @@ class LayerCache:
                                           ctypes.byref(self.handle))
         if rc != OK:
             raise AttentionError(rc)
+        ctx._children.add(self)
 
     def close(self):
         if self.handle:
@@ -450,6 +472,16 @@ class LayerCache:
                                                  ctypes.byref(pending)))
         return pending
 
+    def append_transformed(self, transform, raw_q_ptr, raw_k_ptr, raw_v_ptr, n, q_out_ptr):
+        """The step's raw projections through `transform` (a HeadTransform):
+        prepared K/V rows appended, prepared queries written to q_out."""
+        pending = PclPending()
+        self._check(self.lib.pcl_kv_cache_append_transformed(
+            self.handle, transform.handle, ctypes.c_void_p(raw_q_ptr),
+            ctypes.c_void_p(raw_k_ptr), ctypes.c_void_p(raw_v_ptr or None), int(n),
+            ctypes.c_void_p(q_out_ptr), ctypes.byref(pending)))
+        return pending
+
     def advance(self, n):
         """A shared-K/V layer's step (encode_shared_in_place's position move)."""
         pending = PclPending()
@@ -486,3 +518,51 @@ class LayerCache:
                                                       ctypes.byref(source_pending), int(n),
                                                       ctypes.byref(d)))
         return d
+
+
+class HeadTransform:
+    """HeadTransform (src/engine/attention.rs:51-243) on the device. Scales
+    and factors are host arrays; prepare()/query() take device pointers of
+    [n][heads][dim] rows, token i at position `position + i`."""
+
+    def __init__(self, ctx, qheads, kv_heads, head_dim, query_scale, key_scale, epsilon, base,
+                 factors=None, sliding=False):
+        self.ctx = ctx
+        self.lib = ctx.lib
+        qs, ks = _f32(query_scale), _f32(key_scale)
+        fs = _f32(factors) if factors is not None else None
+        self._keep = (qs, ks, fs)
+        self.handle = ctypes.c_void_p()
+        rc = self.lib.pcl_head_transform_create(
+            ctx.handle, int(qheads), int(kv_heads), int(head_dim), int(bool(sliding)), _fptr(qs),
+            _fptr(ks), float(epsilon), float(base), _fptr(fs) if fs is not None else None,
+            ctypes.byref(self.handle))
+        if rc != OK:
+            raise AttentionError(rc)
+        ctx._children.add(self)
+
+    def close(self):
+        if self.handle:
+            self.lib.pcl_head_transform_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def prepare(self, raw_q_ptr, raw_k_ptr, raw_v_ptr, n, position, q_out_ptr, k_out_ptr,
+                v_out_ptr):
+        rc = self.lib.pcl_head_transform_prepare(
+            self.handle, ctypes.c_void_p(raw_q_ptr), ctypes.c_void_p(raw_k_ptr),
+            ctypes.c_void_p(raw_v_ptr or None), int(n), int(position),
+            ctypes.c_void_p(q_out_ptr), ctypes.c_void_p(k_out_ptr), ctypes.c_void_p(v_out_ptr))
+        if rc != OK:
+            raise AttentionError(rc)
+
+    def query(self, raw_q_ptr, n, position, q_out_ptr):
+        rc = self.lib.pcl_head_transform_query(self.handle, ctypes.c_void_p(raw_q_ptr), int(n),
+                                               int(position), ctypes.c_void_p(q_out_ptr))
+        if rc != OK:
+            raise AttentionError(rc)

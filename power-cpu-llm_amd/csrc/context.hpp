@@ -1,5 +1,5 @@
-// Host-side state of a pcl_context (shared by the attention entry points and
-// the device-resident layer cache).
+// Host-side state of a pcl_context and of a layer cache (shared by the
+// attention entry points, the layer cache and the head transform).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -28,3 +28,28 @@ struct pcl_context {
     std::vector<TimedSpan> spans;
     std::vector<hipEvent_t> free_events;
 };
+
+// A device-resident layer cache: rows [start, len) of k / v are retained.
+struct pcl_kv_cache {
+    pcl_context *ctx = nullptr;
+    int64_t kvheads = 0, dim = 0, width = 0; // width = floats per token
+    int64_t context = 0, window = 0;
+    size_t max_bytes = 0;
+    int64_t total = 0; // positions processed (LayerCache::total)
+    int64_t start = 0; // first retained row
+    int64_t len = 0;   // rows in the buffers
+    int64_t cap = 0;   // rows the buffers hold
+    float *k = nullptr, *v = nullptr;
+};
+
+struct pcl_kv_pending;
+
+namespace pcl {
+
+// Checks the position and byte limits of an n-row step and makes room for
+// its rows after the retained ones (the cache is unchanged on an error).
+int kv_cache_reserve(pcl_kv_cache *c, int64_t n);
+// Records the step in *pending and counts its n rows (written at row len).
+void kv_cache_advance_rows(pcl_kv_cache *c, int64_t n, pcl_kv_pending *pending);
+
+} // namespace pcl

@@ -1,0 +1,418 @@
+// Head normalisation and rotary transform of projected Q/K/V rows on gfx950:
+// the engine's HeadTransform (src/engine/attention.rs:51-243), applied to n
+// tokens at once on the device, with K and V optionally written straight
+// into a layer cache's rows (no staging copy).
+//
+// Per head (p9_ref_rms_norm, src/kernels/portable/reference.rs:11-33):
+//   sum = sequential f64 sum of f64(x_j)^2, j ascending;
+//   inv = 1 / sqrt(sum / dim + f64(eps))            (f64, correctly rounded);
+//   y_j = f32(f64(x_j) * inv), times scale_j in f32 for Q and K.
+// Q and K then rotate pairs (j, j + dim/2) (p9_ref_rope, reference.rs:277-318):
+//   y_j' = y_j*c - y_{j+h}*s,  y_{j+h}' = y_{j+h}*c + y_j*s   (f32, unfused),
+// with (s, c) = sincosf(f32(position) * f32(1 / powf(base, 2j/dim)) / factor_j)
+// from a host-built table (the C library's powf and sincosf). V is normalised
+// without scale and not rotated; a global layer without a V projection uses
+// the raw K as V (attention.rs:121-129).
+//
+// One 64-lane workgroup takes up to kItems heads: it stages their rows in LDS
+// with coalesced loads (row stride dim+1, so the per-lane row walks of the
+// f64 sum hit distinct banks), each lane sums one row in order, and the
+// outputs are written back coalesced.
+#include "attention_device.hpp"
+#include "context.hpp"
+#include "pcl_attention.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <new>
+#include <vector>
+
+namespace pcl {
+
+constexpr int kErrTransform = 4; // non-finite head-transform input or output
+
+struct TransformParams {
+    const float *rq, *rk, *rv; // raw rows [n][heads*dim]; rv null: V = raw K
+    float *oq, *ok, *ov;       // outputs; ok null: query heads only
+    int64_t o_kv_stride;       // floats between K/V output rows
+    const float *qs, *ks;      // learned scales [dim]
+    const float *tab;          // (sin, cos) pairs [position][dim/2][2]
+    int64_t pos0;
+    int n, qheads, kvh, dim, slots;
+    float eps;
+    int *err;
+};
+
+// Heads per workgroup: about 32 KiB of staged rows, so several workgroups
+// share a CU and hide the latency of the per-lane f64 sums.
+template <int DK>
+constexpr int transform_items()
+{
+    return 8192 / DK < 64 ? 8192 / DK : 64;
+}
+
+template <int DK>
+__global__ __launch_bounds__(64) void head_transform_kernel(TransformParams p)
+{
+    constexpr int kItems = transform_items<DK>();
+    constexpr int kStride = DK + 1;
+    constexpr int kHalf = DK / 2;
+    __shared__ float rows[kItems * kStride];
+    __shared__ double inv[kItems];
+    const int lane = threadIdx.x;
+    const int64_t first = (int64_t)blockIdx.x * kItems;
+    const int64_t items = (int64_t)p.n * p.slots;
+    const int count = (int)std::min<int64_t>(kItems, items - first);
+
+    // row r of the block: token t, slot s (Q heads, then K heads, then V heads)
+    auto source = [&](int r, int &kind) -> const float * {
+        const int64_t item = first + r;
+        const int64_t t = item / p.slots;
+        const int s = (int)(item - t * p.slots);
+        if (s < p.qheads) {
+            kind = 0;
+            return p.rq + (t * p.qheads + s) * DK;
+        }
+        if (s < p.qheads + p.kvh) {
+            kind = 1;
+            return p.rk + (t * p.kvh + (s - p.qheads)) * DK;
+        }
+        kind = 2;
+        const float *v = p.rv ? p.rv : p.rk;
+        return v + (t * p.kvh + (s - p.qheads - p.kvh)) * DK;
+    };
+
+    bool bad = false;
+    for (int r = 0; r < count; ++r) {
+        int kind;
+        const float *x = source(r, kind);
+#pragma unroll
+        for (int j = lane; j < DK; j += 64) {
+            const float v = ldg(x + j);
+            bad |= !is_finite(v);
+            rows[r * kStride + j] = v;
+        }
+    }
+    __syncthreads();
+    if (lane < count) {
+        double sum = 0.0;
+        const float *row = rows + lane * kStride;
+#pragma unroll 8
+        for (int j = 0; j < DK; ++j) {
+            const double v = (double)row[j];
+            sum = sum + v * v;
+        }
+        inv[lane] = 1.0 / __builtin_sqrt(sum / (double)DK + (double)p.eps);
+    }
+    __syncthreads();
+    for (int r = 0; r < count; ++r) {
+        int kind;
+        (void)source(r, kind);
+        const int64_t item = first + r;
+        const int64_t t = item / p.slots;
+        const int s = (int)(item - t * p.slots);
+        const double iv = inv[r];
+        const float *row = rows + r * kStride;
+        float *out;
+        const float *scale = nullptr;
+        if (kind == 0) {
+            out = p.oq + (t * p.qheads + s) * DK;
+            scale = p.qs;
+        } else if (kind == 1) {
+            out = p.ok + t * p.o_kv_stride + (int64_t)(s - p.qheads) * DK;
+            scale = p.ks;
+        } else {
+            out = p.ov + t * p.o_kv_stride + (int64_t)(s - p.qheads - p.kvh) * DK;
+        }
+        const float *tab = p.tab + (p.pos0 + t) * DK;
+#pragma unroll
+        for (int j = lane; j < kHalf; j += 64) {
+            float a = (float)((double)row[j] * iv);
+            float b = (float)((double)row[j + kHalf] * iv);
+            if (kind != 2) {
+                a = a * ldg(scale + j);
+                b = b * ldg(scale + j + kHalf);
+                typedef float f2 __attribute__((ext_vector_type(2)));
+                const f2 sc = *(const __attribute__((address_space(1))) f2 *)(tab + 2 * j);
+                const float ac = a * sc.y, bs = b * sc.x;
+                const float bc = b * sc.y, as = a * sc.x;
+                a = ac - bs;
+                b = bc + as;
+            }
+            bad |= !is_finite(a) || !is_finite(b);
+            stg(out + j, a);
+            stg(out + j + kHalf, b);
+        }
+    }
+    if (bad)
+        atomicOr(p.err, kErrTransform);
+}
+
+hipError_t launch_head_transform(const TransformParams &p, hipStream_t stream)
+{
+    const int64_t items = (int64_t)p.n * p.slots;
+    auto go = [&](auto kernel, int per) {
+        const unsigned blocks = (unsigned)((items + per - 1) / per);
+        hipLaunchKernelGGL(kernel, dim3(blocks), dim3(64), 0, stream, p);
+        return hipGetLastError();
+    };
+    switch (p.dim) {
+    case 16: return go(head_transform_kernel<16>, transform_items<16>());
+    case 32: return go(head_transform_kernel<32>, transform_items<32>());
+    case 64: return go(head_transform_kernel<64>, transform_items<64>());
+    case 128: return go(head_transform_kernel<128>, transform_items<128>());
+    case 256: return go(head_transform_kernel<256>, transform_items<256>());
+    case 512: return go(head_transform_kernel<512>, transform_items<512>());
+    default: return hipErrorInvalidValue;
+    }
+}
+
+} // namespace pcl
+
+struct pcl_head_transform {
+    pcl_context *ctx = nullptr;
+    int64_t qheads = 0, kvheads = 0, dim = 0;
+    int sliding = 0;
+    float eps = 0.0f, base = 0.0f;
+    std::vector<float> factors; // empty: none
+    float *scales = nullptr;    // device [2][dim]: query, key
+    float *tab = nullptr;       // device (sin, cos) pairs [rows][dim/2][2]
+    int64_t tab_rows = 0;
+};
+
+namespace {
+
+using pcl::TransformParams;
+
+// Positions are converted to f32 for the angles (exact below 2^24).
+constexpr int64_t kMaxPositions = (int64_t)1 << 24;
+
+void report(const char *what, hipError_t e)
+{
+    std::fprintf(stderr, "pcl_head_transform: %s: %s\n", what, hipGetErrorString(e));
+}
+
+bool finite_all(const float *x, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i)
+        if (!std::isfinite(x[i]))
+            return false;
+    return true;
+}
+
+// (sin, cos) of every pair of positions [from, to): p9_ref_rope's
+// frequencies and angles in f32 (reference.rs:294-305), the C library's
+// powf and sincosf. False on a non-finite angle.
+bool rope_rows(const pcl_head_transform *t, int64_t from, int64_t to, float *out)
+{
+    const int64_t half = t->dim / 2;
+    std::vector<float> inv(half);
+    for (int64_t i = 0; i < half; ++i) {
+        float f = 1.0f / powf(t->base, (2.0f * (float)i) / (float)t->dim);
+        if (!t->factors.empty())
+            f = f / t->factors[i];
+        inv[i] = f;
+    }
+    for (int64_t p = from; p < to; ++p) {
+        for (int64_t i = 0; i < half; ++i) {
+            const float angle = (float)p * inv[i];
+            if (!std::isfinite(angle))
+                return false;
+            float s, c;
+            sincosf(angle, &s, &c);
+            out[2 * ((p - from) * half + i)] = s;
+            out[2 * ((p - from) * half + i) + 1] = c;
+        }
+    }
+    return true;
+}
+
+// Table rows for positions [0, end): grown by doubling, built on the host.
+int ensure_table(pcl_head_transform *t, int64_t end)
+{
+    if (end <= t->tab_rows)
+        return PCL_OK;
+    const int64_t half = t->dim / 2;
+    const int64_t rows = std::min<int64_t>(
+        kMaxPositions, std::max<int64_t>(end, std::max<int64_t>(2 * t->tab_rows, 256)));
+    std::vector<float> host;
+    try {
+        host.resize((size_t)(rows - t->tab_rows) * half * 2);
+    } catch (const std::bad_alloc &) {
+        return PCL_RESOURCE_LIMIT;
+    }
+    if (!rope_rows(t, t->tab_rows, rows, host.data()))
+        return PCL_NON_FINITE_VALUE;
+    float *tab = nullptr;
+    hipError_t e = hipMalloc(&tab, (size_t)rows * half * 2 * sizeof(float));
+    if (e == hipSuccess && t->tab_rows)
+        e = hipMemcpyAsync(tab, t->tab, (size_t)t->tab_rows * half * 2 * sizeof(float),
+                           hipMemcpyDeviceToDevice, t->ctx->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(tab + t->tab_rows * half * 2, host.data(),
+                           host.size() * sizeof(float), hipMemcpyHostToDevice, t->ctx->stream);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(t->ctx->stream); // the old table and host rows are read
+    if (e != hipSuccess) {
+        report("growing the rotary table", e);
+        if (tab)
+            (void)hipFree(tab);
+        return PCL_RESOURCE_LIMIT;
+    }
+    if (t->tab)
+        (void)hipFree(t->tab);
+    t->tab = tab;
+    t->tab_rows = rows;
+    return PCL_OK;
+}
+
+int run(pcl_head_transform *t, const float *rq, const float *rk, const float *rv, int64_t n,
+        int64_t position, float *oq, float *ok, float *ov, int64_t kv_stride)
+{
+    if (n <= 0 || position < 0 || position > kMaxPositions - n)
+        return PCL_RESOURCE_LIMIT;
+    if (!rq || !oq || (ok && (!rk || !ov)))
+        return PCL_INVALID_SHAPE;
+    if (ok && !rv && t->sliding)
+        return PCL_INVALID_SHAPE; // "sliding attention needs V"
+    const int64_t slots = t->qheads + (ok ? 2 * t->kvheads : 0);
+    if (n > ((int64_t)1 << 31) / slots)
+        return PCL_INVALID_SHAPE;
+    (void)hipSetDevice(t->ctx->device);
+    const int rc = ensure_table(t, position + n);
+    if (rc != PCL_OK)
+        return rc;
+    TransformParams p{};
+    p.rq = rq;
+    p.rk = rk;
+    p.rv = rv;
+    p.oq = oq;
+    p.ok = ok;
+    p.ov = ov;
+    p.o_kv_stride = kv_stride;
+    p.qs = t->scales;
+    p.ks = t->scales + t->dim;
+    p.tab = t->tab;
+    p.pos0 = position;
+    p.n = (int)n;
+    p.qheads = (int)t->qheads;
+    p.kvh = (int)t->kvheads;
+    p.dim = (int)t->dim;
+    p.slots = (int)slots;
+    p.eps = t->eps;
+    p.err = t->ctx->err;
+    const hipError_t e = pcl::launch_head_transform(p, t->ctx->stream);
+    if (e != hipSuccess) {
+        report("launch", e);
+        return PCL_NON_FINITE_VALUE;
+    }
+    return PCL_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+int pcl_head_transform_create(pcl_context *ctx, int64_t qheads, int64_t kvheads, int64_t dim,
+                              int sliding, const float *query_scale, const float *key_scale,
+                              float epsilon, float base, const float *factors,
+                              pcl_head_transform **out)
+{
+    if (!out)
+        return PCL_INVALID_SHAPE;
+    *out = nullptr;
+    // widths (attention.rs:12-32) and this backend's head dims
+    if (!ctx || qheads <= 0 || kvheads <= 0 || qheads % kvheads != 0 || qheads > 4096 ||
+        !query_scale || !key_scale)
+        return PCL_INVALID_SHAPE;
+    if (dim != 16 && dim != 32 && dim != 64 && dim != 128 && dim != 256 && dim != 512)
+        return PCL_INVALID_SHAPE;
+    // HeadTransform::new's parameter checks (attention.rs:74-97)
+    if (!std::isfinite(epsilon) || epsilon <= 0.0f || !std::isfinite(base) || base <= 0.0f ||
+        !finite_all(query_scale, dim) || !finite_all(key_scale, dim))
+        return PCL_INVALID_PARAMETER;
+    if (factors) {
+        for (int64_t i = 0; i < dim / 2; ++i)
+            if (!std::isfinite(factors[i]) || factors[i] <= 0.0f)
+                return PCL_INVALID_PARAMETER;
+    }
+    auto *t = new pcl_head_transform;
+    t->ctx = ctx;
+    t->qheads = qheads;
+    t->kvheads = kvheads;
+    t->dim = dim;
+    t->sliding = sliding != 0;
+    t->eps = epsilon;
+    t->base = base;
+    if (factors)
+        t->factors.assign(factors, factors + dim / 2);
+    (void)hipSetDevice(ctx->device);
+    hipError_t e = hipMalloc(&t->scales, 2 * dim * sizeof(float));
+    if (e == hipSuccess)
+        e = hipMemcpy(t->scales, query_scale, dim * sizeof(float), hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = hipMemcpy(t->scales + dim, key_scale, dim * sizeof(float), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        report("create", e);
+        if (t->scales)
+            (void)hipFree(t->scales);
+        delete t;
+        return PCL_RESOURCE_LIMIT;
+    }
+    *out = t;
+    return PCL_OK;
+}
+
+void pcl_head_transform_destroy(pcl_head_transform *t)
+{
+    if (!t)
+        return;
+    (void)hipSetDevice(t->ctx->device);
+    (void)hipStreamSynchronize(t->ctx->stream);
+    if (t->scales)
+        (void)hipFree(t->scales);
+    if (t->tab)
+        (void)hipFree(t->tab);
+    delete t;
+}
+
+int pcl_head_transform_prepare(pcl_head_transform *t, const float *raw_q, const float *raw_k,
+                               const float *raw_v, int64_t n, int64_t position, float *q_out,
+                               float *k_out, float *v_out)
+{
+    if (!t || !k_out)
+        return PCL_INVALID_SHAPE;
+    return run(t, raw_q, raw_k, raw_v, n, position, q_out, k_out, v_out, t->kvheads * t->dim);
+}
+
+int pcl_head_transform_query(pcl_head_transform *t, const float *raw_q, int64_t n,
+                             int64_t position, float *q_out)
+{
+    if (!t)
+        return PCL_INVALID_SHAPE;
+    return run(t, raw_q, nullptr, nullptr, n, position, q_out, nullptr, nullptr, 0);
+}
+
+int pcl_kv_cache_append_transformed(pcl_kv_cache *c, pcl_head_transform *t, const float *raw_q,
+                                    const float *raw_k, const float *raw_v, int64_t n,
+                                    float *q_out, pcl_kv_pending *pending)
+{
+    if (!c || !t || !pending || n <= 0 || !raw_q || !raw_k || !q_out)
+        return PCL_INVALID_SHAPE;
+    if (t->ctx != c->ctx || t->kvheads != c->kvheads || t->dim != c->dim)
+        return PCL_INVALID_SHAPE; // "cache owner/layer/geometry mismatch"
+    if (!raw_v && t->sliding)
+        return PCL_INVALID_SHAPE;
+    int rc = pcl::kv_cache_reserve(c, n);
+    if (rc != PCL_OK)
+        return rc;
+    rc = run(t, raw_q, raw_k, raw_v, n, c->total, q_out, c->k + c->len * c->width,
+             c->v + c->len * c->width, c->width);
+    if (rc != PCL_OK)
+        return rc;
+    pcl::kv_cache_advance_rows(c, n, pending);
+    return PCL_OK;
+}
+
+} // extern "C"

@@ -15,18 +15,6 @@
 #include <cstdio>
 #include <cstring>
 
-struct pcl_kv_cache {
-    pcl_context *ctx = nullptr;
-    int64_t kvheads = 0, dim = 0, width = 0; // width = floats per token
-    int64_t context = 0, window = 0;
-    size_t max_bytes = 0;
-    int64_t total = 0;      // positions processed (LayerCache::total)
-    int64_t start = 0;      // first retained row
-    int64_t len = 0;        // rows in the buffers
-    int64_t cap = 0;        // rows the buffers hold
-    float *k = nullptr, *v = nullptr;
-};
-
 namespace {
 
 void report(const char *what, hipError_t e)
@@ -66,6 +54,65 @@ bool valid_pending(const pcl_kv_cache *c, const pcl_kv_pending *p)
 }
 
 } // namespace
+
+namespace pcl {
+
+int kv_cache_reserve(pcl_kv_cache *c, int64_t n)
+{
+    // check_stage (attention.rs:543-558): the next position within the
+    // context, the retained plus appended K+V within the byte limit
+    if (n > c->context - c->total)
+        return PCL_RESOURCE_LIMIT;
+    const int64_t retained = c->len - c->start;
+    const double bytes = (double)(retained + n) * (double)c->width * 2.0 * sizeof(float);
+    if (bytes > (double)c->max_bytes)
+        return PCL_RESOURCE_LIMIT;
+    (void)hipSetDevice(c->ctx->device);
+    if (c->len + n <= c->cap)
+        return PCL_OK;
+    // new buffers for at least twice the step's rows (a Vec's growth),
+    // holding at most what the byte limit allows, retained rows first
+    const int64_t limit = (int64_t)(c->max_bytes / ((size_t)c->width * 2 * sizeof(float)));
+    const int64_t need = retained + n;
+    const int64_t cap = std::max(need, std::min(2 * need, limit));
+    float *nk = nullptr, *nv = nullptr;
+    hipError_t e = hipMalloc(&nk, (size_t)cap * c->width * sizeof(float));
+    if (e == hipSuccess)
+        e = hipMalloc(&nv, (size_t)cap * c->width * sizeof(float));
+    if (e == hipSuccess && retained)
+        e = copy_rows(c, nk, nv, c->k + c->start * c->width, c->v + c->start * c->width,
+                      retained);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(c->ctx->stream); // the old buffers are read
+    if (e != hipSuccess) {
+        report("growing the cache", e);
+        if (nk)
+            (void)hipFree(nk);
+        if (nv)
+            (void)hipFree(nv);
+        return PCL_RESOURCE_LIMIT;
+    }
+    if (c->k)
+        (void)hipFree(c->k);
+    if (c->v)
+        (void)hipFree(c->v);
+    c->k = nk;
+    c->v = nv;
+    c->cap = cap;
+    c->len = retained;
+    c->start = 0;
+    return PCL_OK;
+}
+
+void kv_cache_advance_rows(pcl_kv_cache *c, int64_t n, pcl_kv_pending *pending)
+{
+    pending->old_len = c->len;
+    pending->old_total = c->total;
+    c->len += n;
+    c->total += n;
+}
+
+} // namespace pcl
 
 extern "C" {
 
@@ -159,58 +206,16 @@ int pcl_kv_cache_append(pcl_kv_cache *c, const float *keys, const float *values,
 {
     if (!c || !pending || n <= 0 || !keys || !values)
         return PCL_INVALID_SHAPE;
-    // check_stage (attention.rs:543-558): the next position within the
-    // context, the retained plus appended K+V within the byte limit
-    if (n > c->context - c->total)
-        return PCL_RESOURCE_LIMIT;
-    const int64_t retained = c->len - c->start;
-    const double bytes = (double)(retained + n) * (double)c->width * 2.0 * sizeof(float);
-    if (bytes > (double)c->max_bytes)
-        return PCL_RESOURCE_LIMIT;
-    (void)hipSetDevice(c->ctx->device);
-    if (c->len + n > c->cap) {
-        // new buffers for at least twice the step's rows (a Vec's growth),
-        // holding at most what the byte limit allows, retained rows first
-        const int64_t limit = (int64_t)(c->max_bytes / ((size_t)c->width * 2 * sizeof(float)));
-        const int64_t need = retained + n;
-        const int64_t cap = std::max(need, std::min(2 * need, limit));
-        float *nk = nullptr, *nv = nullptr;
-        hipError_t e = hipMalloc(&nk, (size_t)cap * c->width * sizeof(float));
-        if (e == hipSuccess)
-            e = hipMalloc(&nv, (size_t)cap * c->width * sizeof(float));
-        if (e == hipSuccess && retained)
-            e = copy_rows(c, nk, nv, c->k + c->start * c->width, c->v + c->start * c->width,
-                          retained);
-        if (e == hipSuccess)
-            e = hipStreamSynchronize(c->ctx->stream); // the old buffers are read
-        if (e != hipSuccess) {
-            report("growing the cache", e);
-            if (nk)
-                (void)hipFree(nk);
-            if (nv)
-                (void)hipFree(nv);
-            return PCL_RESOURCE_LIMIT;
-        }
-        if (c->k)
-            (void)hipFree(c->k);
-        if (c->v)
-            (void)hipFree(c->v);
-        c->k = nk;
-        c->v = nv;
-        c->cap = cap;
-        c->len = retained;
-        c->start = 0;
-    }
+    const int rc = pcl::kv_cache_reserve(c, n);
+    if (rc != PCL_OK)
+        return rc;
     const hipError_t e = copy_rows(c, c->k + c->len * c->width, c->v + c->len * c->width, keys,
                                    values, n, hipMemcpyDefault);
     if (e != hipSuccess) {
         report("appending rows", e);
         return PCL_NON_FINITE_VALUE;
     }
-    pending->old_len = c->len;
-    pending->old_total = c->total;
-    c->len += n;
-    c->total += n;
+    pcl::kv_cache_advance_rows(c, n, pending);
     return PCL_OK;
 }
 
