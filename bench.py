@@ -54,6 +54,11 @@ WORKLOADS = {
     # one decode step through the device-resident layer cache: append the
     # token's K/V row, attend over the 32K cache in place, roll back
     "decode_32k_cache": (16, 8, 256, 1, 32768, True, 0, 32767, "cache", False),
+    # the head-transform prologue over a 4K-token prompt (norms and rotation
+    # of 16 Q, 8 K and 8 V heads per token), and a whole decode step from raw
+    # projections: transform fused with the cache append, then attention
+    "transform_4k": (16, 8, 256, 4096, 0, True, 0, 0, "transform", False),
+    "decode_32k_step": (16, 8, 256, 1, 32768, True, 0, 32767, "step", False),
 }
 HEADLINE = "decode_32k"
 
@@ -87,6 +92,10 @@ def allowed_pairs(nq, nkeys, causal, window, first_query):
 
 def work(name):
     qh, kvh, dim, nq, nkeys, causal, window, fq, kind, _ = WORKLOADS[name]
+    if kind == "transform":
+        # raw Q/K/V rows read, prepared rows written, (sin, cos) table rows read
+        heads = qh + 2 * kvh
+        return 0, nq * (2 * heads * dim * 4 + dim * 4), 0
     pairs = allowed_pairs(nq, nkeys, causal, window, fq)
     flops = 4 * dim * pairs * qh
     # decode bytes: attended K and V rows of every KV head, plus Q and O
@@ -144,6 +153,11 @@ def time_workload(torch, pcl, ctx, name, steps, warmup, seed=0, kernel=0):
     nsets = max(2, min(MAX_SETS, -(-CYCLE_BYTES // set_bytes)))
     if kind == "cache":
         return time_cache_workload(torch, pcl, ctx, name, steps, warmup, nsets, seed)
+    if kind == "step":
+        return time_cache_workload(torch, pcl, ctx, name, steps, warmup, nsets, seed,
+                                   transform=True)
+    if kind == "transform":
+        return time_transform_workload(torch, pcl, ctx, name, steps, warmup, seed)
     sets = []
     for i in range(nsets):
         q, k, v = make_inputs(torch, name, seed + 1000 * i)
@@ -188,12 +202,65 @@ def time_workload(torch, pcl, ctx, name, steps, warmup, seed=0, kernel=0):
     return ev, wall, kernel, host, roles, nsets
 
 
-def time_cache_workload(torch, pcl, ctx, name, steps, warmup, nsets, seed):
-    """Decode steps through pcl.LayerCache: per step, append one token's K/V
-    (device rows) after nkeys-1 cached rows, attend over the cache's rows in
-    place (its encoder descriptor), roll the step back. Each input set is
-    its own cache."""
+def make_transform(torch, pcl, ctx, qh, kvh, dim):
+    g = torch.Generator()
+    g.manual_seed(0x5EED0600)
+    qs = (1 + 0.1 * torch.randn(dim, generator=g)).numpy()
+    ks = (1 + 0.1 * torch.randn(dim, generator=g)).numpy()
+    return pcl.HeadTransform(ctx, qh, kvh, dim, qs, ks, 1e-6, 10000.0)
+
+
+def time_transform_workload(torch, pcl, ctx, name, steps, warmup, seed):
+    """The head transform of nq tokens at positions 0.. (raw rows seeded
+    N(0,1)); HIP events around the launches."""
     qh, kvh, dim, nq, nkeys, causal, window, fq, kind, _ = WORKLOADS[name]
+    t = make_transform(torch, pcl, ctx, qh, kvh, dim)
+    set_bytes = 8 * nq * (qh + 2 * kvh) * dim
+    nsets = max(2, min(MAX_SETS, -(-CYCLE_BYTES // set_bytes)))
+    sets = []
+    dev = torch.device("cuda:0")
+    for i in range(nsets):
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(0x5EED0700 + seed + i)
+        raw = [torch.randn((nq, h * dim), generator=gen, device=dev) for h in (qh, kvh, kvh)]
+        outs = [torch.empty_like(x) for x in raw]
+        sets.append((raw, outs))
+
+    def step(i):
+        raw, outs = sets[i % nsets]
+        t.prepare(raw[0].data_ptr(), raw[1].data_ptr(), raw[2].data_ptr(), nq, 0,
+                  outs[0].data_ptr(), outs[1].data_ptr(), outs[2].data_ptr())
+
+    for i in range(max(warmup, nsets)):
+        step(i)
+    torch.cuda.synchronize()
+    if ctx.sync():
+        raise RuntimeError("device error flag set for %s" % name)
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for i in range(steps):
+        step(i)
+    stop.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    ev = start.elapsed_time(stop) / steps
+    if ctx.sync():
+        raise RuntimeError("device error flag set for %s" % name)
+    t.close()
+    roles = {"stream_ms": ev, "combine_ms": 0.0}
+    return ev, wall, "head_transform", None, roles, nsets
+
+
+def time_cache_workload(torch, pcl, ctx, name, steps, warmup, nsets, seed, transform=False):
+    """Decode steps through pcl.LayerCache: per step, append one token's K/V
+    after nkeys-1 cached rows (as device rows, or with transform=True from the
+    token's raw Q/K/V projections through the head transform, fused with the
+    append), attend over the cache's rows in place (its encoder descriptor),
+    roll the step back. Each input set is its own cache."""
+    qh, kvh, dim, nq, nkeys, causal, window, fq, kind, _ = WORKLOADS[name]
+    t = make_transform(torch, pcl, ctx, qh, kvh, dim) if transform else None
     sets = []
     for i in range(nsets):
         q, k, v = make_inputs(torch, name, seed + 1000 * i)
@@ -202,13 +269,24 @@ def time_cache_workload(torch, pcl, ctx, name, steps, warmup, nsets, seed):
         cache.commit()
         out = torch.empty((nq, qh, dim), device="cuda:0", dtype=torch.float32)
         kt, vt = k[nkeys - 1:].clone(), v[nkeys - 1:].clone()
-        sets.append(({"q": q, "k": k, "v": v, "out": out, "kt": kt, "vt": vt}, cache))
+        host = {"q": q, "k": k, "v": v, "out": out, "kt": kt, "vt": vt}
+        if transform:
+            host["raw_q"] = q.clone()
+            host["q_prepared"] = torch.empty_like(q)
+        sets.append((host, cache))
     torch.cuda.synchronize()
 
     def step(i):
         host, cache = sets[i % nsets]
-        pending = cache.append(host["kt"].data_ptr(), host["vt"].data_ptr(), 1)
-        d = cache.encoder_desc(pending, q=host["q"].data_ptr(), q_stride=qh * dim, nq=nq,
+        if transform:
+            pending = cache.append_transformed(t, host["raw_q"].data_ptr(), host["kt"].data_ptr(),
+                                               host["vt"].data_ptr(), 1,
+                                               host["q_prepared"].data_ptr())
+            qptr = host["q_prepared"].data_ptr()
+        else:
+            pending = cache.append(host["kt"].data_ptr(), host["vt"].data_ptr(), 1)
+            qptr = host["q"].data_ptr()
+        d = cache.encoder_desc(pending, q=qptr, q_stride=qh * dim, nq=nq,
                                qheads=qh, kh_first=0, kh_end=kvh, out=host["out"].data_ptr(),
                                o_stride=qh * dim)
         ctx.launch(d)
@@ -245,6 +323,8 @@ def time_cache_workload(torch, pcl, ctx, name, steps, warmup, nsets, seed):
     host = sets[(steps - 1) % nsets][0]
     for _, cache in sets:
         cache.close()
+    if t is not None:
+        t.close()
     return ev, wall, kernel, host, roles, nsets
 
 
@@ -320,7 +400,7 @@ def main():
              "algorithmic_bytes": bytes_, "algorithmic_flops": flops}
         r["GB/s"] = bytes_ / (ev * 1e-3) / 1e9
         r["TFLOP/s"] = flops / (ev * 1e-3) / 1e12
-        if kind in ("decode", "cache"):
+        if kind in ("decode", "cache", "step", "transform"):
             r["frac_hbm"] = r["GB/s"] / HBM_PEAK_GBS
         else:
             r["frac_mfma"] = r["TFLOP/s"] / FP32_MFMA_PEAK_TFS

@@ -14,10 +14,10 @@
 // without scale and not rotated; a global layer without a V projection uses
 // the raw K as V (attention.rs:121-129).
 //
-// One 64-lane workgroup takes up to kItems heads: it stages their rows in LDS
-// with coalesced loads (row stride dim+1, so the per-lane row walks of the
-// f64 sum hit distinct banks), each lane sums one row in order, and the
-// outputs are written back coalesced.
+// One 64-lane workgroup takes up to kItems heads of one token: it loads the
+// token's rotation factors and the scales once per lane, issues the loads of
+// all its rows at once (16-byte, coalesced) and stages them in LDS, each lane
+// sums one row in order, and the outputs are written back coalesced.
 #include "attention_device.hpp"
 #include "context.hpp"
 #include "pcl_attention.h"
@@ -44,54 +44,76 @@ struct TransformParams {
     int *err;
 };
 
-// Heads per workgroup: about 32 KiB of staged rows, so several workgroups
-// share a CU and hide the latency of the per-lane f64 sums.
+// Heads per workgroup: about 16 KiB of staged rows, so that several
+// workgroups share a CU and one's loads overlap another's sums and stores.
 template <int DK>
 constexpr int transform_items()
 {
-    return 8192 / DK < 64 ? 8192 / DK : 64;
+    return 4096 / DK < 64 ? 4096 / DK : 64;
 }
 
+// Workgroup (token t, slot group y): heads y*kItems.. of token t.
 template <int DK>
 __global__ __launch_bounds__(64) void head_transform_kernel(TransformParams p)
 {
     constexpr int kItems = transform_items<DK>();
-    constexpr int kStride = DK + 1;
+    constexpr int kStride = DK + 4; // 16-byte aligned rows
     constexpr int kHalf = DK / 2;
-    __shared__ float rows[kItems * kStride];
+    constexpr int kPairs = (kHalf + 63) / 64;
+    constexpr int kVec = DK / 4;                          // float4 per row
+    constexpr int kLoads = (kItems * kVec + 63) / 64;     // float4 per lane
+    __shared__ __attribute__((aligned(16))) float rows[kItems * kStride];
     __shared__ double inv[kItems];
     const int lane = threadIdx.x;
-    const int64_t first = (int64_t)blockIdx.x * kItems;
-    const int64_t items = (int64_t)p.n * p.slots;
-    const int count = (int)std::min<int64_t>(kItems, items - first);
+    const int64_t t = blockIdx.x;
+    const int s0 = blockIdx.y * kItems;
+    const int count = p.slots - s0 < kItems ? p.slots - s0 : kItems;
 
-    // row r of the block: token t, slot s (Q heads, then K heads, then V heads)
-    auto source = [&](int r, int &kind) -> const float * {
-        const int64_t item = first + r;
-        const int64_t t = item / p.slots;
-        const int s = (int)(item - t * p.slots);
-        if (s < p.qheads) {
-            kind = 0;
+    // this lane's pairs j = lane + 64m: (sin, cos) of the token's position
+    // and the learned scales of both halves
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    f2 sc[kPairs];
+    float qa[kPairs], qb[kPairs], ka[kPairs], kb[kPairs];
+    const float *tab = p.tab + (p.pos0 + t) * DK;
+#pragma unroll
+    for (int m = 0; m < kPairs; ++m) {
+        const int j = lane + 64 * m < kHalf ? lane + 64 * m : 0;
+        sc[m] = *(const __attribute__((address_space(1))) f2 *)(tab + 2 * j);
+        qa[m] = ldg(p.qs + j);
+        qb[m] = ldg(p.qs + j + kHalf);
+        ka[m] = ldg(p.ks + j);
+        kb[m] = ldg(p.ks + j + kHalf);
+    }
+
+    // slot s of the token: Q heads, then K heads, then V heads
+    auto source = [&](int s) -> const float * {
+        if (s < p.qheads)
             return p.rq + (t * p.qheads + s) * DK;
-        }
-        if (s < p.qheads + p.kvh) {
-            kind = 1;
+        if (s < p.qheads + p.kvh)
             return p.rk + (t * p.kvh + (s - p.qheads)) * DK;
-        }
-        kind = 2;
         const float *v = p.rv ? p.rv : p.rk;
         return v + (t * p.kvh + (s - p.qheads - p.kvh)) * DK;
     };
 
+    // every row's loads in flight at once, then the LDS stores
+    f4 staged[kLoads];
     bool bad = false;
-    for (int r = 0; r < count; ++r) {
-        int kind;
-        const float *x = source(r, kind);
 #pragma unroll
-        for (int j = lane; j < DK; j += 64) {
-            const float v = ldg(x + j);
-            bad |= !is_finite(v);
-            rows[r * kStride + j] = v;
+    for (int k = 0; k < kLoads; ++k) {
+        const int idx = lane + 64 * k;
+        const int r = idx / kVec, c = idx % kVec;
+        if (r < count)
+            staged[k] = ldg4(source(s0 + r) + 4 * c);
+    }
+#pragma unroll
+    for (int k = 0; k < kLoads; ++k) {
+        const int idx = lane + 64 * k;
+        const int r = idx / kVec, c = idx % kVec;
+        if (r < count) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                bad |= !is_finite(staged[k][e]);
+            *(f4 *)(rows + r * kStride + 4 * c) = staged[k];
         }
     }
     __syncthreads();
@@ -107,36 +129,30 @@ __global__ __launch_bounds__(64) void head_transform_kernel(TransformParams p)
     }
     __syncthreads();
     for (int r = 0; r < count; ++r) {
-        int kind;
-        (void)source(r, kind);
-        const int64_t item = first + r;
-        const int64_t t = item / p.slots;
-        const int s = (int)(item - t * p.slots);
+        const int s = s0 + r;
+        const int kind = s < p.qheads ? 0 : s < p.qheads + p.kvh ? 1 : 2;
+        float *out = kind == 0   ? p.oq + (t * p.qheads + s) * DK
+                     : kind == 1 ? p.ok + t * p.o_kv_stride + (int64_t)(s - p.qheads) * DK
+                                 : p.ov + t * p.o_kv_stride + (int64_t)(s - p.qheads - p.kvh) * DK;
         const double iv = inv[r];
         const float *row = rows + r * kStride;
-        float *out;
-        const float *scale = nullptr;
-        if (kind == 0) {
-            out = p.oq + (t * p.qheads + s) * DK;
-            scale = p.qs;
-        } else if (kind == 1) {
-            out = p.ok + t * p.o_kv_stride + (int64_t)(s - p.qheads) * DK;
-            scale = p.ks;
-        } else {
-            out = p.ov + t * p.o_kv_stride + (int64_t)(s - p.qheads - p.kvh) * DK;
-        }
-        const float *tab = p.tab + (p.pos0 + t) * DK;
 #pragma unroll
-        for (int j = lane; j < kHalf; j += 64) {
+        for (int m = 0; m < kPairs; ++m) {
+            const int j = lane + 64 * m;
+            if (j >= kHalf)
+                continue;
             float a = (float)((double)row[j] * iv);
             float b = (float)((double)row[j + kHalf] * iv);
+            if (kind == 0) {
+                a = a * qa[m];
+                b = b * qb[m];
+            } else if (kind == 1) {
+                a = a * ka[m];
+                b = b * kb[m];
+            }
             if (kind != 2) {
-                a = a * ldg(scale + j);
-                b = b * ldg(scale + j + kHalf);
-                typedef float f2 __attribute__((ext_vector_type(2)));
-                const f2 sc = *(const __attribute__((address_space(1))) f2 *)(tab + 2 * j);
-                const float ac = a * sc.y, bs = b * sc.x;
-                const float bc = b * sc.y, as = a * sc.x;
+                const float ac = a * sc[m].y, bs = b * sc[m].x;
+                const float bc = b * sc[m].y, as = a * sc[m].x;
                 a = ac - bs;
                 b = bc + as;
             }
@@ -151,10 +167,9 @@ __global__ __launch_bounds__(64) void head_transform_kernel(TransformParams p)
 
 hipError_t launch_head_transform(const TransformParams &p, hipStream_t stream)
 {
-    const int64_t items = (int64_t)p.n * p.slots;
     auto go = [&](auto kernel, int per) {
-        const unsigned blocks = (unsigned)((items + per - 1) / per);
-        hipLaunchKernelGGL(kernel, dim3(blocks), dim3(64), 0, stream, p);
+        const dim3 grid((unsigned)p.n, (unsigned)((p.slots + per - 1) / per));
+        hipLaunchKernelGGL(kernel, grid, dim3(64), 0, stream, p);
         return hipGetLastError();
     };
     switch (p.dim) {
