@@ -53,7 +53,9 @@ constexpr int kRows = 16;
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kNegInf = -__builtin_huge_valf();
 
-enum ErrorBits { kErrScore = 1, kErrOutput = 2 };
+// Device error flag bits: a non-finite allowed score, a non-finite output, a
+// non-finite head-transform value.
+enum ErrorBits { kErrScore = 1, kErrOutput = 2, kErrTransform = 4 };
 
 // Launch parameters shared by every kernel (host fills, passed by value).
 struct Params {

@@ -30,8 +30,6 @@
 
 namespace pcl {
 
-constexpr int kErrTransform = 4; // non-finite head-transform input or output
-
 struct TransformParams {
     const float *rq, *rk, *rv; // raw rows [n][heads*dim]; rv null: V = raw K
     float *oq, *ok, *ov;       // outputs; ok null: query heads only
