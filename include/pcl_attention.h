@@ -20,7 +20,8 @@
  *      segments, asynchronous on a caller-visible stream);
  *   4. a device-resident layer cache whose rows the entry of 3 reads in
  *      place;
- *   5. the head transform that prepares Q, K and V rows for 3 and 4.
+ *   5. the head transform that prepares Q, K and V rows for 3 and 4;
+ *   6. the attention output block (projection, post-norm, residual).
  */
 #ifndef PCL_ATTENTION_H
 #define PCL_ATTENTION_H
@@ -166,7 +167,9 @@ int pcl_attention_launch(pcl_context *ctx, const pcl_attention_desc *desc);
 size_t pcl_attention_workspace_bytes(const pcl_attention_desc *desc);
 int pcl_context_reserve(pcl_context *ctx, size_t bytes);
 /* Wait for the stream; *device_error receives the error flag (bit 0: a
- * non-finite allowed score, bit 1: a non-finite output) and is cleared. */
+ * non-finite allowed score, bit 1: a non-finite output, bit 2: a non-finite
+ * head-transform value, bit 3: a non-finite output-block value) and is
+ * cleared. */
 int pcl_context_sync(pcl_context *ctx, int *device_error);
 /* Kernel the descriptor resolves to under PCL_KERNEL_AUTO. */
 int pcl_attention_resolve_kernel(const pcl_attention_desc *desc);
@@ -300,6 +303,23 @@ int pcl_head_transform_query(pcl_head_transform *transform, const float *raw_q, 
 int pcl_kv_cache_append_transformed(pcl_kv_cache *cache, pcl_head_transform *transform,
                                     const float *raw_q, const float *raw_k, const float *raw_v,
                                     int64_t n, float *q_out, pcl_kv_pending *pending);
+
+/* ---- 6. attention output block ---------------------------------------------
+ *
+ * The step after attention (src/engine/attention.rs:866-884): projected =
+ * W . attended with f32 weights [out][in] (Matrix::project / p9_ref_matvec,
+ * src/kernels/portable/reference.rs:36-78: f64 sums of exact f32 products),
+ * then result = residual + rms_norm(projected, post_scale, epsilon) in the
+ * engine's rounding (f64 norm, f32 scale and add). attended [n][in],
+ * residual, projected and result [n][out], post_scale [out]: device pointers;
+ * result may be the residual buffer. Asynchronous on the context's stream; a
+ * non-finite projected or result value sets bit 3 of the device error flag.
+ * The sums are f64 in the kernels' own order, so a value equals the engine's
+ * unless the two f64 sums fall on opposite sides of an f32 rounding
+ * boundary. */
+int pcl_attention_output(pcl_context *ctx, const float *attended, int64_t n, int64_t in,
+                         const float *weights, int64_t out, const float *post_scale,
+                         float epsilon, const float *residual, float *projected, float *result);
 
 /* Library identification (for loaders). */
 const char *pcl_version(void);

@@ -466,6 +466,27 @@ uint64_t oracle_libm_digest(int which)
     return h;
 }
 
+/* ---- output block primitives -------------------------------------------- */
+
+/* p9_ref_matvec (src/kernels/portable/reference.rs:36-78); its eight-row
+ * interleave does not change any row's sum. */
+void oracle_matvec(const float *matrix, const float *x, size_t rows, size_t cols, float *out)
+{
+    for (size_t r = 0; r < rows; ++r) {
+        double sum = 0.0;
+        for (size_t c = 0; c < cols; ++c)
+            sum += (double)matrix[r * cols + c] * (double)x[c];
+        out[r] = (float)sum;
+    }
+}
+
+/* p9_ref_add. */
+void oracle_add(const float *a, const float *b, size_t n, float *out)
+{
+    for (size_t i = 0; i < n; ++i)
+        out[i] = a[i] + b[i];
+}
+
 /* ---- threaded CPU baseline (the engine's decomposition) ---------------- */
 
 struct job {

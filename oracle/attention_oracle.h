@@ -133,6 +133,12 @@ bool oracle_rope(const float *x, size_t heads, size_t dim, size_t position, floa
  * reference's platform. */
 uint64_t oracle_libm_digest(int which);
 
+/* Output block primitives. p9_ref_matvec (src/kernels/portable/
+ * reference.rs:36-78): out[r] = f32(sequential f64 sum over c ascending of
+ * f64(m[r][c]) * f64(x[c])); p9_ref_add: out = a + b in f32. */
+void oracle_matvec(const float *matrix, const float *x, size_t rows, size_t cols, float *out);
+void oracle_add(const float *a, const float *b, size_t n, float *out);
+
 /* CPU baseline: the exact (a1) or binary32 (a3) path threaded as the engine
  * threads it (src/engine/attention.rs:755-836): one query's heads split
  * into ceil(qheads/split) ranges with split = clamp(workers/queries, 1,

@@ -271,3 +271,39 @@ def head_transform(raw_q, raw_k, raw_v, qheads, kvheads, dim, position, query_sc
     okq, q = rope(q, dim, position, base, factors)
     okk, k = rope(k, dim, position, base, factors)
     return okq and okk, q, k, v
+
+
+def _block_lib():
+    lib = _transform_lib()
+    if not getattr(lib, "_block_bound", False):
+        fp, sz = ctypes.POINTER(ctypes.c_float), ctypes.c_size_t
+        lib.oracle_matvec.restype = None
+        lib.oracle_matvec.argtypes = [fp, fp, sz, sz, fp]
+        lib.oracle_add.restype = None
+        lib.oracle_add.argtypes = [fp, fp, sz, fp]
+        lib._block_bound = True
+    return lib
+
+
+def matvec(matrix, x, rows, cols):
+    """p9_ref_matvec: [rows] f32."""
+    lib = _block_lib()
+    m, v = _f32(matrix), _f32(x)
+    out = np.zeros(rows, np.float32)
+    lib.oracle_matvec(_f(m), _f(v), rows, cols, _f(out))
+    return out
+
+
+def add(a, b):
+    lib = _block_lib()
+    a, b = _f32(a), _f32(b)
+    out = np.zeros(a.size, np.float32)
+    lib.oracle_add(_f(a), _f(b), a.size, _f(out))
+    return out
+
+
+def attention_output(attended, weights, post_scale, eps, residual, rows, cols):
+    """The output block of one token (src/engine/attention.rs:866-884):
+    (projected, residual + rms_norm(projected, post_scale, eps))."""
+    projected = matvec(weights, attended, rows, cols)
+    return projected, add(residual, rms_norm(projected, post_scale, eps))

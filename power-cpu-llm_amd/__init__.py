@@ -76,6 +76,7 @@ EXPORTS = (
     "pcl_head_transform_prepare",
     "pcl_head_transform_query",
     "pcl_kv_cache_append_transformed",
+    "pcl_attention_output",
     "pcl_version",
 )
 
@@ -199,7 +200,9 @@ def load():
             ("pcl_head_transform_prepare", ctypes.c_int, [vp, vp, vp, vp, i64, i64, vp, vp, vp]),
             ("pcl_head_transform_query", ctypes.c_int, [vp, vp, i64, i64, vp]),
             ("pcl_kv_cache_append_transformed", ctypes.c_int,
-             [vp, vp, vp, vp, vp, i64, vp, pend])):
+             [vp, vp, vp, vp, vp, i64, vp, pend]),
+            ("pcl_attention_output", ctypes.c_int,
+             [vp, vp, i64, i64, vp, i64, vp, ctypes.c_float, vp, vp, vp])):
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
@@ -396,6 +399,19 @@ class Context:
         if rc != OK:
             raise AttentionError(rc)
         return (ms[0], ms[1]), (n[0], n[1])
+
+    def attention_output(self, attended_ptr, n, in_width, weights_ptr, out_width,
+                         post_scale_ptr, epsilon, residual_ptr, projected_ptr, result_ptr):
+        """The attention output block (src/engine/attention.rs:866-884) on
+        device rows: projected = W . attended (W [out][in]), result =
+        residual + rms_norm(projected, post_scale, epsilon)."""
+        rc = self.lib.pcl_attention_output(
+            self.handle, ctypes.c_void_p(attended_ptr), int(n), int(in_width),
+            ctypes.c_void_p(weights_ptr), int(out_width), ctypes.c_void_p(post_scale_ptr),
+            float(epsilon), ctypes.c_void_p(residual_ptr), ctypes.c_void_p(projected_ptr),
+            ctypes.c_void_p(result_ptr))
+        if rc != OK:
+            raise AttentionError(rc)
 
     def sync(self):
         """Wait; returns the device error flag (cleared)."""

@@ -1,0 +1,314 @@
+// The attention output block on gfx950: projected = W_o . attended, then
+// result = residual + rms_norm(projected, post_scale) (src/engine/
+// attention.rs:866-884; project_streamed / project_streamed_batch_with over
+// p9_ref_matvec, src/kernels/portable/reference.rs:36-78).
+//
+// The engine's exact projection sums f64 products of f32 weights and inputs
+// (each product is exact in f64) per output row. Both projection kernels here
+// accumulate in f64 as well, in their own order, so a projected value is the
+// f32 rounding of nearly the same f64 sum: it equals the engine's except when
+// the two f64 sums straddle an f32 rounding boundary, and a sum like
+// 2^24 + 1 - 2^24 stays exact.
+//
+//   project_rows_kernel: few tokens (decode, verification). HBM-bound on the
+//     weights: one wave per output row streams the row once with 16-byte
+//     loads and keeps one f64 accumulator per token per lane; the tokens'
+//     inputs come from L2.
+//   project_tiles_kernel: many tokens (prompt). MFMA-bound: 128 x 128 output
+//     tiles, 32-column K steps double-buffered in LDS as f32, the products on
+//     v_mfma_f64_16x16x4f64 after converting the operands to f64.
+//   post_norm_kernel: one workgroup per token: the row's f64 sum of squares
+//     (per-thread partial sums, then a fixed tree), inv = 1/sqrt(ms + eps) in
+//     f64, y = f32(x * inv) * scale, result = residual + y (f32).
+#include "attention_device.hpp"
+#include "context.hpp"
+#include "pcl_attention.h"
+
+#include <cstdio>
+
+namespace pcl {
+
+constexpr int kErrBlock = 8; // non-finite value in the output block
+
+struct BlockParams {
+    const float *x;     // attended rows [n][in]
+    const float *w;     // weights [out][in]
+    float *proj;        // projected rows [n][out]
+    const float *scale; // post-norm scale [out]
+    const float *res;   // residual rows [n][out]
+    float *result;      // [n][out]
+    int n, in, out;
+    float eps;
+    int *err;
+};
+
+constexpr int kRowTokens = 16; // tokens per pass of the row kernel
+
+// One wave per output row; tokens [t0, t0 + 16) per launch pass.
+__global__ __launch_bounds__(256) void project_rows_kernel(BlockParams p, int t0)
+{
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= p.out)
+        return;
+    const int nt = p.n - t0 < kRowTokens ? p.n - t0 : kRowTokens;
+    const float *wr = p.w + (int64_t)r * p.in;
+    double acc[kRowTokens];
+#pragma unroll
+    for (int t = 0; t < kRowTokens; ++t)
+        acc[t] = 0.0;
+    // 16-byte steps of the row, 4 in flight per lane
+    const int vecs = p.in / 4;
+    int v = lane;
+    for (; v + 192 < vecs; v += 256) {
+        f4 wv[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            wv[k] = ldg4_stream(wr + 4 * (v + 64 * k));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+#pragma unroll
+            for (int t = 0; t < kRowTokens; ++t) {
+                if (t < nt) {
+                    const f4 xv = ldg4(p.x + (int64_t)(t0 + t) * p.in + 4 * (v + 64 * k));
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        acc[t] = __builtin_fma((double)wv[k][e], (double)xv[e], acc[t]);
+                }
+            }
+        }
+    }
+    for (; v < vecs; v += 64) {
+        const f4 wv = ldg4_stream(wr + 4 * v);
+#pragma unroll
+        for (int t = 0; t < kRowTokens; ++t) {
+            if (t < nt) {
+                const f4 xv = ldg4(p.x + (int64_t)(t0 + t) * p.in + 4 * v);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc[t] = __builtin_fma((double)wv[e], (double)xv[e], acc[t]);
+            }
+        }
+    }
+    // columns past the last whole 16-byte step
+    for (int c = 4 * vecs + lane; c < p.in; c += 64) {
+        const double wc = (double)ldg(wr + c);
+#pragma unroll
+        for (int t = 0; t < kRowTokens; ++t)
+            if (t < nt)
+                acc[t] = __builtin_fma(wc, (double)ldg(p.x + (int64_t)(t0 + t) * p.in + c), acc[t]);
+    }
+#pragma unroll
+    for (int t = 0; t < kRowTokens; ++t) {
+        double s = acc[t];
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1)
+            s += __shfl_xor(s, o);
+        acc[t] = s;
+    }
+    if (lane < nt) {
+        double mine = 0.0;
+#pragma unroll
+        for (int t = 0; t < kRowTokens; ++t)
+            mine = lane == t ? acc[t] : mine;
+        stg(p.proj + (int64_t)(t0 + lane) * p.out + r, (float)mine);
+    }
+}
+
+// 128 x 128 output tile per 256-thread workgroup (2 x 2 waves of 64 x 64),
+// K in steps of 32 columns, LDS rows padded to 36 floats (16-byte aligned,
+// and the 16 rows an MFMA operand read touches fall in distinct banks).
+constexpr int kTileM = 128, kTileN = 128, kTileK = 32, kLdsRow = 36;
+
+typedef double d4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256, 1) void project_tiles_kernel(BlockParams p)
+{
+    __shared__ __attribute__((aligned(16))) float sa[2][kTileM * kLdsRow];
+    __shared__ __attribute__((aligned(16))) float sb[2][kTileN * kLdsRow];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int m0 = blockIdx.y * kTileM, n0 = blockIdx.x * kTileN;
+
+    // global -> registers -> LDS: each thread moves 4 float4 of A and 4 of B
+    // per K step; the next step's loads are in flight during this step's MFMAs
+    f4 ra[4], rb[4];
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int idx = tid + 256 * i; // row = idx / 8, quad = idx % 8
+            const int row = idx >> 3, q = idx & 7;
+            const int k = k0 + 4 * q;
+            ra[i] = f4{0.f, 0.f, 0.f, 0.f};
+            rb[i] = f4{0.f, 0.f, 0.f, 0.f};
+            if (m0 + row < p.n) {
+                const float *src = p.x + (int64_t)(m0 + row) * p.in;
+                if (k + 3 < p.in)
+                    ra[i] = ldg4(src + k);
+                else
+                    for (int e = 0; e < 4; ++e)
+                        ra[i][e] = k + e < p.in ? ldg(src + k + e) : 0.f;
+            }
+            if (n0 + row < p.out) {
+                const float *src = p.w + (int64_t)(n0 + row) * p.in;
+                if (k + 3 < p.in)
+                    rb[i] = ldg4_stream(src + k);
+                else
+                    for (int e = 0; e < 4; ++e)
+                        rb[i][e] = k + e < p.in ? ldg(src + k + e) : 0.f;
+            }
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int idx = tid + 256 * i;
+            const int row = idx >> 3, q = idx & 7;
+            *(f4 *)(sa[buf] + row * kLdsRow + 4 * q) = ra[i];
+            *(f4 *)(sb[buf] + row * kLdsRow + 4 * q) = rb[i];
+        }
+    };
+
+    d4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            acc[i][j] = d4{0.0, 0.0, 0.0, 0.0};
+
+    const int steps = (p.in + kTileK - 1) / kTileK;
+    load(0);
+    store(0);
+    __syncthreads();
+    const int r16 = lane & 15, kq = lane >> 4;
+    for (int s = 0; s < steps; ++s) {
+        const int buf = s & 1;
+        if (s + 1 < steps)
+            load((s + 1) * kTileK);
+#pragma unroll
+        for (int kc = 0; kc < kTileK; kc += 16) {
+            // MFMA k slot kq of step j holds column kc + 4 kq + j
+            f4 a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                a[i] = *(const f4 *)(sa[buf] + (wm + 16 * i + r16) * kLdsRow + kc + 4 * kq);
+                b[i] = *(const f4 *)(sb[buf] + (wn + 16 * i + r16) * kLdsRow + kc + 4 * kq);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj)
+                        acc[i][jj] = __builtin_amdgcn_mfma_f64_16x16x4f64(
+                            (double)a[i][j], (double)b[jj][j], acc[i][jj], 0, 0, 0);
+        }
+        if (s + 1 < steps)
+            store(buf ^ 1); // read last in step s - 1, before that step's barrier
+        __syncthreads();
+    }
+    // acc[i][jj][e]: row wm + 16i + kq + 4e, column wn + 16 jj + r16 (the f64
+    // MFMA's output rows interleave by lane group, unlike the f32 one's)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int row = m0 + wm + 16 * i + kq + 4 * e;
+            if (row >= p.n)
+                continue;
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const int col = n0 + wn + 16 * jj + r16;
+                if (col < p.out)
+                    stg(p.proj + (int64_t)row * p.out + col, (float)acc[i][jj][e]);
+            }
+        }
+}
+
+// One 256-thread workgroup per token row.
+__global__ __launch_bounds__(256) void post_norm_kernel(BlockParams p)
+{
+    __shared__ double part[256];
+    __shared__ double inv_s;
+    const int t = blockIdx.x;
+    const int tid = threadIdx.x;
+    const float *x = p.proj + (int64_t)t * p.out;
+    double sum = 0.0;
+    bool bad = false;
+    for (int c = tid; c < p.out; c += 256) {
+        const float v = ldg(x + c);
+        bad |= !is_finite(v);
+        sum = __builtin_fma((double)v, (double)v, sum);
+    }
+    part[tid] = sum;
+    __syncthreads();
+    for (int o = 128; o >= 1; o >>= 1) {
+        if (tid < o)
+            part[tid] = part[tid] + part[tid + o];
+        __syncthreads();
+    }
+    if (tid == 0)
+        inv_s = 1.0 / __builtin_sqrt(part[0] / (double)p.out + (double)p.eps);
+    __syncthreads();
+    const double inv = inv_s;
+    const float *res = p.res + (int64_t)t * p.out;
+    float *y = p.result + (int64_t)t * p.out;
+    for (int c = tid; c < p.out; c += 256) {
+        const float normed = (float)((double)ldg(x + c) * inv) * ldg(p.scale + c);
+        const float r = ldg(res + c) + normed;
+        bad |= !is_finite(r);
+        stg(y + c, r);
+    }
+    if (bad)
+        atomicOr(p.err, kErrBlock);
+}
+
+hipError_t launch_output_block(const BlockParams &p, hipStream_t stream)
+{
+    if (p.n <= 2 * kRowTokens) {
+        for (int t0 = 0; t0 < p.n; t0 += kRowTokens)
+            hipLaunchKernelGGL(project_rows_kernel, dim3((p.out + 3) / 4), dim3(256), 0, stream,
+                               p, t0);
+    } else {
+        const dim3 grid((p.out + kTileN - 1) / kTileN, (p.n + kTileM - 1) / kTileM);
+        hipLaunchKernelGGL(project_tiles_kernel, grid, dim3(256), 0, stream, p);
+    }
+    hipLaunchKernelGGL(post_norm_kernel, dim3(p.n), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+} // namespace pcl
+
+extern "C" int pcl_attention_output(pcl_context *ctx, const float *attended, int64_t n,
+                                    int64_t in, const float *weights, int64_t out,
+                                    const float *post_scale, float epsilon,
+                                    const float *residual, float *projected, float *result)
+{
+    if (!ctx || !attended || !weights || !post_scale || !residual || !projected || !result)
+        return PCL_INVALID_SHAPE;
+    if (n <= 0 || in <= 0 || out <= 0 || n > (1 << 24) || in > (1 << 20) || out > (1 << 20))
+        return PCL_INVALID_SHAPE;
+    if (!(epsilon > 0.0f) || !__builtin_isfinite(epsilon))
+        return PCL_INVALID_PARAMETER;
+    (void)hipSetDevice(ctx->device);
+    pcl::BlockParams p{};
+    p.x = attended;
+    p.w = weights;
+    p.proj = projected;
+    p.scale = post_scale;
+    p.res = residual;
+    p.result = result;
+    p.n = (int)n;
+    p.in = (int)in;
+    p.out = (int)out;
+    p.eps = epsilon;
+    p.err = ctx->err;
+    const hipError_t e = pcl::launch_output_block(p, ctx->stream);
+    if (e != hipSuccess) {
+        std::fprintf(stderr, "pcl_attention_output: launch: %s\n", hipGetErrorString(e));
+        return PCL_NON_FINITE_VALUE;
+    }
+    return PCL_OK;
+}
