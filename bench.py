@@ -24,6 +24,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
 FP32_MFMA_PEAK_TFS = 157.3   # MI355X dense fp32 matrix, TFLOP/s
+FP64_MFMA_PEAK_TFS = 78.6    # MI355X dense fp64 matrix, TFLOP/s
 
 
 def load_package():
@@ -59,6 +60,11 @@ WORKLOADS = {
     # projections: transform fused with the cache append, then attention
     "transform_4k": (16, 8, 256, 4096, 0, True, 0, 0, "transform", False),
     "decode_32k_step": (16, 8, 256, 1, 32768, True, 0, 32767, "step", False),
+    # the attention output block (projection of the 16 x 256 attended heads
+    # to a 2816-wide hidden row, post-norm, residual) for one decode token and
+    # for a 4K-token prompt; here `nkeys` is the hidden width
+    "output_decode": (16, 8, 256, 1, 2816, False, 0, 0, "output", False),
+    "output_4k": (16, 8, 256, 4096, 2816, False, 0, 0, "output", False),
 }
 HEADLINE = "decode_32k"
 
@@ -75,6 +81,10 @@ def traffic_bytes(name):
         if len(f) == 3 and f[0] == "traffic_bytes" and f[1] == name:
             return int(f[2])
     return None
+
+
+def nq_of(name):
+    return WORKLOADS[name][3]
 
 
 def allowed_pairs(nq, nkeys, causal, window, first_query):
@@ -96,6 +106,10 @@ def work(name):
         # raw Q/K/V rows read, prepared rows written, (sin, cos) table rows read
         heads = qh + 2 * kvh
         return 0, nq * (2 * heads * dim * 4 + dim * 4), 0
+    if kind == "output":
+        # weights and attended rows read, residual read, result written
+        width, hidden = qh * dim, nkeys
+        return 2 * nq * width * hidden, 4 * (width * hidden + nq * width + 2 * nq * hidden), 0
     pairs = allowed_pairs(nq, nkeys, causal, window, fq)
     flops = 4 * dim * pairs * qh
     # decode bytes: attended K and V rows of every KV head, plus Q and O
@@ -158,6 +172,8 @@ def time_workload(torch, pcl, ctx, name, steps, warmup, seed=0, kernel=0):
                                    transform=True)
     if kind == "transform":
         return time_transform_workload(torch, pcl, ctx, name, steps, warmup, seed)
+    if kind == "output":
+        return time_output_workload(torch, pcl, ctx, name, steps, warmup, seed)
     sets = []
     for i in range(nsets):
         q, k, v = make_inputs(torch, name, seed + 1000 * i)
@@ -251,6 +267,52 @@ def time_transform_workload(torch, pcl, ctx, name, steps, warmup, seed):
     t.close()
     roles = {"stream_ms": ev, "combine_ms": 0.0}
     return ev, wall, "head_transform", None, roles, nsets
+
+
+def time_output_workload(torch, pcl, ctx, name, steps, warmup, seed):
+    """The output block of nq tokens (weights [hidden][qheads*dim], seeded
+    N(0, 1/width)); each timed call reads its own weight and input set."""
+    qh, kvh, dim, nq, hidden, causal, window, fq, kind, _ = WORKLOADS[name]
+    width = qh * dim
+    set_bytes = 4 * (width * hidden + nq * width + 3 * nq * hidden)
+    nsets = max(2, min(MAX_SETS, -(-CYCLE_BYTES // set_bytes)))
+    dev = torch.device("cuda:0")
+    sets = []
+    for i in range(nsets):
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(0x5EED0800 + seed + i)
+        w = torch.randn((hidden, width), generator=gen, device=dev) * (1.0 / math.sqrt(width))
+        x = torch.randn((nq, width), generator=gen, device=dev)
+        res = torch.randn((nq, hidden), generator=gen, device=dev)
+        scale = 1 + 0.1 * torch.randn(hidden, generator=gen, device=dev)
+        proj = torch.empty((nq, hidden), device=dev)
+        out = torch.empty((nq, hidden), device=dev)
+        sets.append((w, x, res, scale, proj, out))
+
+    def step(i):
+        w, x, res, scale, proj, out = sets[i % nsets]
+        ctx.attention_output(x.data_ptr(), nq, width, w.data_ptr(), hidden, scale.data_ptr(),
+                             1e-6, res.data_ptr(), proj.data_ptr(), out.data_ptr())
+
+    for i in range(max(warmup, nsets)):
+        step(i)
+    torch.cuda.synchronize()
+    if ctx.sync():
+        raise RuntimeError("device error flag set for %s" % name)
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for i in range(steps):
+        step(i)
+    stop.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    ev = start.elapsed_time(stop) / steps
+    if ctx.sync():
+        raise RuntimeError("device error flag set for %s" % name)
+    kernel = "project_rows" if nq <= 32 else "project_tiles"
+    return ev, wall, kernel, None, {"stream_ms": ev, "combine_ms": 0.0}, nsets
 
 
 def time_cache_workload(torch, pcl, ctx, name, steps, warmup, nsets, seed, transform=False):
@@ -400,7 +462,9 @@ def main():
              "algorithmic_bytes": bytes_, "algorithmic_flops": flops}
         r["GB/s"] = bytes_ / (ev * 1e-3) / 1e9
         r["TFLOP/s"] = flops / (ev * 1e-3) / 1e12
-        if kind in ("decode", "cache", "step", "transform"):
+        if kind == "output" and nq_of(name) > 32:
+            r["frac_mfma_fp64"] = r["TFLOP/s"] / FP64_MFMA_PEAK_TFS
+        elif kind in ("decode", "cache", "step", "transform", "output"):
             r["frac_hbm"] = r["GB/s"] / HBM_PEAK_GBS
         else:
             r["frac_mfma"] = r["TFLOP/s"] / FP32_MFMA_PEAK_TFS

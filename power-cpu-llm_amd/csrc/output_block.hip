@@ -12,14 +12,15 @@
 //
 //   project_rows_kernel: few tokens (decode, verification). HBM-bound on the
 //     weights: one wave per output row streams the row once with 16-byte
-//     loads and keeps one f64 accumulator per token per lane; the tokens'
-//     inputs come from L2.
+//     loads, 4096 columns in flight at a time, and keeps one f64 accumulator
+//     per token per lane; the tokens' inputs come from L2.
 //   project_tiles_kernel: many tokens (prompt). MFMA-bound: 128 x 128 output
 //     tiles, 32-column K steps double-buffered in LDS as f32, the products on
 //     v_mfma_f64_16x16x4f64 after converting the operands to f64.
 //   post_norm_kernel: one workgroup per token: the row's f64 sum of squares
-//     (per-thread partial sums, then a fixed tree), inv = 1/sqrt(ms + eps) in
-//     f64, y = f32(x * inv) * scale, result = residual + y (f32).
+//     (per-thread partial sums, then a fixed tree of lane shuffles and the
+//     four waves), inv = 1/sqrt(ms + eps) in f64, y = f32(x * inv) * scale,
+//     result = residual + y (f32).
 #include "attention_device.hpp"
 #include "context.hpp"
 #include "pcl_attention.h"
@@ -57,16 +58,17 @@ __global__ __launch_bounds__(256) void project_rows_kernel(BlockParams p, int t0
 #pragma unroll
     for (int t = 0; t < kRowTokens; ++t)
         acc[t] = 0.0;
-    // 16-byte steps of the row, 4 in flight per lane
+    // 16-byte steps of the row: 4096 columns (16 per lane) in flight at once,
+    // so a wave's row costs one memory round trip
     const int vecs = p.in / 4;
     int v = lane;
-    for (; v + 192 < vecs; v += 256) {
-        f4 wv[4];
+    for (; v + 960 < vecs; v += 1024) {
+        f4 wv[16];
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
+        for (int k = 0; k < 16; ++k)
             wv[k] = ldg4_stream(wr + 4 * (v + 64 * k));
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < 16; ++k) {
 #pragma unroll
             for (int t = 0; t < kRowTokens; ++t) {
                 if (t < nt) {
@@ -100,11 +102,13 @@ __global__ __launch_bounds__(256) void project_rows_kernel(BlockParams p, int t0
     }
 #pragma unroll
     for (int t = 0; t < kRowTokens; ++t) {
-        double s = acc[t];
+        if (t < nt) {
+            double s = acc[t];
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1)
-            s += __shfl_xor(s, o);
-        acc[t] = s;
+            for (int o = 32; o >= 1; o >>= 1)
+                s += __shfl_xor(s, o);
+            acc[t] = s;
+        }
     }
     if (lane < nt) {
         double mine = 0.0;
@@ -227,39 +231,68 @@ __global__ __launch_bounds__(256, 1) void project_tiles_kernel(BlockParams p)
         }
 }
 
-// One 256-thread workgroup per token row.
+// One 256-thread workgroup per token row; rows up to 4096 wide stay in
+// registers between the sum of squares and the output.
+constexpr int kNormPer = 16;
+
 __global__ __launch_bounds__(256) void post_norm_kernel(BlockParams p)
 {
-    __shared__ double part[256];
-    __shared__ double inv_s;
+    __shared__ double part[4];
     const int t = blockIdx.x;
     const int tid = threadIdx.x;
     const float *x = p.proj + (int64_t)t * p.out;
-    double sum = 0.0;
-    bool bad = false;
-    for (int c = tid; c < p.out; c += 256) {
-        const float v = ldg(x + c);
-        bad |= !is_finite(v);
-        sum = __builtin_fma((double)v, (double)v, sum);
-    }
-    part[tid] = sum;
-    __syncthreads();
-    for (int o = 128; o >= 1; o >>= 1) {
-        if (tid < o)
-            part[tid] = part[tid] + part[tid + o];
-        __syncthreads();
-    }
-    if (tid == 0)
-        inv_s = 1.0 / __builtin_sqrt(part[0] / (double)p.out + (double)p.eps);
-    __syncthreads();
-    const double inv = inv_s;
     const float *res = p.res + (int64_t)t * p.out;
     float *y = p.result + (int64_t)t * p.out;
-    for (int c = tid; c < p.out; c += 256) {
-        const float normed = (float)((double)ldg(x + c) * inv) * ldg(p.scale + c);
-        const float r = ldg(res + c) + normed;
-        bad |= !is_finite(r);
-        stg(y + c, r);
+    const bool cached = p.out <= 256 * kNormPer;
+    float xv[kNormPer], rv[kNormPer], sv[kNormPer];
+    double sum = 0.0;
+    bool bad = false;
+    if (cached) {
+#pragma unroll
+        for (int k = 0; k < kNormPer; ++k) {
+            const int c = tid + 256 * k;
+            xv[k] = c < p.out ? ldg(x + c) : 0.f;
+            rv[k] = c < p.out ? ldg(res + c) : 0.f;
+            sv[k] = c < p.out ? ldg(p.scale + c) : 0.f;
+        }
+#pragma unroll
+        for (int k = 0; k < kNormPer; ++k) {
+            bad |= !is_finite(xv[k]);
+            sum = __builtin_fma((double)xv[k], (double)xv[k], sum);
+        }
+    } else {
+        for (int c = tid; c < p.out; c += 256) {
+            const float v = ldg(x + c);
+            bad |= !is_finite(v);
+            sum = __builtin_fma((double)v, (double)v, sum);
+        }
+    }
+    // the block's sum: a fixed tree over lanes, then over the four waves
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+        sum += __shfl_xor(sum, o);
+    if ((tid & 63) == 0)
+        part[tid >> 6] = sum;
+    __syncthreads();
+    const double total = (part[0] + part[1]) + (part[2] + part[3]);
+    const double inv = 1.0 / __builtin_sqrt(total / (double)p.out + (double)p.eps);
+    if (cached) {
+#pragma unroll
+        for (int k = 0; k < kNormPer; ++k) {
+            const int c = tid + 256 * k;
+            if (c < p.out) {
+                const float r = rv[k] + (float)((double)xv[k] * inv) * sv[k];
+                bad |= !is_finite(r);
+                stg(y + c, r);
+            }
+        }
+    } else {
+        for (int c = tid; c < p.out; c += 256) {
+            const float normed = (float)((double)ldg(x + c) * inv) * ldg(p.scale + c);
+            const float r = ldg(res + c) + normed;
+            bad |= !is_finite(r);
+            stg(y + c, r);
+        }
     }
     if (bad)
         atomicOr(p.err, kErrBlock);
