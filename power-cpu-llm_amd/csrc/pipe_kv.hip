@@ -11,7 +11,16 @@
 // wave reads Q^T from LDS so its registers can hold the 32 KiB K block.
 //
 // Each wave keeps exactly one 16-key block of K or V in flight, loading the
-// next block into the same registers as soon as its MFMAs have consumed them.
+// next block into the same registers as its MFMAs consume them: each 32-dim
+// K slice (each 4-key V slice) is reloaded right after the MFMAs that read
+// it, so a block's MFMA time overlaps the next block's memory latency
+// (issuing the whole next block only after the last MFMA cost ~10 % at 32K).
+// Head dim 512 keeps whole-block reloads: there the earlier issue made the
+// 128K decode 40 % slower (its 32 KiB K blocks then overlap in flight).
+template <int DK> constexpr bool pipe_slice_loads()
+{
+    return DK <= 256;
+}
 // Measured on MI355X with inputs larger than the last-level cache, one block
 // in flight per wave streams at the HBM limit (~6.9 TB/s for a pure K+V read)
 // even with a microsecond of compute between loads, while two blocks in
@@ -105,6 +114,26 @@ __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, i
     constexpr int PU = PD / 32; // u-steps per piece
     constexpr int PB = DK / PD; // pieces per 16-key block
     f4 kb[PU][2];
+    auto load_k_u = [&](int t, int b, int pc, int uu) {
+        const int64_t key = cbase + t * kTile + 16 * b + col;
+        const float *kp = key_row(p, key < klast ? key : klast) + hoff;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int d = 32 * (pc * PU + uu) + 8 * g + 4 * h;
+            const bool din = FULL || d < p.dim;
+            const f4 x = ldg4_stream(kp + (din ? d : 0));
+            kb[uu][h] = din ? x : f4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    // slice uu of the piece after (t, b, pc), if any
+    auto load_next_u = [&](int t, int b, int pc, int uu) {
+        if (pc + 1 < PB)
+            load_k_u(t, b, pc + 1, uu);
+        else if (b == 0)
+            load_k_u(t, 1, 0, uu);
+        else if (t + 1 < kTilesPerChunk)
+            load_k_u(t + 1, 0, 0, uu);
+    };
     auto load_k = [&](int t, int b, int pc) {
         const int64_t key = cbase + t * kTile + 16 * b + col;
         const float *kp = key_row(p, key < klast ? key : klast) + hoff;
@@ -160,16 +189,23 @@ __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, i
 #pragma unroll
                         for (int jj = 0; jj < 8; ++jj)
                             acc[b] = mfma(kb[uu][jj >> 2][jj & 3], qv[jj], acc[b]);
+                        if constexpr (pipe_slice_loads<DK>()) {
+                            // this slice's registers are consumed: the next piece's slice
+                            __builtin_amdgcn_sched_barrier(0);
+                            load_next_u(t, b, pc, uu);
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
                     }
                 }
                 __builtin_amdgcn_sched_barrier(0);
-                // the next piece into the registers just consumed
-                if (pc + 1 < PB)
-                    load_k(t, b, pc + 1);
-                else if (b == 0)
-                    load_k(t, 1, 0);
-                else if (t + 1 < kTilesPerChunk)
-                    load_k(t + 1, 0, 0);
+                if (!tile_any || !pipe_slice_loads<DK>()) { // the whole next piece at once
+                    if (pc + 1 < PB)
+                        load_k(t, b, pc + 1);
+                    else if (b == 0)
+                        load_k(t, 1, 0);
+                    else if (t + 1 < kTilesPerChunk)
+                        load_k(t + 1, 0, 0);
+                }
             }
         float pr[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
         float alpha = 1.f, rs = 0.f;
@@ -231,6 +267,25 @@ __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, i
 
     const int dv = d0 + 4 * col; // + 64a
     f4 vv[4][NQ];           // the half tile in flight: [slice][64-dim group]
+    auto load_v_sl = [&](int t, int half, int sl) {
+        const int br = 4 * half + sl;
+        const int64_t key = cbase + t * kTile + 16 * (br >> 2) + 4 * g + (br & 3);
+        const float *vp = value_row(p, key < klast ? key : klast) + hoff;
+#pragma unroll
+        for (int a = 0; a < NQ; ++a) {
+            const int d = 64 * a + dv;
+            const bool din = FULL || d < p.dim;
+            const f4 x = ldg4_stream(vp + (din ? d : 0));
+            vv[sl][a] = din ? x : f4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    // slice sl of the half tile after (t, half), if any
+    auto load_next_sl = [&](int t, int half, int sl) {
+        if (half == 0)
+            load_v_sl(t, 1, sl);
+        else if (t + 1 < kTilesPerChunk)
+            load_v_sl(t + 1, 0, sl);
+    };
     auto load_v = [&](int t, int half) {
 #pragma unroll
         for (int sl = 0; sl < 4; ++sl) {
@@ -280,14 +335,21 @@ __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, i
 #pragma unroll
                         for (int j = 0; j < 4; ++j)
                             O[a][j] = mfma(vv[sl][a][j], pb, O[a][j]);
+                    if constexpr (pipe_slice_loads<DK>()) {
+                        // this slice's registers are consumed: the next half tile's slice
+                        __builtin_amdgcn_sched_barrier(0);
+                        load_next_sl(t, half, sl);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
-            // the next half tile into the registers just consumed
-            if (half == 0)
-                load_v(t, 1);
-            else if (t + 1 < kTilesPerChunk)
-                load_v(t + 1, 0);
+            if (!tile_any || !pipe_slice_loads<DK>()) { // the whole next half tile at once
+                if (half == 0)
+                    load_v(t, 1);
+                else if (t + 1 < kTilesPerChunk)
+                    load_v(t + 1, 0);
+            }
         }
         __syncthreads(); // tile t + 1 handed over (the last one: the chunk maximum)
     }
