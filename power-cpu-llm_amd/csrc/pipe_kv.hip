@@ -39,6 +39,16 @@ template <int DK> constexpr int pipe_value_waves()
     return DK > 256 ? DK / 256 : 1;
 }
 
+// Score waves per workgroup. Above head dim 256 a tile's K is as many bytes
+// as its V, which two value waves stream: two score waves then stream K, one
+// per 16-key block of each tile (the second runs a tile ahead and hands its
+// raw scores to the first, which owns the softmax), so K and V have the same
+// bytes in flight.
+template <int DK> constexpr int pipe_score_waves()
+{
+    return DK > 256 ? 2 : 1;
+}
+
 // Head dims above 256 keep Q^T in LDS (the score wave's registers hold the K
 // block in flight); padded rows avoid bank conflicts.
 template <int DK> constexpr bool pipe_q_lds()
@@ -54,6 +64,9 @@ template <int DK> struct PipeLds {
     int any[2];
     float m[kRows];       // chunk maximum
     float q[pipe_q_lds<DK>() ? kRows * (DK + 4) : 1];
+    // raw scores of a tile's second 16-key block from the second score
+    // wave, [tile & 1][r][lane]
+    float sb[pipe_score_waves<DK>() > 1 ? 2 : 1][4][64];
 };
 
 template <int DK, bool FULL>
@@ -247,15 +260,190 @@ __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, i
     __syncthreads(); // chunk maximum handed over
 }
 
+// The two score waves of head dims above 256. ROLE 0 scores the first 16-key
+// block of every tile and runs the tile's softmax; ROLE 1 scores the second
+// block one tile ahead and leaves its raw scores in s.sb. Each block's score
+// chain is the canonical one, so the results equal the one-wave kernel's.
+// Barriers (the value waves keep the same count): #Q after Q^T is staged,
+// #0 after the second wave's tile-0 scores, #t+1 after tile t is handed over,
+// and one after the chunk maximum.
+template <int DK, bool FULL, int ROLE>
+__device__ __forceinline__ void score_wave_dual(const Params &p, int unit, int kvl, int c,
+                                                PipeLds<DK> &s)
+{
+    static_assert(pipe_q_lds<DK>(), "the two score waves share Q^T in LDS");
+    constexpr int QLD = DK + 4;
+    constexpr int PD = 256;     // dims per K piece
+    constexpr int PU = PD / 32; // u-steps per piece
+    constexpr int PB = DK / PD; // pieces per 16-key block
+    const int lane = threadIdx.x & 63;
+    const int col = lane & 15;
+    const int g = lane >> 4;
+    const int kh = p.kh_first + kvl;
+    const int row = unit * kRows + col;
+    const int64_t cbase = (int64_t)c * kChunk;
+    const int64_t klast = p.nkeys - 1;
+    const int64_t hoff = (int64_t)kh * p.dim;
+
+    // Q^T, staged by both score waves
+    for (int i = lane + 64 * ROLE; i < kRows * (DK / 4); i += 128) {
+        const int r = i / (DK / 4);
+        const int d = (i % (DK / 4)) * 4;
+        const int f = unit * kRows + r;
+        f4 v = f4{0.f, 0.f, 0.f, 0.f};
+        if (f < p.nrows && d < p.dim) {
+            const int qq = f / p.group;
+            const int hh = kh * p.group + f % p.group;
+            v = ldg4(p.q + (int64_t)qq * p.q_stride + (int64_t)hh * p.dim + d) * p.q_scale;
+        }
+        *(f4 *)(s.q + r * QLD + d) = v;
+    }
+    __syncthreads(); // #Q: Q^T staged
+
+    f4 kb[PU][2]; // the K piece in flight: 16 keys (this wave's block) x 256 dims
+    auto load_k = [&](int t, int pc) {
+        const int64_t key = cbase + t * kTile + 16 * ROLE + col;
+        const float *kp = key_row(p, key < klast ? key : klast) + hoff;
+#pragma unroll
+        for (int uu = 0; uu < PU; ++uu)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int d = 32 * (pc * PU + uu) + 8 * g + 4 * h;
+                const bool din = FULL || d < p.dim;
+                const f4 x = ldg4_stream(kp + (din ? d : 0));
+                kb[uu][h] = din ? x : f4{0.f, 0.f, 0.f, 0.f};
+            }
+    };
+    // this wave's block of tile t: its canonical score chain (run: any key of
+    // the block allowed for the unit), the next piece loaded as registers free
+    auto chain = [&](int t, bool run) {
+        f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int pc = 0; pc < PB; ++pc) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (run) {
+#pragma unroll
+                for (int uu = 0; uu < PU; ++uu) {
+                    const int u = pc * PU + uu;
+                    const f4 qa0 = *(const f4 *)(s.q + col * QLD + 32 * u + 8 * g);
+                    const f4 qa1 = *(const f4 *)(s.q + col * QLD + 32 * u + 8 * g + 4);
+                    float qv[8];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        qv[j] = qa0[j];
+                        qv[4 + j] = qa1[j];
+                    }
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj)
+                        acc = mfma(kb[uu][jj >> 2][jj & 3], qv[jj], acc);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (pc + 1 < PB)
+                load_k(t, pc + 1);
+            else if (t + 1 < kTilesPerChunk)
+                load_k(t + 1, 0);
+        }
+        return acc;
+    };
+    // whether any key of this wave's block of tile t is allowed for the unit
+    auto block_any = [&](int t, bool ok[4]) {
+        bool any = false;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            ok[r] = allowed(p, row, cbase + t * kTile + 16 * ROLE + 4 * g + r);
+            any |= ok[r];
+        }
+        return (bool)__any(any);
+    };
+
+    load_k(0, 0);
+    if constexpr (ROLE == 1) {
+        {
+            bool ok[4];
+            const f4 acc = chain(0, block_any(0, ok));
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                s.sb[0][r][lane] = acc[r];
+        }
+        __syncthreads(); // #0: tile 0's second block scored
+#pragma unroll 1
+        for (int t = 0; t < kTilesPerChunk; ++t) {
+            if (t + 1 < kTilesPerChunk) {
+                bool ok[4];
+                const f4 acc = chain(t + 1, block_any(t + 1, ok));
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    s.sb[(t + 1) & 1][r][lane] = acc[r];
+            }
+            __syncthreads(); // #t+1
+        }
+        __syncthreads(); // chunk maximum
+        return;
+    }
+    __syncthreads(); // #0
+    float m = kNegInf;
+    bool bad = false;
+#pragma unroll 1
+    for (int t = 0; t < kTilesPerChunk; ++t) {
+        bool ok[2][4];
+        bool any1 = false;
+        const bool any0 = block_any(t, ok[0]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            ok[1][r] = allowed(p, row, cbase + t * kTile + 16 + 4 * g + r);
+            any1 |= ok[1][r];
+        }
+        const bool tile_any = any0 || __any(any1);
+        const f4 acc0 = chain(t, any0);
+        float pr[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        float alpha = 1.f, rs = 0.f;
+        if (tile_any) {
+            float sc[2][4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                sc[0][r] = acc0[r];
+                sc[1][r] = s.sb[t & 1][r][lane];
+            }
+            bad |= bad_scores(sc, ok);
+            const float mn = fmaxf(m, tile_max(sc, ok));
+            const float ms = safe_max(mn);
+            alpha = fexp(m - ms);
+            rs = tile_probs(sc, ok, ms, pr);
+            m = mn;
+        } else {
+            alpha = fexp(m - safe_max(m));
+        }
+        const int slot = t & 1;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                s.p[slot][4 * b + r][lane] = pr[b][r];
+        if (g == 0) {
+            s.alpha[slot][col] = alpha;
+            s.rs[slot][col] = rs;
+        }
+        if (lane == 0)
+            s.any[slot] = tile_any;
+        __syncthreads(); // #t+1: tile t handed over
+    }
+    if (g == 0)
+        s.m[col] = m;
+    if (bad)
+        atomicOr(p.err, kErrScore);
+    __syncthreads(); // chunk maximum handed over
+}
+
 // Output modes of the pipelined kernel.
 enum PipeMode { kDirect = 0, kPartial = 1 };
 
 template <int DK, int MODE, bool FULL>
 __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, int c,
-                                           PipeLds<DK> &s)
+                                           PipeLds<DK> &s, int vw)
 {
     constexpr int NQ = DK > 256 ? 4 : DK / 64; // 64-dim output groups of this wave
-    const int d0 = 256 * ((int)(threadIdx.x >> 6) - 1); // the wave's first output dim
+    const int d0 = 256 * vw; // the wave's first output dim
     const int lane = threadIdx.x & 63;
     const int col = lane & 15;
     const int g = lane >> 4;
@@ -409,17 +597,36 @@ __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, i
 }
 
 // FULL: the head dim equals the padded head dim (no dim clamping).
+template <int DK>
+constexpr int pipe_threads()
+{
+    return 64 * (pipe_score_waves<DK>() + pipe_value_waves<DK>());
+}
+
 template <int DK, int MODE, bool FULL>
-__global__ __launch_bounds__(64 * (1 + pipe_value_waves<DK>()), 2) void pipe_kv_kernel(Params p)
+__global__ __launch_bounds__(pipe_threads<DK>(), 2) void pipe_kv_kernel(Params p)
 {
     __shared__ PipeLds<DK> s;
     const int c = p.c_lo + blockIdx.x;
     const int unit = blockIdx.y % p.units;
     const int kvl = blockIdx.y / p.units;
-    if (threadIdx.x < 64)
-        score_wave<DK, FULL>(p, unit, kvl, c, s);
-    else
-        value_wave<DK, MODE, FULL>(p, unit, kvl, c, s);
+    const int wave = threadIdx.x >> 6;
+    if constexpr (pipe_score_waves<DK>() == 1) {
+        if (wave == 0)
+            score_wave<DK, FULL>(p, unit, kvl, c, s);
+        else
+            value_wave<DK, MODE, FULL>(p, unit, kvl, c, s, wave - 1);
+    } else {
+        if (wave == 0) {
+            score_wave_dual<DK, FULL, 0>(p, unit, kvl, c, s);
+        } else if (wave == 1) {
+            score_wave_dual<DK, FULL, 1>(p, unit, kvl, c, s);
+        } else {
+            __syncthreads(); // #Q
+            __syncthreads(); // #0
+            value_wave<DK, MODE, FULL>(p, unit, kvl, c, s, wave - 2);
+        }
+    }
 }
 
 template <int MODE, bool FULL> hipError_t launch_mode(const Params &p, hipStream_t stream)
@@ -429,7 +636,7 @@ template <int MODE, bool FULL> hipError_t launch_mode(const Params &p, hipStream
     case 64: pipe_kv_kernel<64, MODE, FULL><<<grid, 128, 0, stream>>>(p); break;
     case 128: pipe_kv_kernel<128, MODE, FULL><<<grid, 128, 0, stream>>>(p); break;
     case 256: pipe_kv_kernel<256, MODE, FULL><<<grid, 128, 0, stream>>>(p); break;
-    case 512: pipe_kv_kernel<512, MODE, FULL><<<grid, 192, 0, stream>>>(p); break;
+    case 512: pipe_kv_kernel<512, MODE, FULL><<<grid, pipe_threads<512>(), 0, stream>>>(p); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
