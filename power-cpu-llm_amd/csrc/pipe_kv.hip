@@ -285,21 +285,6 @@ __device__ __forceinline__ void score_wave_dual(const Params &p, int unit, int k
     const int64_t klast = p.nkeys - 1;
     const int64_t hoff = (int64_t)kh * p.dim;
 
-    // Q^T, staged by both score waves
-    for (int i = lane + 64 * ROLE; i < kRows * (DK / 4); i += 128) {
-        const int r = i / (DK / 4);
-        const int d = (i % (DK / 4)) * 4;
-        const int f = unit * kRows + r;
-        f4 v = f4{0.f, 0.f, 0.f, 0.f};
-        if (f < p.nrows && d < p.dim) {
-            const int qq = f / p.group;
-            const int hh = kh * p.group + f % p.group;
-            v = ldg4(p.q + (int64_t)qq * p.q_stride + (int64_t)hh * p.dim + d) * p.q_scale;
-        }
-        *(f4 *)(s.q + r * QLD + d) = v;
-    }
-    __syncthreads(); // #Q: Q^T staged
-
     f4 kb[PU][2]; // the K piece in flight: 16 keys (this wave's block) x 256 dims
     auto load_k = [&](int t, int pc) {
         const int64_t key = cbase + t * kTile + 16 * ROLE + col;
@@ -314,6 +299,41 @@ __device__ __forceinline__ void score_wave_dual(const Params &p, int unit, int k
                 kb[uu][h] = din ? x : f4{0.f, 0.f, 0.f, 0.f};
             }
     };
+    // the first piece is requested before Q^T is staged, so the two loads'
+    // latencies overlap (a barrier waits on LDS traffic only)
+    load_k(0, 0);
+
+    // Q^T, staged by both score waves: every load is issued before the first
+    // LDS store (a load-store loop would wait out one round trip per row).
+    // Padding rows and dims read a valid row and store zeros.
+    constexpr int QN = kRows * (DK / 4) / 128; // f4 per lane
+    auto q_in = [&](int it, int *f, int *d) {
+        const int i = lane + 64 * ROLE + 128 * it;
+        *f = unit * kRows + i / (DK / 4);
+        *d = (i % (DK / 4)) * 4;
+        return *f < p.nrows && (FULL || *d < p.dim);
+    };
+    f4 qs[QN];
+#pragma unroll
+    for (int it = 0; it < QN; ++it) {
+        int f, d;
+        const bool in = q_in(it, &f, &d);
+        const int ff = in ? f : 0;
+        qs[it] = ldg4(p.q + (int64_t)(ff / p.group) * p.q_stride +
+                      (int64_t)(kh * p.group + ff % p.group) * p.dim + (in ? d : 0));
+    }
+#pragma unroll
+    for (int it = 0; it < QN; ++it) {
+        int f, d;
+        const bool in = q_in(it, &f, &d);
+        f4 x = qs[it];
+        // an unconditional use: keeps the (wave-uniform) row test from
+        // sinking each load into a branch that waits for it alone
+        asm volatile("" : "+v"(x));
+        *(f4 *)(s.q + (f - unit * kRows) * QLD + d) = in ? x * p.q_scale : f4{0.f, 0.f, 0.f, 0.f};
+    }
+    __syncthreads(); // #Q: Q^T staged
+
     // this wave's block of tile t: its canonical score chain (run: any key of
     // the block allowed for the unit), the next piece loaded as registers free
     auto chain = [&](int t, bool run) {
@@ -357,7 +377,6 @@ __device__ __forceinline__ void score_wave_dual(const Params &p, int unit, int k
         return (bool)__any(any);
     };
 
-    load_k(0, 0);
     if constexpr (ROLE == 1) {
         {
             bool ok[4];
@@ -490,6 +509,12 @@ __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, i
         }
     };
     load_v(0, 0);
+    if constexpr (pipe_score_waves<DK>() > 1) {
+        // the score waves' prologue barriers (Q^T staged, the first block
+        // scored) pass with the first half tile already requested
+        __syncthreads(); // #Q
+        __syncthreads(); // #0
+    }
     float l = 0.f;
     f4 O[NQ][4];
 #pragma unroll
@@ -622,8 +647,6 @@ __global__ __launch_bounds__(pipe_threads<DK>(), 2) void pipe_kv_kernel(Params p
         } else if (wave == 1) {
             score_wave_dual<DK, FULL, 1>(p, unit, kvl, c, s);
         } else {
-            __syncthreads(); // #Q
-            __syncthreads(); // #0
             value_wave<DK, MODE, FULL>(p, unit, kvl, c, s, wave - 2);
         }
     }
