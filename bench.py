@@ -65,6 +65,10 @@ WORKLOADS = {
     # for a 4K-token prompt; here `nkeys` is the hidden width
     "output_decode": (16, 8, 256, 1, 2816, False, 0, 0, "output", False),
     "output_4k": (16, 8, 256, 4096, 2816, False, 0, 0, "output", False),
+    # the engine's own call of the 32K decode: the AttentionF32 entry over
+    # pageable host arrays, so each call copies K and V over PCIe (the rate
+    # that includes the copies, never the headline)
+    "decode_32k_host": (16, 8, 256, 1, 32768, True, 0, 32767, "host", False),
 }
 HEADLINE = "decode_32k"
 
@@ -174,6 +178,8 @@ def time_workload(torch, pcl, ctx, name, steps, warmup, seed=0, kernel=0):
         return time_transform_workload(torch, pcl, ctx, name, steps, warmup, seed)
     if kind == "output":
         return time_output_workload(torch, pcl, ctx, name, steps, warmup, seed)
+    if kind == "host":
+        return time_host_workload(torch, pcl, name, steps, warmup, seed)
     sets = []
     for i in range(nsets):
         q, k, v = make_inputs(torch, name, seed + 1000 * i)
@@ -216,6 +222,36 @@ def time_workload(torch, pcl, ctx, name, steps, warmup, seed=0, kernel=0):
              "combine_ms": ms_comb / n_comb if n_comb else 0.0}
     host = sets[(steps - 1) % nsets][0]
     return ev, wall, kernel, host, roles, nsets
+
+
+def time_host_workload(torch, pcl, name, steps, warmup, seed):
+    """Wall time (ms) of pcl_hip_attention_f32_heads, the entry the engine
+    binds as its AttentionF32 pointer, over pageable host arrays: the copies of
+    Q, K and V to the device, the attention and the copy of the output back."""
+    import ctypes
+    qh, kvh, dim, nq, nkeys, causal, window, fq, kind, _ = WORKLOADS[name]
+    q, k, v = make_inputs(torch, name, seed)
+    hq, hk, hv = (np.ascontiguousarray(x.cpu().numpy().reshape(-1)) for x in (q, k, v))
+    del q, k, v
+    out = np.empty(qh * dim, np.float32)
+    lib = pcl.load()
+    fptr = ctypes.POINTER(ctypes.c_float)
+
+    def call():
+        # all keys allowed: the decode position is the last key (no mask)
+        if not lib.pcl_hip_attention_f32_heads(
+                hq.ctypes.data_as(fptr), hk.ctypes.data_as(fptr), hv.ctypes.data_as(fptr),
+                qh, kvh, dim, nkeys, None, None, out.ctypes.data_as(fptr), 0, qh):
+            raise RuntimeError("pcl_hip_attention_f32_heads failed for %s" % name)
+
+    for _ in range(max(warmup, 1)):
+        call()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        call()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    roles = {"stream_ms": 0.0, "combine_ms": 0.0}
+    return wall, wall, "host+auto", {"q": torch.from_numpy(hq)}, roles, 1
 
 
 def make_transform(torch, pcl, ctx, qh, kvh, dim):
@@ -464,6 +500,8 @@ def main():
         r["TFLOP/s"] = flops / (ev * 1e-3) / 1e12
         if kind == "output" and nq_of(name) > 32:
             r["frac_mfma_fp64"] = r["TFLOP/s"] / FP64_MFMA_PEAK_TFS
+        elif kind == "host":
+            r["pcie_inclusive_GB/s"] = r["GB/s"]
         elif kind in ("decode", "cache", "step", "transform", "output"):
             r["frac_hbm"] = r["GB/s"] / HBM_PEAK_GBS
         else:
@@ -496,7 +534,13 @@ def main():
     # roofline of the dominant kernel(s): the launches that stream K/V, timed by
     # the library's event spans (the ordered combine is excluded)
     stream_s = hr["stream_kernel_ms"] * 1e-3
-    if kind == "decode":
+    if kind == "host":
+        # host buffers: the copies dominate; no kernel roofline applies
+        value, unit = hr["GB/s"], "GB/s"
+        metric = "decode-attn GB/s at 32K KV incl. host copies"
+        roof = {"bound": "pcie", "achieved": value, "peak": None, "unit": "GB/s",
+                "frac": None, "traffic": None}
+    elif kind == "decode":
         value, unit, metric = hr["GB/s"], "GB/s", "decode-attn HBM GB/s at 32K KV"
         ach = hr["algorithmic_bytes"] / stream_s / 1e9
         roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS,
