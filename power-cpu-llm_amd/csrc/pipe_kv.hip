@@ -7,16 +7,19 @@
 // row sum to the value waves through a double-buffered LDS slot. The value
 // waves stream V and run the P.V chain one tile behind. One barrier per tile
 // keeps the workgroup in step; at head dim 256 the score and value waves'
-// MFMA work is balanced (128 MFMAs each per tile). At head dim 512 the score
-// wave reads Q^T from LDS so its registers can hold the 32 KiB K block.
+// MFMA work is balanced (128 MFMAs each per tile). At head dim 512 two score
+// waves share Q^T in LDS and two value waves split the output dims.
 //
-// Each wave keeps exactly one 16-key block of K or V in flight, loading the
-// next block into the same registers as its MFMAs consume them: each 32-dim
-// K slice (each 4-key V slice) is reloaded right after the MFMAs that read
-// it, so a block's MFMA time overlaps the next block's memory latency
-// (issuing the whole next block only after the last MFMA cost ~10 % at 32K).
-// Head dim 512 keeps whole-block reloads: there the earlier issue made the
-// 128K decode 40 % slower (its 32 KiB K blocks then overlap in flight).
+// Up to head dim 256 each wave keeps exactly one 16-key block of K or V in
+// flight, loading the next block into the same registers as its MFMAs
+// consume them: each 32-dim K slice (each 4-key V slice) is reloaded right
+// after the MFMAs that read it, so a block's MFMA time overlaps the next
+// block's memory latency (issuing the whole next block only after the last
+// MFMA cost ~10 % at 32K). At head dim 512 each wave holds 8 KiB (16 keys x
+// 128 dims of K, 8 keys x 256 dims of V) and reloads it whole after its
+// MFMAs: at 127 VGPRs four workgroups share a CU, so a 128K decode's 1024
+// workgroups are all resident (3.5 % faster than 16 KiB pieces at three per
+// CU, which left a third round); early reloads there cost 10-40 %.
 template <int DK> constexpr bool pipe_slice_loads()
 {
     return DK <= 256;
@@ -38,6 +41,18 @@ template <int DK> constexpr int pipe_value_waves()
 {
     return DK > 256 ? DK / 256 : 1;
 }
+
+// V slices (4 keys x 256 dims each) a value wave keeps in flight: a 16-key
+// block up to head dim 256; half a block at 512, where a workgroup has four
+// waves and holds 8 KiB per wave so that four workgroups fit on a CU.
+template <int DK> constexpr int pipe_v_slices()
+{
+    return DK > 256 ? 2 : 4;
+}
+
+// Dims of the K piece a score wave keeps in flight at head dim 512 (16 keys
+// x 128 dims = 8 KiB; four pieces per 16-key block).
+constexpr int kPipeKPieceDims512 = 128;
 
 // Score waves per workgroup. Above head dim 256 a tile's K is as many bytes
 // as its V, which two value waves stream: two score waves then stream K, one
@@ -273,7 +288,7 @@ __device__ __forceinline__ void score_wave_dual(const Params &p, int unit, int k
 {
     static_assert(pipe_q_lds<DK>(), "the two score waves share Q^T in LDS");
     constexpr int QLD = DK + 4;
-    constexpr int PD = 256;     // dims per K piece
+    constexpr int PD = kPipeKPieceDims512; // dims per K piece
     constexpr int PU = PD / 32; // u-steps per piece
     constexpr int PB = DK / PD; // pieces per 16-key block
     const int lane = threadIdx.x & 63;
@@ -285,7 +300,7 @@ __device__ __forceinline__ void score_wave_dual(const Params &p, int unit, int k
     const int64_t klast = p.nkeys - 1;
     const int64_t hoff = (int64_t)kh * p.dim;
 
-    f4 kb[PU][2]; // the K piece in flight: 16 keys (this wave's block) x 256 dims
+    f4 kb[PU][2]; // the K piece in flight: 16 keys (this wave's block) x PD dims
     auto load_k = [&](int t, int pc) {
         const int64_t key = cbase + t * kTile + 16 * ROLE + col;
         const float *kp = key_row(p, key < klast ? key : klast) + hoff;
@@ -473,9 +488,13 @@ __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, i
     const int64_t hoff = (int64_t)kh * p.dim;
 
     const int dv = d0 + 4 * col; // + 64a
-    f4 vv[4][NQ];           // the half tile in flight: [slice][64-dim group]
-    auto load_v_sl = [&](int t, int half, int sl) {
-        const int br = 4 * half + sl;
+    // V in flight: a group of VS 4-key slices; slice br = 4b + r of a tile
+    // holds keys 16b + 4g + r (lane group g)
+    constexpr int VS = pipe_v_slices<DK>();
+    constexpr int NG = 8 / VS; // groups per tile
+    f4 vv[VS][NQ];             // [slice][64-dim group]
+    auto load_v_sl = [&](int t, int grp, int sl) {
+        const int br = VS * grp + sl;
         const int64_t key = cbase + t * kTile + 16 * (br >> 2) + 4 * g + (br & 3);
         const float *vp = value_row(p, key < klast ? key : klast) + hoff;
 #pragma unroll
@@ -486,32 +505,24 @@ __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, i
             vv[sl][a] = din ? x : f4{0.f, 0.f, 0.f, 0.f};
         }
     };
-    // slice sl of the half tile after (t, half), if any
-    auto load_next_sl = [&](int t, int half, int sl) {
-        if (half == 0)
-            load_v_sl(t, 1, sl);
+    // slice sl of the group after (t, grp), if any
+    auto load_next_sl = [&](int t, int grp, int sl) {
+        if (grp + 1 < NG)
+            load_v_sl(t, grp + 1, sl);
         else if (t + 1 < kTilesPerChunk)
             load_v_sl(t + 1, 0, sl);
     };
-    auto load_v = [&](int t, int half) {
+    auto load_next = [&](int t, int grp) {
 #pragma unroll
-        for (int sl = 0; sl < 4; ++sl) {
-            const int br = 4 * half + sl;
-            const int64_t key = cbase + t * kTile + 16 * (br >> 2) + 4 * g + (br & 3);
-            const float *vp = value_row(p, key < klast ? key : klast) + hoff;
-#pragma unroll
-            for (int a = 0; a < NQ; ++a) {
-                const int d = 64 * a + dv;
-                const bool din = FULL || d < p.dim;
-                const f4 x = ldg4_stream(vp + (din ? d : 0));
-                vv[sl][a] = din ? x : f4{0.f, 0.f, 0.f, 0.f};
-            }
-        }
+        for (int sl = 0; sl < VS; ++sl)
+            load_next_sl(t, grp, sl);
     };
-    load_v(0, 0);
+#pragma unroll
+    for (int sl = 0; sl < VS; ++sl)
+        load_v_sl(0, 0, sl);
     if constexpr (pipe_score_waves<DK>() > 1) {
         // the score waves' prologue barriers (Q^T staged, the first block
-        // scored) pass with the first half tile already requested
+        // scored) pass with the first group already requested
         __syncthreads(); // #Q
         __syncthreads(); // #0
     }
@@ -537,32 +548,28 @@ __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, i
                     O[a][j] = O[a][j] * a_t;
         }
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
+        for (int grp = 0; grp < NG; ++grp) {
             __builtin_amdgcn_sched_barrier(0);
             if (tile_any) {
 #pragma unroll
-                for (int sl = 0; sl < 4; ++sl) {
-                    const float pb = s.p[slot][4 * half + sl][lane];
+                for (int sl = 0; sl < VS; ++sl) {
+                    const float pb = s.p[slot][VS * grp + sl][lane];
 #pragma unroll
                     for (int a = 0; a < NQ; ++a)
 #pragma unroll
                         for (int j = 0; j < 4; ++j)
                             O[a][j] = mfma(vv[sl][a][j], pb, O[a][j]);
                     if constexpr (pipe_slice_loads<DK>()) {
-                        // this slice's registers are consumed: the next half tile's slice
+                        // this slice's registers are consumed: the next group's slice
                         __builtin_amdgcn_sched_barrier(0);
-                        load_next_sl(t, half, sl);
+                        load_next_sl(t, grp, sl);
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
-            if (!tile_any || !pipe_slice_loads<DK>()) { // the whole next half tile at once
-                if (half == 0)
-                    load_v(t, 1);
-                else if (t + 1 < kTilesPerChunk)
-                    load_v(t + 1, 0);
-            }
+            if (!tile_any || !pipe_slice_loads<DK>()) // the whole next group at once
+                load_next(t, grp);
         }
         __syncthreads(); // tile t + 1 handed over (the last one: the chunk maximum)
     }
@@ -628,8 +635,17 @@ constexpr int pipe_threads()
     return 64 * (pipe_score_waves<DK>() + pipe_value_waves<DK>());
 }
 
+// Waves per SIMD the register budget is sized for: four workgroups per CU at
+// head dim 512 (all 1024 workgroups of a 128K two-KV-head decode resident at
+// once, 128 KiB in flight per CU); a padded head dim keeps the larger budget
+// (its clamped loads would spill at 128 VGPRs).
+template <int DK, bool FULL> constexpr int pipe_waves_per_simd()
+{
+    return DK > 256 && FULL ? 4 : 2;
+}
+
 template <int DK, int MODE, bool FULL>
-__global__ __launch_bounds__(pipe_threads<DK>(), 2) void pipe_kv_kernel(Params p)
+__global__ __launch_bounds__(pipe_threads<DK>(), (pipe_waves_per_simd<DK, FULL>())) void pipe_kv_kernel(Params p)
 {
     __shared__ PipeLds<DK> s;
     const int c = p.c_lo + blockIdx.x;
