@@ -171,6 +171,92 @@ def test_attention_multi_kv_ranges_match_single_queries(kernels, oracle):
                     assert np.array_equal(bits(part[i]), bits(want)), (kv, i, masked)
 
 
+def run_threads(fn, args, timeout=60.0):
+    """Runs fn(*a) for every a in args on its own thread; re-raises the first
+    failure (ctypes releases the GIL, so the library calls overlap)."""
+    import threading
+    errors = []
+
+    def body(a):
+        try:
+            fn(*a)
+        except BaseException as e:  # reported on the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=body, args=(a,)) for a in args]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout)
+    assert not any(t.is_alive() for t in threads), "a worker did not finish"
+    if errors:
+        raise errors[0]
+
+
+def test_concurrent_workers_on_disjoint_head_ranges_match_one_call(kernels):
+    # the engine's decode fan-out (src/engine/attention.rs:755-777): up to N
+    # workers call the AttentionF32 entry at once, each on its own head range
+    # of one position, over shared read-only K/V (kernels.rs:230-231)
+    qheads, kvh, dim, nkeys = 16, 8, 256, 1500
+    g = np.random.default_rng(0xC0C0)
+    q = prescale(g.standard_normal(qheads * dim, dtype=np.float32), dim)
+    k = g.standard_normal(nkeys * kvh * dim, dtype=np.float32)
+    v = g.standard_normal(nkeys * kvh * dim, dtype=np.float32)
+    allowed = np.arange(nkeys) > nkeys - 1 - 700
+    full = kernels.attention(q, k, v, kvh, dim, allowed)
+    got = {}
+
+    def worker(h0, h1):
+        got[(h0, h1)] = [kernels.attention_heads(q, k, v, kvh, dim, allowed, (h0, h1))
+                         for _ in range(4)]
+
+    run_threads(worker, [(2 * i, 2 * i + 2) for i in range(8)] + [(0, qheads), (5, 11)])
+    assert len(got) == 10
+    for (h0, h1), outs in got.items():
+        for out in outs:
+            assert np.array_equal(bits(out), bits(full[h0 * dim:h1 * dim])), (h0, h1)
+
+
+def test_a_context_per_thread_gives_the_single_context_bits(pcl, torch, ctx):
+    # "a context per thread" re-entrancy: each worker owns a device context
+    # (and its stream and workspace), launches over the shared device K/V,
+    # and reads its own output; kernels alternate between workers
+    qheads, kvh, dim, nq, nkeys = 16, 8, 256, 3, 5000
+    g = np.random.default_rng(0xC0DE)
+    dev = torch.device("cuda:0")
+    q = torch.from_numpy(prescale(g.standard_normal((nq, qheads * dim), dtype=np.float32),
+                                  dim)).to(dev)
+    k = torch.from_numpy(g.standard_normal((nkeys, kvh, dim), dtype=np.float32)).to(dev)
+    v = torch.from_numpy(g.standard_normal((nkeys, kvh, dim), dtype=np.float32)).to(dev)
+    workers = 6
+    outs = [torch.full((nq, qheads * dim), float("nan"), device=dev) for _ in range(workers + 1)]
+    torch.cuda.synchronize()
+
+    def desc(c, out, kernel):
+        return c.desc(q=q.data_ptr(), q_stride=qheads * dim, nq=nq, qheads=qheads,
+                      kvheads=kvh, dim=dim, kh_first=0, kh_end=kvh, causal=1, window=0,
+                      first_key=0, first_query=nkeys - nq, k0=k.data_ptr(), v0=v.data_ptr(),
+                      n0=nkeys, out=out.data_ptr(), o_stride=qheads * dim, kernel=kernel)
+
+    ctx.launch(desc(ctx, outs[workers], pcl.KERNEL_SPLIT_KV))
+    assert ctx.sync() == 0
+    kernels = (pcl.KERNEL_PIPE_KV, pcl.KERNEL_SPLIT_KV, pcl.KERNEL_TWO_PASS)
+
+    def worker(i):
+        c = pcl.Context(0)
+        try:
+            for r in range(5):
+                c.launch(desc(c, outs[i], kernels[(i + r) % len(kernels)]))
+                assert c.sync() == 0
+        finally:
+            c.close()
+
+    run_threads(worker, [(i,) for i in range(workers)])
+    want = bits(outs[workers].cpu().numpy())
+    for i in range(workers):
+        assert np.array_equal(bits(outs[i].cpu().numpy()), want), i
+
+
 def test_attention_score_bounds_handle_holes_and_query_tails(kernels, oracle):
     # int8/tests.rs:1118-1177: holes, wholly masked blocks, disjoint masks
     rng = Rng(0x78124)
