@@ -16,14 +16,18 @@
 // output. Tiles wholly masked for the workgroup are never loaded; tiles
 // wholly masked for a wave are skipped by that wave.
 //
-// split != 0: the workgroup computes the single chunk c_lo + blockIdx.z and
-// writes its chunk partial for the combine kernels.
+// split != 0: the workgroup computes the single chunk c_lo + z0 + blockIdx.z
+// and writes its chunk partial for the combine kernels. A split launch whose
+// chunk items leave a small last round runs that round's chunks as
+// single-wave workgroups of 16 rows instead (more, shorter items fill the
+// CUs); each row's arithmetic is the same either way.
 #include "attention_device.hpp"
 
 namespace pcl {
 
 constexpr int kTiledWaves = 8;
 constexpr int kTiledRows = kTiledWaves * kRows; // 128
+constexpr int kTailWaves = 1; // waves of the workgroups of a split launch's tail
 
 template <int DK> struct TiledLds {
     static constexpr int tileFloats = kTile * DK;
@@ -58,16 +62,19 @@ __device__ __forceinline__ bool tile_whole(const Params &p, int row_lo, int row_
     return kmax <= qlo && (p.window == 0 || qhi - kmin < p.window);
 }
 
-// One workgroup per CU (its K/V stages fill the LDS), so two waves per SIMD:
-// each wave may hold 256 VGPRs, which the operand double-buffering below uses.
-template <int DK>
-__global__ __launch_bounds__(512, 2) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void tiled_kernel(Params p, int split)
+// One workgroup per CU (its K/V stages fill the LDS), so at most two waves
+// per SIMD: each wave may hold 256 VGPRs, which the operand double-buffering
+// below uses. W waves per workgroup, one 16-row unit each.
+template <int DK, int W>
+__global__ __launch_bounds__(64 * W, 2) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void tiled_kernel(Params p, int split, int z0)
 {
     using LD = TiledLds<DK>;
-    constexpr int NU = DK / 32;                         // score chain steps
-    constexpr int NQ = DK / 64;                         // 64-dim output groups
-    constexpr int NI = kTile * DK / 256 / kTiledWaves;  // DMA pieces per wave per array
+    constexpr int NU = DK / 32;                // score chain steps
+    constexpr int NQ = DK / 64;                // 64-dim output groups
+    constexpr int NI = kTile * DK / 256 / W;   // DMA pieces per wave per array
+    constexpr int ROWS = W * kRows;            // rows of the workgroup
+    static_assert(NI * W * 256 == kTile * DK, "whole 1 KiB pieces per wave");
     extern __shared__ float lds[];
 
     const int tid = threadIdx.x;
@@ -82,7 +89,7 @@ void tiled_kernel(Params p, int split)
     const int kvl = blockIdx.x % p.nkv;
     const int qb = nqb - 1 - (int)(blockIdx.x / p.nkv);
     const int kh = p.kh_first + kvl;
-    const int fa = qb * kTiledRows;
+    const int fa = qb * ROWS;
     const int row = fa + w * kRows + col;
     // the wave's real rows
     const int wrow_lo = fa + w * kRows;
@@ -96,7 +103,7 @@ void tiled_kernel(Params p, int split)
     // Key range the workgroup can see.
     int64_t k_lo = 0, k_hi = p.nkeys;
     if (!p.mask && p.causal) {
-        const int fb = min(fa + kTiledRows, p.nrows) - 1;
+        const int fb = min(fa + ROWS, p.nrows) - 1;
         const int64_t qa = p.first_query + fa / p.group;
         const int64_t qz = p.first_query + fb / p.group;
         k_hi = min(max(qz - p.first_key + 1, (int64_t)0), p.nkeys);
@@ -106,7 +113,7 @@ void tiled_kernel(Params p, int split)
     int t_lo = (int)(k_lo / kTile);
     int t_hi = (int)((k_hi + kTile - 1) / kTile);
     if (split) {
-        const int c = p.c_lo + blockIdx.z;
+        const int c = p.c_lo + z0 + (int)blockIdx.z;
         t_lo = max(t_lo, c * kTilesPerChunk);
         t_hi = min(t_hi, (c + 1) * kTilesPerChunk);
     }
@@ -361,7 +368,7 @@ void tiled_kernel(Params p, int split)
     // O[a][j][i] holds dim 64a + 16g + 4i + j of `row`.
     if (!rin)
         return;
-    const int64_t slot = ((int64_t)kvl * p.nrows_pad + row) * p.nch + blockIdx.z;
+    const int64_t slot = ((int64_t)kvl * p.nrows_pad + row) * p.nch + z0 + blockIdx.z;
     float *wo = p.ws_o + slot * p.dk;
 #pragma unroll
     for (int a = 0; a < NQ; ++a)
@@ -382,20 +389,73 @@ void tiled_kernel(Params p, int split)
     }
 }
 
-template <int DK> static hipError_t launch_tiled_dk(const Params &p, int split, hipStream_t stream)
+// Compute units of the current device (cached per device).
+static int device_cus()
+{
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return 0;
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return 0;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+template <int DK, int W> static hipError_t configure_tiled()
 {
     static bool configured = false; // dynamic LDS above 64 KiB must be allowed once
     if (!configured) {
-        const hipError_t e = hipFuncSetAttribute((const void *)tiled_kernel<DK>,
+        const hipError_t e = hipFuncSetAttribute((const void *)tiled_kernel<DK, W>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  (int)TiledLds<DK>::bytes);
         if (e != hipSuccess)
             return e;
         configured = true;
     }
+    return hipSuccess;
+}
+
+// Chunks of a split launch to run as single-wave workgroups: the last chunk
+// when the 8-wave items leave a last round of at most one chunk's items and
+// the tail's 16-row items fit one round. A lone wave is latency-bound: it
+// takes ~0.8 of an 8-wave item's time per chunk (canvas 256 x 2304 on
+// MI355X: 0.175 -> 0.157 ms), so a tail of two chunks would lose. 0: no tail.
+static int tail_chunks(const Params &p, int nqb, int cus)
+{
+    const int64_t per_chunk = (int64_t)nqb * p.nkv;
+    const int64_t items = per_chunk * p.nch;
+    if (cus <= 0 || items <= cus || items % cus == 0 || items % cus > per_chunk)
+        return 0;
+    const int64_t units = (p.nrows + kRows - 1) / kRows;
+    if (p.nch < 2 || units * p.nkv > cus)
+        return 0;
+    return 1;
+}
+
+template <int DK> static hipError_t launch_tiled_dk(const Params &p, int split, hipStream_t stream)
+{
+    hipError_t e = configure_tiled<DK, kTiledWaves>();
+    if (e != hipSuccess)
+        return e;
     const int nqb = (p.nrows + kTiledRows - 1) / kTiledRows;
-    const dim3 grid(nqb * p.nkv, 1, split ? p.nch : 1);
-    tiled_kernel<DK><<<grid, 64 * kTiledWaves, TiledLds<DK>::bytes, stream>>>(p, split);
+    const int tail = split ? tail_chunks(p, nqb, device_cus()) : 0;
+    const dim3 grid(nqb * p.nkv, 1, split ? p.nch - tail : 1);
+    tiled_kernel<DK, kTiledWaves>
+        <<<grid, 64 * kTiledWaves, TiledLds<DK>::bytes, stream>>>(p, split, 0);
+    e = hipGetLastError();
+    if (e != hipSuccess || !tail)
+        return e;
+    e = configure_tiled<DK, kTailWaves>();
+    if (e != hipSuccess)
+        return e;
+    const int nub = (p.nrows + kTailWaves * kRows - 1) / (kTailWaves * kRows);
+    const dim3 tgrid(nub * p.nkv, 1, tail);
+    tiled_kernel<DK, kTailWaves>
+        <<<tgrid, 64 * kTailWaves, TiledLds<DK>::bytes, stream>>>(p, split, p.nch - tail);
     return hipGetLastError();
 }
 

@@ -343,6 +343,10 @@ DESC_CASES = [
     (6, 3, 48, 20, 90, 1, 0, 70),
     (10, 2, 80, 33, 517, 1, 0, 484),
     (16, 16, 16, 9, 1000, 1, 17, 991),
+    # 4 row blocks x 8 KV heads x 9 chunks = 288 chunk items: on 256 CUs the
+    # chunk-split kernel runs the last chunk as single-wave workgroups
+    (16, 8, 64, 256, 2304, 0, 0, 0),
+    (16, 8, 128, 256, 2304, 1, 700, 2048),
 ]
 
 
