@@ -17,7 +17,9 @@
 // One 64-lane workgroup takes up to kItems heads of one token: it loads the
 // token's rotation factors and the scales once per lane, issues the loads of
 // all its rows at once (16-byte, coalesced) and stages them in LDS, each lane
-// sums one row in order, and the outputs are written back coalesced.
+// sums one row in order, and the outputs are written back coalesced. Launches
+// of a few tokens take 4 or 1 heads per workgroup instead, so that a decode
+// step's heads run on many CUs at once.
 #include "attention_device.hpp"
 #include "context.hpp"
 #include "pcl_attention.h"
@@ -50,11 +52,11 @@ constexpr int transform_items()
     return 4096 / DK < 64 ? 4096 / DK : 64;
 }
 
-// Workgroup (token t, slot group y): heads y*kItems.. of token t.
-template <int DK>
+// Workgroup (token t, slot group y): heads y*ITEMS.. of token t.
+template <int DK, int ITEMS>
 __global__ __launch_bounds__(64) void head_transform_kernel(TransformParams p)
 {
-    constexpr int kItems = transform_items<DK>();
+    constexpr int kItems = ITEMS;
     constexpr int kStride = DK + 4; // 16-byte aligned rows
     constexpr int kHalf = DK / 2;
     constexpr int kPairs = (kHalf + 63) / 64;
@@ -163,20 +165,37 @@ __global__ __launch_bounds__(64) void head_transform_kernel(TransformParams p)
         atomicOr(p.err, kErrTransform);
 }
 
-hipError_t launch_head_transform(const TransformParams &p, hipStream_t stream)
+// Workgroups a launch should at least fill before its heads are packed
+// kItems to a workgroup: a decode step (one or a few tokens) is a chain of
+// one load round trip, one lane's sequential sum and the row stores per
+// workgroup, so fewer heads per workgroup spread it over more CUs.
+constexpr int64_t kTransformSpreadGroups = 256;
+
+template <int DK> static hipError_t launch_dk(const TransformParams &p, hipStream_t stream)
 {
     auto go = [&](auto kernel, int per) {
         const dim3 grid((unsigned)p.n, (unsigned)((p.slots + per - 1) / per));
         hipLaunchKernelGGL(kernel, grid, dim3(64), 0, stream, p);
         return hipGetLastError();
     };
+    constexpr int full = transform_items<DK>();
+    auto groups = [&](int per) { return (int64_t)p.n * ((p.slots + per - 1) / per); };
+    if (groups(full) >= kTransformSpreadGroups || full <= 4)
+        return go(head_transform_kernel<DK, full>, full);
+    if (groups(4) >= kTransformSpreadGroups)
+        return go(head_transform_kernel<DK, 4>, 4);
+    return go(head_transform_kernel<DK, 1>, 1);
+}
+
+hipError_t launch_head_transform(const TransformParams &p, hipStream_t stream)
+{
     switch (p.dim) {
-    case 16: return go(head_transform_kernel<16>, transform_items<16>());
-    case 32: return go(head_transform_kernel<32>, transform_items<32>());
-    case 64: return go(head_transform_kernel<64>, transform_items<64>());
-    case 128: return go(head_transform_kernel<128>, transform_items<128>());
-    case 256: return go(head_transform_kernel<256>, transform_items<256>());
-    case 512: return go(head_transform_kernel<512>, transform_items<512>());
+    case 16: return launch_dk<16>(p, stream);
+    case 32: return launch_dk<32>(p, stream);
+    case 64: return launch_dk<64>(p, stream);
+    case 128: return launch_dk<128>(p, stream);
+    case 256: return launch_dk<256>(p, stream);
+    case 512: return launch_dk<512>(p, stream);
     default: return hipErrorInvalidValue;
     }
 }
