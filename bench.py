@@ -451,7 +451,23 @@ def cpu_baseline(name, host, threads, budget_s=20.0):
     med = float(np.median(times))
     gpu = host["out"].cpu().numpy().reshape(-1)
     maxerr = float(np.max(np.abs(gpu - out)))
-    return med, len(times), maxerr
+    # the same call on one host core (median of 5)
+    one = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        orc.threaded(q, nq, k, v, qh, kvh, dim, nkeys, causal, 0, fq, window, threads=1)
+        one.append(time.perf_counter() - t0)
+    return med, len(times), maxerr, float(np.median(one))
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def main():
@@ -535,13 +551,20 @@ def main():
     cpu = None
     if not args.no_cpu and head in hosts:
         threads = min(16, len(os.sched_getaffinity(0)))
-        med, runs, maxerr = cpu_baseline(head, hosts[head], threads, args.cpu_budget)
+        med, runs, maxerr, med1 = cpu_baseline(head, hosts[head], threads, args.cpu_budget)
         flops, bytes_, _ = work(head)
-        cpu = {"value": (bytes_ / med / 1e9) if kind == "decode" else (flops / med / 1e12),
+
+        def rate(sec):
+            return (bytes_ / sec / 1e9) if kind == "decode" else (flops / sec / 1e12)
+
+        cpu = {"value": rate(med),
                "unit": "GB/s" if kind == "decode" else "TFLOP/s", "cores": threads,
                "kind": "port",
                "sample": "%d whole %s calls (exact f64 path, engine head split), median %.3f s"
                          % (runs, head, med),
+               "value_1core": rate(med1),
+               "sample_1core": "5 whole calls on one thread, median %.3f s" % med1,
+               "cpu": cpu_model(),
                "gpu_vs_oracle_maxabs": maxerr}
     qh, kvh, dim, nq, nkeys, causal, window, fq, _, _ = WORKLOADS[head]
     # roofline of the dominant kernel(s): the launches that stream K/V, timed by
