@@ -17,10 +17,10 @@
 // directly.
 //
 // The combine (also used by the pipelined and tiled split kernels) runs both
-// levels of the ordered merge of attention_device.hpp in one launch: span
-// lanes merge the chunks of their spans, one batch of loads per span, and the
-// span partials are folded in ascending order from registers of the same
-// wave.
+// levels of the ordered merge of attention_device.hpp in one launch up to 32
+// spans (128K keys): span lanes merge the chunks of their spans, one batch of
+// loads per span, and the span partials are folded in ascending order from
+// registers of the same wave (up to 8 spans) or from LDS (up to 32).
 #include "attention_device.hpp"
 
 namespace pcl {
@@ -314,22 +314,15 @@ __global__ __launch_bounds__(DK, SplitCfg<DK>::waves_per_eu) void split_kv_kerne
     }
 }
 
-// Two-level combine for launches of many spans, one wave per 256 output dims
-// of one row, so every load is a contiguous KiB of one partial.
-// Level 1: wave ((kv, row), span, piece) merges the span's chunks in order;
-// with a single span it writes the output, else the span partial.
-__global__ __launch_bounds__(64) void combine_level1_kernel(Params p)
+// Level 1 of the ordered merge for four dims [d, d+4) of one row: span sl's
+// chunk partials merged in ascending order from (-inf, 0, 0), all of the
+// span's loads in one batch (a wave's loads are a contiguous KiB of one
+// partial). slot0: the row's first chunk slot.
+__device__ __forceinline__ Merged4 merge_span_chunks(const Params &p, int64_t slot0, int sl,
+                                                     int d, bool din)
 {
-    const int lane = threadIdx.x;
-    const int piece = blockIdx.z;
-    const int sl = blockIdx.y;
-    const int kvl = blockIdx.x / p.nrows;
-    const int row = blockIdx.x % p.nrows;
-    const int d = 256 * piece + 4 * lane;
-    const bool din = d < p.dim;
     int c0, c1;
     span_chunks(p, sl, &c0, &c1);
-    const int64_t slot0 = ((int64_t)kvl * p.nrows_pad + row) * p.nch;
     float mv[kSpanChunks], lv[kSpanChunks];
     f4 ov[kSpanChunks];
 #pragma unroll
@@ -346,6 +339,24 @@ __global__ __launch_bounds__(64) void combine_level1_kernel(Params p)
         const bool in = c0 + i < c1;
         merge_into4(s, in ? mv[i] : kNegInf, in ? lv[i] : 0.f, in ? ov[i] : zero4());
     }
+    return s;
+}
+
+// Two-level combine for launches of many spans, one wave per 256 output dims
+// of one row, so every load is a contiguous KiB of one partial.
+// Level 1: wave ((kv, row), span, piece) merges the span's chunks in order;
+// with a single span it writes the output, else the span partial.
+__global__ __launch_bounds__(64) void combine_level1_kernel(Params p)
+{
+    const int lane = threadIdx.x;
+    const int piece = blockIdx.z;
+    const int sl = blockIdx.y;
+    const int kvl = blockIdx.x / p.nrows;
+    const int row = blockIdx.x % p.nrows;
+    const int d = 256 * piece + 4 * lane;
+    const bool din = d < p.dim;
+    const int64_t slot0 = ((int64_t)kvl * p.nrows_pad + row) * p.nch;
+    const Merged4 s = merge_span_chunks(p, slot0, sl, d, din);
     if (p.nspan == 1) {
         float *o = out_ptr(p, p.kh_first + kvl, row);
         if (!o || !din)
@@ -410,6 +421,58 @@ __global__ __launch_bounds__(64) void combine_level2_kernel(Params p)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         v[j] = s.acc[j] / s.L;
+        nonfinite |= !is_finite(v[j]);
+    }
+    stg4(o + d, v);
+    if (nonfinite)
+        atomicOr(p.err, kErrOutput);
+}
+
+// Both levels in one launch for up to kCombineLdsSpans spans: a workgroup
+// per ((kv, row), slab of 4 * kCombineSpanLanes dims); each group of
+// kCombineSpanLanes lanes merges one span's chunks exactly as level 1 (one
+// batch of loads, contiguous bytes of a partial per group) and leaves the
+// span partial in LDS, then the first group folds the spans in ascending
+// order exactly as level 2. Saves level 2's launch and its workspace round
+// trip.
+constexpr int kCombineSpanLanes = 8;
+constexpr int kCombineLdsSpans = 32;
+constexpr int kCombineSpanThreads = kCombineLdsSpans * kCombineSpanLanes;
+
+__global__ __launch_bounds__(kCombineSpanThreads) void combine_spans_kernel(Params p)
+{
+    constexpr int L = kCombineSpanLanes;
+    __shared__ f4 so[kCombineLdsSpans][L];
+    __shared__ float sm[kCombineLdsSpans], sls[kCombineLdsSpans];
+    const int sl = threadIdx.x / L; // this lane group's span
+    const int q = threadIdx.x % L;
+    const int kvl = blockIdx.x / p.nrows;
+    const int row = blockIdx.x % p.nrows;
+    const int d = 4 * L * blockIdx.z + 4 * q;
+    const bool din = d < p.dim;
+    float *o = out_ptr(p, p.kh_first + kvl, row);
+    if (!o) // the whole workgroup's row is not written
+        return;
+    const int64_t slot0 = ((int64_t)kvl * p.nrows_pad + row) * p.nch;
+    if (sl < p.nspan) {
+        const Merged4 s = merge_span_chunks(p, slot0, sl, d, din);
+        so[sl][q] = s.acc;
+        if (q == 0) {
+            sm[sl] = s.M;
+            sls[sl] = s.L;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x >= L || !din)
+        return;
+    Merged4 t = {kNegInf, 0.f, zero4()};
+    for (int i = 0; i < p.nspan; ++i)
+        merge_into4(t, sm[i], sls[i], so[i][q]);
+    f4 v;
+    bool nonfinite = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        v[j] = t.acc[j] / t.L;
         nonfinite |= !is_finite(v[j]);
     }
     stg4(o + d, v);
@@ -540,9 +603,15 @@ hipError_t launch_combine(const Params &p, hipStream_t stream)
         combine_kernel<<<dim3(bx, p.nkv), 64, 0, stream>>>(p, lanes);
         return hipGetLastError();
     }
-    // many spans: span partials through the workspace, two launches
     const unsigned pieces = (unsigned)((p.dim + 255) / 256);
     const unsigned rows = (unsigned)(p.nkv * p.nrows);
+    if (p.nspan <= kCombineLdsSpans) {
+        const unsigned slabs = (unsigned)((p.dim + 4 * kCombineSpanLanes - 1) /
+                                          (4 * kCombineSpanLanes));
+        combine_spans_kernel<<<dim3(rows, 1, slabs), kCombineSpanThreads, 0, stream>>>(p);
+        return hipGetLastError();
+    }
+    // more spans: span partials through the workspace, two launches
     combine_level1_kernel<<<dim3(rows, p.nspan, pieces), 64, 0, stream>>>(p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.nspan == 1)
