@@ -88,9 +88,8 @@ template <int DK, bool FULL>
 __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, int c,
                                            PipeLds<DK> &s)
 {
+    static_assert(!pipe_q_lds<DK>(), "head dims above 256 take the two score waves");
     constexpr int NU = DK / 32; // score chain steps
-    constexpr bool QLDS = pipe_q_lds<DK>();
-    constexpr int QLD = DK + 4;
     const int lane = threadIdx.x & 63;
     const int col = lane & 15;
     const int g = lane >> 4;
@@ -101,23 +100,8 @@ __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, i
     const int64_t hoff = (int64_t)kh * p.dim;
 
     // Q^T B operands: Q[row][32u + 8g + jj] * q_scale (0 for padding rows).
-    float q[QLDS ? 1 : NU][8];
-    if constexpr (QLDS) {
-        for (int i = lane; i < kRows * (DK / 4); i += 64) {
-            const int r = i / (DK / 4);
-            const int d = (i % (DK / 4)) * 4;
-            const int f = unit * kRows + r;
-            f4 v = f4{0.f, 0.f, 0.f, 0.f};
-            if (f < p.nrows && d < p.dim) {
-                const int qq = f / p.group;
-                const int hh = kh * p.group + f % p.group;
-                v = ldg4(p.q + (int64_t)qq * p.q_stride + (int64_t)hh * p.dim + d) * p.q_scale;
-            }
-            *(f4 *)(s.q + r * QLD + d) = v;
-        }
-        // only this wave reads them; its LDS operations complete in order
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    } else {
+    float q[NU][8];
+    {
         const bool rin = row < p.nrows;
         const int query = rin ? row / p.group : 0;
         const int h = kh * p.group + (rin ? row % p.group : 0);
@@ -135,10 +119,8 @@ __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, i
                     q[u][4 * hh + j] = v[j];
             }
     }
-    // The K piece in flight: 16 keys x PD dims (a whole 16-key block up to
-    // head dim 256, half a block at 512, so a workgroup keeps ~the same bytes
-    // in flight at every head dim).
-    constexpr int PD = DK > 256 ? 256 : DK;
+    // The K piece in flight: a whole 16-key block (16 keys x DK dims).
+    constexpr int PD = DK;
     constexpr int PU = PD / 32; // u-steps per piece
     constexpr int PB = DK / PD; // pieces per 16-key block
     f4 kb[PU][2];
@@ -200,23 +182,9 @@ __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, i
 #pragma unroll
                     for (int uu = 0; uu < PU; ++uu) {
                         const int u = pc * PU + uu;
-                        float qv[8];
-                        if constexpr (QLDS) {
-                            const f4 qa0 = *(const f4 *)(s.q + col * QLD + 32 * u + 8 * g);
-                            const f4 qa1 = *(const f4 *)(s.q + col * QLD + 32 * u + 8 * g + 4);
-#pragma unroll
-                            for (int j = 0; j < 4; ++j) {
-                                qv[j] = qa0[j];
-                                qv[4 + j] = qa1[j];
-                            }
-                        } else {
-#pragma unroll
-                            for (int jj = 0; jj < 8; ++jj)
-                                qv[jj] = q[u][jj];
-                        }
 #pragma unroll
                         for (int jj = 0; jj < 8; ++jj)
-                            acc[b] = mfma(kb[uu][jj >> 2][jj & 3], qv[jj], acc[b]);
+                            acc[b] = mfma(kb[uu][jj >> 2][jj & 3], q[u][jj], acc[b]);
                         if constexpr (pipe_slice_loads<DK>()) {
                             // this slice's registers are consumed: the next piece's slice
                             __builtin_amdgcn_sched_barrier(0);
