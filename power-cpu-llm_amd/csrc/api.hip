@@ -29,10 +29,15 @@ namespace {
 constexpr int kMaxDim = 512;
 constexpr int kTiledMaxDk = 256;
 constexpr int kPipeMaxDk = 512;
-// Decode launches of at least this many (chunk, unit, KV head) items are
-// bandwidth-bound and take the pipelined kernel; shorter ones are
-// latency-bound and take the four-phase kernel.
-constexpr int64_t kStreamMinItems = 256;
+// Decode launches take the pipelined kernel, except at head dims above 256
+// with fewer than this many (chunk, unit, KV head) items: there each
+// pipelined wave needs 32 round trips per chunk (8 KiB pieces), while the
+// four-phase kernel spreads a chunk over DK/64 waves. Measured on MI355X
+// (2 KV heads, d512): four-phase 13-30 % faster from 2K to 32K keys (16-256
+// items), pipelined 24-27 % faster at 64K and 128K (512 and 1024 items).
+// Up to head dim 256 the pipelined kernel was as fast or faster at every
+// size tried (16 to 1024 items, d64/128/256).
+constexpr int64_t kPipeMinItemsWide = 512;
 
 void report(const char *what, hipError_t e)
 {
@@ -85,11 +90,10 @@ int choose_kernel(int requested, int dk, int64_t nrows, int64_t nkv, int64_t nch
     if (requested == PCL_KERNEL_TWO_PASS)
         return requested;
     if (dk > kTiledMaxDk || nrows < 64) {
-        // decode: long caches take a streaming kernel; short launches (few
-        // workgroups, so latency-bound) take the four-phase kernel with DK/64
-        // waves per chunk
+        // decode: the pipelined kernel; at head dim 512 short launches (few
+        // workgroups, so latency-bound) take the four-phase kernel
         const int64_t units = (nrows + pcl::kRows - 1) / pcl::kRows;
-        if (nch * nkv * units < kStreamMinItems)
+        if (dk > 256 && nch * nkv * units < kPipeMinItemsWide)
             return PCL_KERNEL_SPLIT_KV;
         return PCL_KERNEL_PIPE_KV;
     }

@@ -88,11 +88,13 @@ def test_descriptor_validation_on_the_host(pcl):
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
     assert lib.pcl_attention_workspace_bytes(ctypes.byref(d)) > 0
     d.dim, d.q_stride, d.o_stride = 512, 16 * 512, 16 * 512
-    # also at head dim 512 (one score wave, two value waves)
+    # also at head dim 512 (two score waves, two value waves)
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
-    d.dim, d.q_stride, d.o_stride = 256, 16 * 256, 16 * 256
-    d.window = 1024  # five chunks per head: the four-phase kernel
+    d.window = 1024  # five chunks per head: short, so at d512 the four-phase kernel
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_SPLIT_KV
+    d.dim, d.q_stride, d.o_stride = 256, 16 * 256, 16 * 256
+    # up to head dim 256 every decode streams through the pipelined kernel
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
     d.kernel = pcl.KERNEL_PIPE_KV  # forced choices are kept where the kernel exists
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
     d.kernel = pcl.KERNEL_TWO_PASS
