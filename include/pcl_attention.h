@@ -158,7 +158,10 @@ void pcl_context_destroy(pcl_context *ctx);
 /* The stream launches go to (a hipStream_t). */
 void *pcl_context_stream(pcl_context *ctx);
 /* Launch asynchronously. Returns PCL_OK, PCL_INVALID_SHAPE for a descriptor
- * that fails validation, or PCL_NON_FINITE_VALUE for a launch failure. Data
+ * that fails validation (including the size limits: at most 2^30 keys, and
+ * nq * (qheads / kvheads) * (kh_end - kh_first) at most 2^22; larger calls
+ * are split by query range or KV-head range, which leaves every result bit
+ * unchanged), or PCL_NON_FINITE_VALUE for a launch failure. Data
  * errors (non-finite allowed score or output) are recorded in the context's
  * device error flag. Grows the context's workspace when needed (a device
  * allocation); pcl_context_reserve avoids that inside timed regions. */

@@ -27,6 +27,8 @@ using pcl::Params;
 namespace {
 
 constexpr int kMaxDim = 512;
+constexpr int64_t kMaxKeys = (int64_t)1 << 30;
+constexpr int64_t kMaxRowsTimesKvHeads = (int64_t)1 << 22;
 constexpr int kTiledMaxDk = 256;
 constexpr int kPipeMaxDk = 512;
 // Decode launches take the pipelined kernel, except at head dims above 256
@@ -130,7 +132,10 @@ int make_plan(const pcl_attention_desc &d, int64_t h_lo, int64_t h_hi, int64_t h
         (d.n1 > 0 && (!aligned16(d.k1) || !aligned16(d.v1))))
         return PCL_INVALID_SHAPE;
     const int64_t nrows = d.nq * group;
-    if (nrows > (int64_t)1 << 30 || nkeys > (int64_t)1 << 40)
+    // size limits: every launch's grid stays below 2^31 work-items per
+    // dimension (at most 2^22 chunks x 512 threads; 2^22 rows x 256 threads)
+    // and chunk indices fit an int
+    if (nkeys > kMaxKeys || nrows * nkv > kMaxRowsTimesKvHeads)
         return PCL_INVALID_SHAPE;
     int64_t c_lo, c_hi;
     bool none;

@@ -111,6 +111,16 @@ def test_descriptor_validation_on_the_host(pcl):
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_TILED
     d.first_key = 5000  # no query sees a key
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == -1
+    # size limits (every grid below 2^31 work-items): 2^30 keys, and
+    # 2^22 rows x KV heads; calls beyond them are split by the caller
+    d.first_key, d.nq, d.first_query, d.n0 = 0, 1, (1 << 30) - 1, 1 << 30
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
+    d.n0, d.first_query = (1 << 30) + 1, 1 << 30
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == -1
+    d.n0, d.nq, d.first_query = 4096, (1 << 22) // 16, 0  # x group 2 x 8 KV heads
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_TILED
+    d.nq += 1
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == -1
 
 
 def test_product_path_has_no_cpu_fallback():
