@@ -319,7 +319,7 @@ int pcl_kv_cache_append_transformed(pcl_kv_cache *cache, pcl_head_transform *tra
  * non-finite projected or result value sets bit 3 of the device error flag.
  * The sums are f64 in the kernels' own order, so a value equals the engine's
  * unless the two f64 sums fall on opposite sides of an f32 rounding
- * boundary. */
+ * boundary. PCL_INVALID_SHAPE beyond n = 2^22 tokens or in, out = 2^20. */
 int pcl_attention_output(pcl_context *ctx, const float *attended, int64_t n, int64_t in,
                          const float *weights, int64_t out, const float *post_scale,
                          float epsilon, const float *residual, float *projected, float *result);

@@ -321,7 +321,8 @@ extern "C" int pcl_attention_output(pcl_context *ctx, const float *attended, int
 {
     if (!ctx || !attended || !weights || !post_scale || !residual || !projected || !result)
         return PCL_INVALID_SHAPE;
-    if (n <= 0 || in <= 0 || out <= 0 || n > (1 << 24) || in > (1 << 20) || out > (1 << 20))
+    // sizes keep every grid below 2^31 work-items (post-norm: 256 per token)
+    if (n <= 0 || in <= 0 || out <= 0 || n > (1 << 22) || in > (1 << 20) || out > (1 << 20))
         return PCL_INVALID_SHAPE;
     if (!(epsilon > 0.0f) || !__builtin_isfinite(epsilon))
         return PCL_INVALID_PARAMETER;
