@@ -20,10 +20,7 @@
 // MFMAs: at 127 VGPRs four workgroups share a CU, so a 128K decode's 1024
 // workgroups are all resident (3.5 % faster than 16 KiB pieces at three per
 // CU, which left a third round); early reloads there cost 10-40 %.
-template <int DK> constexpr bool pipe_slice_loads()
-{
-    return DK <= 256;
-}
+template <int DK, bool WIDE> constexpr bool pipe_slice_loads();
 // Measured on MI355X with inputs larger than the last-level cache, one block
 // in flight per wave streams at the HBM limit (~6.9 TB/s for a pure K+V read)
 // even with a microsecond of compute between loads, while two blocks in
@@ -36,59 +33,81 @@ template <int DK> constexpr bool pipe_slice_loads()
 
 namespace pcl {
 
-// Value waves per workgroup: one per 256 output dims.
-template <int DK> constexpr int pipe_value_waves()
+// The wide layout: two score waves (one per 16-key block of each tile; the
+// second runs a tile ahead and hands its raw scores to the first, which owns
+// the softmax, through LDS, where both read Q^T) and two value waves (half
+// the output dims each). Always above head dim 256, where a tile's K is as
+// many bytes as its V; at 128 and 256 for launches of few workgroups (WIDE),
+// which are bound by each wave's chain of memory round trips: a chunk then
+// takes 8 round trips per wave instead of 16.
+template <int DK, bool WIDE> constexpr bool pipe_dual()
 {
-    return DK > 256 ? DK / 256 : 1;
+    return DK > 256 || WIDE;
 }
 
-// V slices (4 keys x 256 dims each) a value wave keeps in flight: a 16-key
-// block up to head dim 256; half a block at 512, where a workgroup has four
-// waves and holds 8 KiB per wave so that four workgroups fit on a CU.
-template <int DK> constexpr int pipe_v_slices()
+template <int DK, bool WIDE> constexpr int pipe_score_waves()
 {
-    return DK > 256 ? 2 : 4;
+    return pipe_dual<DK, WIDE>() ? 2 : 1;
 }
 
-// Dims of the K piece a score wave keeps in flight at head dim 512 (16 keys
-// x 128 dims = 8 KiB; four pieces per 16-key block).
-constexpr int kPipeKPieceDims512 = 128;
-
-// Score waves per workgroup. Above head dim 256 a tile's K is as many bytes
-// as its V, which two value waves stream: two score waves then stream K, one
-// per 16-key block of each tile (the second runs a tile ahead and hands its
-// raw scores to the first, which owns the softmax), so K and V have the same
-// bytes in flight.
-template <int DK> constexpr int pipe_score_waves()
+template <int DK, bool WIDE> constexpr int pipe_value_waves()
 {
-    return DK > 256 ? 2 : 1;
+    return pipe_dual<DK, WIDE>() ? 2 : 1;
 }
 
-// Head dims above 256 keep Q^T in LDS (the score wave's registers hold the K
+// Output dims of a value wave (whole 64-dim groups).
+template <int DK, bool WIDE> constexpr int pipe_value_dims()
+{
+    return DK / pipe_value_waves<DK, WIDE>();
+}
+
+// V slices (4 keys x the wave's dims each) a value wave keeps in flight: a
+// 16-key block in the narrow layout; a whole tile in the wide layout up to
+// head dim 256 (16 KiB at 256); half a block at 512, where a workgroup holds
+// 8 KiB per wave so that four workgroups fit on a CU.
+template <int DK, bool WIDE> constexpr int pipe_v_slices()
+{
+    return DK > 256 ? 2 : pipe_dual<DK, WIDE>() ? 8 : 4;
+}
+
+// Dims of the K piece a score wave keeps in flight: the whole 16-key block up
+// to head dim 256; 128 dims (8 KiB; four pieces per block) at 512.
+template <int DK> constexpr int pipe_k_piece_dims()
+{
+    return DK > 256 ? 128 : DK;
+}
+
+// The wide layout keeps Q^T in LDS (the score waves' registers hold the K
 // block in flight); padded rows avoid bank conflicts.
-template <int DK> constexpr bool pipe_q_lds()
+template <int DK, bool WIDE> constexpr bool pipe_q_lds()
 {
-    return DK > 256;
+    return pipe_dual<DK, WIDE>();
+}
+
+// The narrow layout reloads each slice right after its MFMAs (see above).
+template <int DK, bool WIDE> constexpr bool pipe_slice_loads()
+{
+    return !pipe_dual<DK, WIDE>();
 }
 
 // LDS hand-over between the score wave and the value waves.
-template <int DK> struct PipeLds {
+template <int DK, bool WIDE> struct PipeLds {
     float p[2][8][64];    // probabilities, [slot][4b + r][lane]
     float alpha[2][kRows];
     float rs[2][kRows];
     int any[2];
     float m[kRows];       // chunk maximum
-    float q[pipe_q_lds<DK>() ? kRows * (DK + 4) : 1];
+    float q[pipe_q_lds<DK, WIDE>() ? kRows * (DK + 4) : 1];
     // raw scores of a tile's second 16-key block from the second score
     // wave, [tile & 1][r][lane]
-    float sb[pipe_score_waves<DK>() > 1 ? 2 : 1][4][64];
+    float sb[pipe_score_waves<DK, WIDE>() > 1 ? 2 : 1][4][64];
 };
 
 template <int DK, bool FULL>
 __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, int c,
-                                           PipeLds<DK> &s)
+                                           PipeLds<DK, false> &s)
 {
-    static_assert(!pipe_q_lds<DK>(), "head dims above 256 take the two score waves");
+    static_assert(!pipe_dual<DK, false>(), "head dims above 256 take the two score waves");
     constexpr int NU = DK / 32; // score chain steps
     const int lane = threadIdx.x & 63;
     const int col = lane & 15;
@@ -185,7 +204,7 @@ __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, i
 #pragma unroll
                         for (int jj = 0; jj < 8; ++jj)
                             acc[b] = mfma(kb[uu][jj >> 2][jj & 3], q[u][jj], acc[b]);
-                        if constexpr (pipe_slice_loads<DK>()) {
+                        if constexpr (pipe_slice_loads<DK, false>()) {
                             // this slice's registers are consumed: the next piece's slice
                             __builtin_amdgcn_sched_barrier(0);
                             load_next_u(t, b, pc, uu);
@@ -194,7 +213,7 @@ __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, i
                     }
                 }
                 __builtin_amdgcn_sched_barrier(0);
-                if (!tile_any || !pipe_slice_loads<DK>()) { // the whole next piece at once
+                if (!tile_any || !pipe_slice_loads<DK, false>()) { // the whole next piece at once
                     if (pc + 1 < PB)
                         load_k(t, b, pc + 1);
                     else if (b == 0)
@@ -250,13 +269,13 @@ __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, i
 // Barriers (the value waves keep the same count): #Q after Q^T is staged,
 // #0 after the second wave's tile-0 scores, #t+1 after tile t is handed over,
 // and one after the chunk maximum.
-template <int DK, bool FULL, int ROLE>
+template <int DK, bool FULL, int ROLE, bool WIDE>
 __device__ __forceinline__ void score_wave_dual(const Params &p, int unit, int kvl, int c,
-                                                PipeLds<DK> &s)
+                                                PipeLds<DK, WIDE> &s)
 {
-    static_assert(pipe_q_lds<DK>(), "the two score waves share Q^T in LDS");
+    static_assert(pipe_q_lds<DK, WIDE>(), "the two score waves share Q^T in LDS");
     constexpr int QLD = DK + 4;
-    constexpr int PD = kPipeKPieceDims512; // dims per K piece
+    constexpr int PD = pipe_k_piece_dims<DK>(); // dims per K piece
     constexpr int PU = PD / 32; // u-steps per piece
     constexpr int PB = DK / PD; // pieces per 16-key block
     const int lane = threadIdx.x & 63;
@@ -440,12 +459,14 @@ __device__ __forceinline__ void score_wave_dual(const Params &p, int unit, int k
 // Output modes of the pipelined kernel.
 enum PipeMode { kDirect = 0, kPartial = 1 };
 
-template <int DK, int MODE, bool FULL>
+template <int DK, int MODE, bool FULL, bool WIDE>
 __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, int c,
-                                           PipeLds<DK> &s, int vw)
+                                           PipeLds<DK, WIDE> &s, int vw)
 {
-    constexpr int NQ = DK > 256 ? 4 : DK / 64; // 64-dim output groups of this wave
-    const int d0 = 256 * vw; // the wave's first output dim
+    constexpr int VD = pipe_value_dims<DK, WIDE>();
+    static_assert(VD % 64 == 0, "whole 64-dim output groups per value wave");
+    constexpr int NQ = VD / 64; // 64-dim output groups of this wave
+    const int d0 = VD * vw;     // the wave's first output dim
     const int lane = threadIdx.x & 63;
     const int col = lane & 15;
     const int g = lane >> 4;
@@ -458,7 +479,7 @@ __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, i
     const int dv = d0 + 4 * col; // + 64a
     // V in flight: a group of VS 4-key slices; slice br = 4b + r of a tile
     // holds keys 16b + 4g + r (lane group g)
-    constexpr int VS = pipe_v_slices<DK>();
+    constexpr int VS = pipe_v_slices<DK, WIDE>();
     constexpr int NG = 8 / VS; // groups per tile
     f4 vv[VS][NQ];             // [slice][64-dim group]
     auto load_v_sl = [&](int t, int grp, int sl) {
@@ -488,7 +509,7 @@ __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, i
 #pragma unroll
     for (int sl = 0; sl < VS; ++sl)
         load_v_sl(0, 0, sl);
-    if constexpr (pipe_score_waves<DK>() > 1) {
+    if constexpr (pipe_score_waves<DK, WIDE>() > 1) {
         // the score waves' prologue barriers (Q^T staged, the first block
         // scored) pass with the first group already requested
         __syncthreads(); // #Q
@@ -527,7 +548,7 @@ __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, i
 #pragma unroll
                         for (int j = 0; j < 4; ++j)
                             O[a][j] = mfma(vv[sl][a][j], pb, O[a][j]);
-                    if constexpr (pipe_slice_loads<DK>()) {
+                    if constexpr (pipe_slice_loads<DK, WIDE>()) {
                         // this slice's registers are consumed: the next group's slice
                         __builtin_amdgcn_sched_barrier(0);
                         load_next_sl(t, grp, sl);
@@ -536,7 +557,7 @@ __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, i
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
-            if (!tile_any || !pipe_slice_loads<DK>()) // the whole next group at once
+            if (!tile_any || !pipe_slice_loads<DK, WIDE>()) // the whole next group at once
                 load_next(t, grp);
         }
         __syncthreads(); // tile t + 1 handed over (the last one: the chunk maximum)
@@ -596,11 +617,9 @@ __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, i
     }
 }
 
-// FULL: the head dim equals the padded head dim (no dim clamping).
-template <int DK>
-constexpr int pipe_threads()
+template <int DK, bool WIDE> constexpr int pipe_threads()
 {
-    return 64 * (pipe_score_waves<DK>() + pipe_value_waves<DK>());
+    return 64 * (pipe_score_waves<DK, WIDE>() + pipe_value_waves<DK, WIDE>());
 }
 
 // Waves per SIMD the register budget is sized for: four workgroups per CU at
@@ -612,38 +631,59 @@ template <int DK, bool FULL> constexpr int pipe_waves_per_simd()
     return DK > 256 && FULL ? 4 : 2;
 }
 
-template <int DK, int MODE, bool FULL>
-__global__ __launch_bounds__(pipe_threads<DK>(), (pipe_waves_per_simd<DK, FULL>())) void pipe_kv_kernel(Params p)
+// FULL: the head dim equals the padded head dim (no dim clamping). WIDE: the
+// wide layout at head dims up to 256.
+template <int DK, int MODE, bool FULL, bool WIDE>
+__global__ __launch_bounds__((pipe_threads<DK, WIDE>()), (pipe_waves_per_simd<DK, FULL>()))
+void pipe_kv_kernel(Params p)
 {
-    __shared__ PipeLds<DK> s;
+    __shared__ PipeLds<DK, WIDE> s;
     const int c = p.c_lo + blockIdx.x;
     const int unit = blockIdx.y % p.units;
     const int kvl = blockIdx.y / p.units;
     const int wave = threadIdx.x >> 6;
-    if constexpr (pipe_score_waves<DK>() == 1) {
+    if constexpr (pipe_score_waves<DK, WIDE>() == 1) {
         if (wave == 0)
             score_wave<DK, FULL>(p, unit, kvl, c, s);
         else
-            value_wave<DK, MODE, FULL>(p, unit, kvl, c, s, wave - 1);
+            value_wave<DK, MODE, FULL, WIDE>(p, unit, kvl, c, s, wave - 1);
     } else {
         if (wave == 0) {
-            score_wave_dual<DK, FULL, 0>(p, unit, kvl, c, s);
+            score_wave_dual<DK, FULL, 0, WIDE>(p, unit, kvl, c, s);
         } else if (wave == 1) {
-            score_wave_dual<DK, FULL, 1>(p, unit, kvl, c, s);
+            score_wave_dual<DK, FULL, 1, WIDE>(p, unit, kvl, c, s);
         } else {
-            value_wave<DK, MODE, FULL>(p, unit, kvl, c, s, wave - 2);
+            value_wave<DK, MODE, FULL, WIDE>(p, unit, kvl, c, s, wave - 2);
         }
     }
+}
+
+// Launches of fewer (chunk, unit, KV head) items than this take the wide
+// layout at head dims 128 and 256: at most one workgroup per CU, so each
+// workgroup's chain of round trips is the time.
+constexpr int64_t kPipeWideMaxItems = 256;
+
+template <int DK, int MODE, bool FULL, bool WIDE>
+static void launch_dk(const Params &p, dim3 grid, hipStream_t stream)
+{
+    pipe_kv_kernel<DK, MODE, FULL, WIDE><<<grid, pipe_threads<DK, WIDE>(), 0, stream>>>(p);
 }
 
 template <int MODE, bool FULL> hipError_t launch_mode(const Params &p, hipStream_t stream)
 {
     const dim3 grid(p.nch, p.nkv * p.units);
+    const bool wide = (int64_t)p.nch * p.nkv * p.units < kPipeWideMaxItems;
     switch (p.dk) {
-    case 64: pipe_kv_kernel<64, MODE, FULL><<<grid, 128, 0, stream>>>(p); break;
-    case 128: pipe_kv_kernel<128, MODE, FULL><<<grid, 128, 0, stream>>>(p); break;
-    case 256: pipe_kv_kernel<256, MODE, FULL><<<grid, 128, 0, stream>>>(p); break;
-    case 512: pipe_kv_kernel<512, MODE, FULL><<<grid, pipe_threads<512>(), 0, stream>>>(p); break;
+    case 64: launch_dk<64, MODE, FULL, false>(p, grid, stream); break;
+    case 128:
+        wide ? launch_dk<128, MODE, FULL, true>(p, grid, stream)
+             : launch_dk<128, MODE, FULL, false>(p, grid, stream);
+        break;
+    case 256:
+        wide ? launch_dk<256, MODE, FULL, true>(p, grid, stream)
+             : launch_dk<256, MODE, FULL, false>(p, grid, stream);
+        break;
+    case 512: launch_dk<512, MODE, FULL, true>(p, grid, stream); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
