@@ -37,9 +37,9 @@ namespace pcl {
 // second runs a tile ahead and hands its raw scores to the first, which owns
 // the softmax, through LDS, where both read Q^T) and two value waves (half
 // the output dims each). Always above head dim 256, where a tile's K is as
-// many bytes as its V; at 128 and 256 for launches of few workgroups (WIDE),
-// which are bound by each wave's chain of memory round trips: a chunk then
-// takes 8 round trips per wave instead of 16.
+// many bytes as its V; at 128 always and at 256 for launches of few
+// workgroups (WIDE), which are bound by each wave's chain of memory round
+// trips: a chunk then takes 8 round trips per wave instead of 16.
 template <int DK, bool WIDE> constexpr bool pipe_dual()
 {
     return DK > 256 || WIDE;
@@ -658,10 +658,13 @@ void pipe_kv_kernel(Params p)
     }
 }
 
-// Launches of fewer (chunk, unit, KV head) items than this take the wide
-// layout at head dims 128 and 256: at most one workgroup per CU, so each
-// workgroup's chain of round trips is the time.
-constexpr int64_t kPipeWideMaxItems = 256;
+// Which launches take the wide layout. Head dim 128: all (its narrow
+// workgroup keeps only 16 KiB in flight; measured on MI355X the wide one was
+// 1.1-1.7x faster from 2K to 32K keys with 8 KV heads). Head dim 256: fewer
+// (chunk, unit, KV head) items than this, where each workgroup's chain of
+// round trips is the time (1.04-1.14x faster at 32-256 items, even at 512;
+// at 1024 items, the 32K decode, the narrow layout is 5 % faster).
+constexpr int64_t kPipeWideMaxItems256 = 512;
 
 template <int DK, int MODE, bool FULL, bool WIDE>
 static void launch_dk(const Params &p, dim3 grid, hipStream_t stream)
@@ -672,13 +675,10 @@ static void launch_dk(const Params &p, dim3 grid, hipStream_t stream)
 template <int MODE, bool FULL> hipError_t launch_mode(const Params &p, hipStream_t stream)
 {
     const dim3 grid(p.nch, p.nkv * p.units);
-    const bool wide = (int64_t)p.nch * p.nkv * p.units < kPipeWideMaxItems;
+    const bool wide = (int64_t)p.nch * p.nkv * p.units < kPipeWideMaxItems256;
     switch (p.dk) {
     case 64: launch_dk<64, MODE, FULL, false>(p, grid, stream); break;
-    case 128:
-        wide ? launch_dk<128, MODE, FULL, true>(p, grid, stream)
-             : launch_dk<128, MODE, FULL, false>(p, grid, stream);
-        break;
+    case 128: launch_dk<128, MODE, FULL, true>(p, grid, stream); break;
     case 256:
         wide ? launch_dk<256, MODE, FULL, true>(p, grid, stream)
              : launch_dk<256, MODE, FULL, false>(p, grid, stream);
