@@ -461,7 +461,7 @@ enum PipeMode { kDirect = 0, kPartial = 1 };
 
 template <int DK, int MODE, bool FULL, bool WIDE>
 __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, int c,
-                                           PipeLds<DK, WIDE> &s, int vw)
+                                           PipeLds<DK, WIDE> &s, int vw, int ci)
 {
     constexpr int VD = pipe_value_dims<DK, WIDE>();
     static_assert(VD % 64 == 0, "whole 64-dim output groups per value wave");
@@ -594,7 +594,7 @@ __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, i
         return;
     }
     { // chunk partial for the combine kernel
-        const int64_t slot = ((int64_t)kvl * p.nrows_pad + row) * p.nch + blockIdx.x;
+        const int64_t slot = ((int64_t)kvl * p.nrows_pad + row) * p.nch + ci;
         float *wo = p.ws_o + slot * p.dk;
 #pragma unroll
         for (int a = 0; a < NQ; ++a)
@@ -635,10 +635,11 @@ template <int DK, bool FULL> constexpr int pipe_waves_per_simd()
 // wide layout at head dims up to 256.
 template <int DK, int MODE, bool FULL, bool WIDE>
 __global__ __launch_bounds__((pipe_threads<DK, WIDE>()), (pipe_waves_per_simd<DK, FULL>()))
-void pipe_kv_kernel(Params p)
+void pipe_kv_kernel(Params p, int c0)
 {
     __shared__ PipeLds<DK, WIDE> s;
-    const int c = p.c_lo + blockIdx.x;
+    const int ci = c0 + (int)blockIdx.x; // the launch's chunk index
+    const int c = p.c_lo + ci;
     const int unit = blockIdx.y % p.units;
     const int kvl = blockIdx.y / p.units;
     const int wave = threadIdx.x >> 6;
@@ -646,14 +647,14 @@ void pipe_kv_kernel(Params p)
         if (wave == 0)
             score_wave<DK, FULL>(p, unit, kvl, c, s);
         else
-            value_wave<DK, MODE, FULL, WIDE>(p, unit, kvl, c, s, wave - 1);
+            value_wave<DK, MODE, FULL, WIDE>(p, unit, kvl, c, s, wave - 1, ci);
     } else {
         if (wave == 0) {
             score_wave_dual<DK, FULL, 0, WIDE>(p, unit, kvl, c, s);
         } else if (wave == 1) {
             score_wave_dual<DK, FULL, 1, WIDE>(p, unit, kvl, c, s);
         } else {
-            value_wave<DK, MODE, FULL, WIDE>(p, unit, kvl, c, s, wave - 2);
+            value_wave<DK, MODE, FULL, WIDE>(p, unit, kvl, c, s, wave - 2, ci);
         }
     }
 }
@@ -667,38 +668,48 @@ void pipe_kv_kernel(Params p)
 constexpr int64_t kPipeWideMaxItems256 = 512;
 
 template <int DK, int MODE, bool FULL, bool WIDE>
-static void launch_dk(const Params &p, dim3 grid, hipStream_t stream)
+static void launch_dk(const Params &p, dim3 grid, int c0, hipStream_t stream)
 {
-    pipe_kv_kernel<DK, MODE, FULL, WIDE><<<grid, pipe_threads<DK, WIDE>(), 0, stream>>>(p);
+    pipe_kv_kernel<DK, MODE, FULL, WIDE><<<grid, pipe_threads<DK, WIDE>(), 0, stream>>>(p, c0);
 }
 
-template <int MODE, bool FULL> hipError_t launch_mode(const Params &p, hipStream_t stream)
+// Chunks [c0, c0 + n) of the launch.
+template <int MODE, bool FULL>
+hipError_t launch_mode(const Params &p, int c0, int n, hipStream_t stream)
 {
-    const dim3 grid(p.nch, p.nkv * p.units);
-    const bool wide = (int64_t)p.nch * p.nkv * p.units < kPipeWideMaxItems256;
+    const dim3 grid(n, p.nkv * p.units);
+    const bool wide = (int64_t)n * p.nkv * p.units < kPipeWideMaxItems256;
     switch (p.dk) {
-    case 64: launch_dk<64, MODE, FULL, false>(p, grid, stream); break;
-    case 128: launch_dk<128, MODE, FULL, true>(p, grid, stream); break;
+    case 64: launch_dk<64, MODE, FULL, false>(p, grid, c0, stream); break;
+    case 128: launch_dk<128, MODE, FULL, true>(p, grid, c0, stream); break;
     case 256:
-        wide ? launch_dk<256, MODE, FULL, true>(p, grid, stream)
-             : launch_dk<256, MODE, FULL, false>(p, grid, stream);
+        wide ? launch_dk<256, MODE, FULL, true>(p, grid, c0, stream)
+             : launch_dk<256, MODE, FULL, false>(p, grid, c0, stream);
         break;
-    case 512: launch_dk<512, MODE, FULL, true>(p, grid, stream); break;
+    case 512: launch_dk<512, MODE, FULL, true>(p, grid, c0, stream); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
-template <bool FULL> hipError_t launch_full(const Params &p, hipStream_t stream)
+template <bool FULL> hipError_t launch_full(const Params &p, int c0, int n, hipStream_t stream)
 {
-    return p.ws_o == nullptr ? launch_mode<kDirect, FULL>(p, stream)
-                             : launch_mode<kPartial, FULL>(p, stream);
+    return p.ws_o == nullptr ? launch_mode<kDirect, FULL>(p, c0, n, stream)
+                             : launch_mode<kPartial, FULL>(p, c0, n, stream);
+}
+
+// Chunks [c0, c0 + n) of the launch, their partials in the launch's chunk
+// slots (the chunk-split prefill runs its last round's chunk this way).
+hipError_t launch_pipe_kv_chunks(const Params &p, int c0, int n, hipStream_t stream)
+{
+    return p.dim == p.dk ? launch_full<true>(p, c0, n, stream)
+                         : launch_full<false>(p, c0, n, stream);
 }
 
 // Direct output for a single chunk, chunk partials otherwise.
 hipError_t launch_pipe_kv(const Params &p, hipStream_t stream)
 {
-    return p.dim == p.dk ? launch_full<true>(p, stream) : launch_full<false>(p, stream);
+    return launch_pipe_kv_chunks(p, 0, p.nch, stream);
 }
 
 } // namespace pcl

@@ -18,16 +18,18 @@
 //
 // split != 0: the workgroup computes the single chunk c_lo + z0 + blockIdx.z
 // and writes its chunk partial for the combine kernels. A split launch whose
-// chunk items leave a small last round runs that round's chunks as
-// single-wave workgroups of 16 rows instead (more, shorter items fill the
-// CUs); each row's arithmetic is the same either way.
+// chunk items leave a small last round runs that round's chunk through the
+// pipelined decode kernel instead (one (16-row unit, chunk) item per
+// workgroup, K/V streamed from L2 by four waves: more, shorter items fill
+// the CUs); each row's arithmetic is the same either way.
 #include "attention_device.hpp"
 
 namespace pcl {
 
+hipError_t launch_pipe_kv_chunks(const Params &p, int c0, int n, hipStream_t stream);
+
 constexpr int kTiledWaves = 8;
 constexpr int kTiledRows = kTiledWaves * kRows; // 128
-constexpr int kTailWaves = 1; // waves of the workgroups of a split launch's tail
 
 template <int DK> struct TiledLds {
     static constexpr int tileFloats = kTile * DK;
@@ -419,11 +421,9 @@ template <int DK, int W> static hipError_t configure_tiled()
     return hipSuccess;
 }
 
-// Chunks of a split launch to run as single-wave workgroups: the last chunk
-// when the 8-wave items leave a last round of at most one chunk's items and
-// the tail's 16-row items fit one round. A lone wave is latency-bound: it
-// takes ~0.8 of an 8-wave item's time per chunk (canvas 256 x 2304 on
-// MI355X: 0.175 -> 0.157 ms), so a tail of two chunks would lose. 0: no tail.
+// Chunks of a split launch to run as (16-row unit, chunk) items of the
+// pipelined kernel: the last chunk when the 8-wave items leave a last round
+// of at most one chunk's items and the tail's items fit one round. 0: none.
 static int tail_chunks(const Params &p, int nqb, int cus)
 {
     const int64_t per_chunk = (int64_t)nqb * p.nkv;
@@ -449,14 +449,7 @@ template <int DK> static hipError_t launch_tiled_dk(const Params &p, int split, 
     e = hipGetLastError();
     if (e != hipSuccess || !tail)
         return e;
-    e = configure_tiled<DK, kTailWaves>();
-    if (e != hipSuccess)
-        return e;
-    const int nub = (p.nrows + kTailWaves * kRows - 1) / (kTailWaves * kRows);
-    const dim3 tgrid(nub * p.nkv, 1, tail);
-    tiled_kernel<DK, kTailWaves>
-        <<<tgrid, 64 * kTailWaves, TiledLds<DK>::bytes, stream>>>(p, split, p.nch - tail);
-    return hipGetLastError();
+    return launch_pipe_kv_chunks(p, p.nch - tail, tail, stream);
 }
 
 int tiled_rows(int)
