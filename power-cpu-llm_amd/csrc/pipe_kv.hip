@@ -1,25 +1,28 @@
-// Pipelined split-KV decode for gfx950: a score wave and value waves per
-// (256-key chunk, 16-row unit).
+// Pipelined split-KV decode for gfx950: score waves and value waves per
+// (256-key chunk, 16-row unit, KV head).
 //
-// Workgroup = 1 score wave + one value wave per 256 output dims. The score
-// wave streams K, runs the canonical score chain and online softmax of each
-// tile (attention_device.hpp) and hands the tile's probabilities, alpha and
-// row sum to the value waves through a double-buffered LDS slot. The value
-// waves stream V and run the P.V chain one tile behind. One barrier per tile
-// keeps the workgroup in step; at head dim 256 the score and value waves'
-// MFMA work is balanced (128 MFMAs each per tile). At head dim 512 two score
-// waves share Q^T in LDS and two value waves split the output dims.
+// The narrow layout (head dims 64 and 256 in long launches): one score wave
+// and one value wave. The score wave streams K, runs the canonical score
+// chain and online softmax of each tile (attention_device.hpp) and hands the
+// tile's probabilities, alpha and row sum to the value wave through a
+// double-buffered LDS slot. The value wave streams V and runs the P.V chain
+// one tile behind. One barrier per tile keeps the workgroup in step; at head
+// dim 256 the score and value waves' MFMA work is balanced (128 MFMAs each
+// per tile). The wide layout (head dim 512; 128; 256 in short launches): two
+// score waves sharing Q^T in LDS and two value waves splitting the output
+// dims (pipe_dual below).
 //
-// Up to head dim 256 each wave keeps exactly one 16-key block of K or V in
+// In the narrow layout each wave keeps exactly one 16-key block of K or V in
 // flight, loading the next block into the same registers as its MFMAs
 // consume them: each 32-dim K slice (each 4-key V slice) is reloaded right
 // after the MFMAs that read it, so a block's MFMA time overlaps the next
 // block's memory latency (issuing the whole next block only after the last
-// MFMA cost ~10 % at 32K). At head dim 512 each wave holds 8 KiB (16 keys x
-// 128 dims of K, 8 keys x 256 dims of V) and reloads it whole after its
-// MFMAs: at 127 VGPRs four workgroups share a CU, so a 128K decode's 1024
-// workgroups are all resident (3.5 % faster than 16 KiB pieces at three per
-// CU, which left a third round); early reloads there cost 10-40 %.
+// MFMA cost ~10 % at 32K). The wide layout reloads whole pieces after the
+// MFMAs (early reloads there cost 9-40 %). At head dim 512 each wave holds
+// 8 KiB (16 keys x 128 dims of K, 8 keys x 256 dims of V): at 127 VGPRs four
+// workgroups share a CU, so a 128K decode's 1024 workgroups are all resident
+// (3.5 % faster than 16 KiB pieces at three per CU, which left a third
+// round).
 template <int DK, bool WIDE> constexpr bool pipe_slice_loads();
 // Measured on MI355X with inputs larger than the last-level cache, one block
 // in flight per wave streams at the HBM limit (~6.9 TB/s for a pure K+V read)
