@@ -371,6 +371,37 @@ def test_every_kernel_gives_identical_bits(torch, ctx, oracle, case):
         assert_parity(outs[1][i], want, dim)
 
 
+def test_split_launch_tail_with_masks_segments_and_kv_ranges(torch, ctx, oracle):
+    # the canvas shape (4 row blocks x 8 KV heads x 9 chunks = 288 items on
+    # 256 CUs) leaves one chunk's items for a last round, which runs as
+    # pipelined-kernel items: with an explicit mask and the canvas K/V as a
+    # second segment every kernel keeps the bits (a 5-head sub-range, 180
+    # items, takes no tail and is checked the same way)
+    qheads, kvh, dim, nq, nkeys = 16, 8, 256, 256, 2304
+    g = np.random.default_rng(0x7A11)
+    q = prescale(g.standard_normal((nq, qheads * dim), dtype=np.float32), dim)
+    k = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+    v = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+    mask = g.random((nq, nkeys)) < 0.7
+    mask[:, -1] = True
+    outs = {}
+    for kernel in (1, 2, 3, 4, 5):
+        for kv in [(0, kvh), (2, 7)]:
+            out, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel, mask=mask,
+                                split_at=nkeys - nq, kv=kv)
+            assert err == 0
+            outs[(kernel, kv)] = out
+    for kv in [(0, kvh), (2, 7)]:
+        for kernel in (2, 3, 4, 5):
+            assert np.array_equal(bits(outs[(1, kv)]), bits(outs[(kernel, kv)])), (kernel, kv)
+    group = qheads // kvh
+    for i in (0, nq - 1):
+        ok, want = oracle.heads(q[i], k.reshape(-1), v.reshape(-1), qheads, kvh, dim, nkeys,
+                                mask[i].astype(np.uint8), 2 * group, 7 * group)
+        assert ok
+        assert_parity(outs[(3, (2, 7))][i], want, dim)
+
+
 def test_explicit_masks_segments_scale_and_kv_ranges_keep_bits(torch, ctx):
     qheads, kvh, dim, nq, nkeys = 16, 8, 256, 40, 777
     g = np.random.default_rng(99)
