@@ -24,6 +24,8 @@
 // the CUs); each row's arithmetic is the same either way.
 #include "attention_device.hpp"
 
+#include <atomic>
+
 namespace pcl {
 
 hipError_t launch_pipe_kv_chunks(const Params &p, int c0, int n, hipStream_t stream);
@@ -391,32 +393,43 @@ void tiled_kernel(Params p, int split, int z0)
     }
 }
 
-// Compute units of the current device (cached per device).
+constexpr int kMaxDevices = 64;
+
+// Compute units of the current device (cached per device; callers on other
+// threads with their own contexts may race here, so the cache is atomic).
 static int device_cus()
 {
-    static int cached[64] = {};
+    static std::atomic<int> cached[kMaxDevices];
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
         return 0;
-    if (!cached[dev]) {
-        int n = 0;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (!n) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             return 0;
-        cached[dev] = n;
+        cached[dev].store(n, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return n;
 }
 
+// Dynamic LDS above 64 KiB must be allowed once per kernel and device; a
+// repeated call from a racing thread is harmless.
 template <int DK, int W> static hipError_t configure_tiled()
 {
-    static bool configured = false; // dynamic LDS above 64 KiB must be allowed once
-    if (!configured) {
-        const hipError_t e = hipFuncSetAttribute((const void *)tiled_kernel<DK, W>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)TiledLds<DK>::bytes);
+    static std::atomic<bool> configured[kMaxDevices];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return e;
+    if (dev < 0 || dev >= kMaxDevices)
+        return hipErrorInvalidDevice;
+    if (!configured[dev].load(std::memory_order_acquire)) {
+        e = hipFuncSetAttribute((const void *)tiled_kernel<DK, W>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)TiledLds<DK>::bytes);
         if (e != hipSuccess)
             return e;
-        configured = true;
+        configured[dev].store(true, std::memory_order_release);
     }
     return hipSuccess;
 }
