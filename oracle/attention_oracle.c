@@ -609,3 +609,18 @@ bool oracle_threaded_attention(int binary32, int threads, const float *query, si
     free(jobs);
     return ok;
 }
+
+void oracle_xorshift_units(uint64_t *state, float scale, size_t n, float *out)
+{
+    uint64_t x = *state;
+    for (size_t i = 0; i < n; ++i) {
+        x ^= x << 13;
+        x ^= x >> 7;
+        x ^= x << 17;
+        float u = (float)(x % 20001) / 10000.0f - 1.0f;
+        if (scale != 1.0f)
+            u = u * scale;
+        out[i] = u;
+    }
+    *state = x;
+}

@@ -133,6 +133,12 @@ bool oracle_rope(const float *x, size_t heads, size_t dim, size_t position, floa
  * reference's platform. */
 uint64_t oracle_libm_digest(int which);
 
+/* Test input generator, not on the attention path: the reference tests'
+ * xorshift64 stream (src/kernels/quantized/int8/tests.rs:15-33). Writes
+ * out[i] = (f32(next % 20001) / 10000 - 1) * scale, every operation in
+ * binary32 (the multiply skipped when scale == 1), and advances *state. */
+void oracle_xorshift_units(uint64_t *state, float scale, size_t n, float *out);
+
 /* Output block primitives. p9_ref_matvec (src/kernels/portable/
  * reference.rs:36-78): out[r] = f32(sequential f64 sum over c ascending of
  * f64(m[r][c]) * f64(x[c])); p9_ref_add: out = a + b in f32. */

@@ -43,6 +43,9 @@ def load():
     lib.oracle_encoder_mask.argtypes = [sz, sz, sz, sz, ctypes.c_int, u8p]
     lib.oracle_retained_count.restype = sz
     lib.oracle_retained_count.argtypes = [sz, sz, ctypes.c_int]
+    lib.oracle_xorshift_units.restype = None
+    lib.oracle_xorshift_units.argtypes = [ctypes.POINTER(ctypes.c_uint64), ctypes.c_float, sz,
+                                          fp]
     lib.oracle_threaded_attention.restype = ctypes.c_bool
     lib.oracle_threaded_attention.argtypes = [ctypes.c_int, ctypes.c_int, fp, sz, fp, fp, sz, sz,
                                               sz, sz, ctypes.c_int, sz, sz, sz, fp]
@@ -307,3 +310,12 @@ def attention_output(attended, weights, post_scale, eps, residual, rows, cols):
     (projected, residual + rms_norm(projected, post_scale, eps))."""
     projected = matvec(weights, attended, rows, cols)
     return projected, add(residual, rms_norm(projected, post_scale, eps))
+
+
+def xorshift_units(state, n, scale=1.0):
+    """n values of the reference tests' xorshift64 stream from `state`
+    (oracle_xorshift_units); returns (values, the advanced state)."""
+    st = ctypes.c_uint64(state)
+    out = np.empty(n, np.float32)
+    load().oracle_xorshift_units(ctypes.byref(st), np.float32(scale), n, _f(out))
+    return out, int(st.value)

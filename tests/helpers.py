@@ -31,6 +31,13 @@ class Rng:
             out = (out * np.float32(scale)).astype(np.float32)
         return out
 
+    def units_c(self, n, scale=1.0):
+        """units() through the oracle's C generator (for inputs of millions of
+        values); the same values and state, which a CPU test checks."""
+        from oracle import binding
+        out, self.state = binding.xorshift_units(self.state, n, scale)
+        return out
+
 
 def normals(seed, n):
     """Seeded i.i.d. N(0,1) f32 (numpy PCG64, deterministic across hosts)."""

@@ -171,6 +171,25 @@ def test_attention_multi_kv_ranges_match_single_queries(kernels, oracle):
                     assert np.array_equal(bits(part[i]), bits(want)), (kv, i, masked)
 
 
+def test_attention_multi_throughput_shapes(kernels, oracle):
+    # the shapes and inputs of int8/tests.rs:770-809 (queries unit() * 0.1,
+    # no mask): 1279 and 3194 keys end inside a chunk; every query row
+    # matches the exact oracle, and the multi call equals single calls
+    rng = Rng(7)
+    for qheads, kvh, dim, nkeys, nq in [(16, 8, 256, 1279, 8), (16, 2, 512, 3194, 8)]:
+        queries = [rng.units_c(qheads * dim, 0.1) for _ in range(nq)]
+        keys = rng.units_c(nkeys * kvh * dim)
+        values = rng.units_c(nkeys * kvh * dim)
+        multi = kernels.attention_multi(queries, keys, values, kvh, dim, None)
+        for i, q in enumerate(queries):
+            ok, want = oracle.heads(q, keys, values, qheads, kvh, dim, nkeys, None)
+            assert ok
+            assert_parity(multi[i], want, dim)
+        for i in (0, nq - 1):
+            single = kernels.attention(queries[i], keys, values, kvh, dim, None)
+            assert np.array_equal(bits(multi[i]), bits(single)), (dim, i)
+
+
 def run_threads(fn, args, timeout=60.0):
     """Runs fn(*a) for every a in args on its own thread; re-raises the first
     failure (ctypes releases the GIL, so the library calls overlap)."""

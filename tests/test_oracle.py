@@ -280,3 +280,19 @@ def test_non_finite_inputs_are_errors(oracle):
     assert oracle.attention_heads_checked(q, bad_k, v, kvh, dim)[0] == 3
     assert not oracle.heads(q, k, bad_v, qheads, kvh, dim, nkeys, binary32=True)[0]
     assert not oracle.heads(q, bad_k, v, qheads, kvh, dim, nkeys, binary32=True)[0]
+
+
+def test_c_xorshift_stream_equals_the_python_generator(oracle):
+    # The reference tests' generator (int8/tests.rs:15-33), whose Python form
+    # follows it line by line; the C form feeds the large GPU cases.
+    for seed, scale in [(7, 1.0), (7, 0.1), (0xa77e, 1.0), (0x7f4a7c159e3779b9, 0.1)]:
+        a, b = Rng(seed), Rng(seed)
+        for n in (1, 3000, 17):
+            want = a.units(n, scale)
+            got = b.units_c(n, scale)
+            assert np.array_equal(want.view(np.uint32), got.view(np.uint32)), (seed, scale, n)
+            assert a.state == b.state
+    # a known point of the stream: xorshift64 of 1 is 0x40822041
+    r = Rng(1)
+    r.units_c(1)
+    assert r.state == 0x40822041
