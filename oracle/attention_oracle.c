@@ -385,6 +385,120 @@ void oracle_rms_norm(const float *x, const float *scale, size_t n, float eps, fl
     }
 }
 
+/* sincosf of glibc 2.28's generic s_sincosf.c / s_sincosf.h, which the
+ * reference ports bit for bit (libm::sincosf, src/libm.rs:350-497): |x| is
+ * reduced by k*pi/2 (a table below 9pi/4, two pi/2 pieces below 2^23, 28-bit
+ * pieces of 4/pi above) and evaluated in f64 with Chebyshev forms on
+ * [-pi/4, pi/4], then rounded to binary32. The multiply-adds are fused
+ * exactly where the reference fuses them (its mul_add calls; glibc built with
+ * FMA contraction); every other operation is unfused. The newer glibc of
+ * this host differs from it in the last bit on some inputs. */
+static const double sc_cos[5] = {-0x1.ffffffffe98aep-2, 0x1.55555545c50c7p-5,
+                                 -0x1.6c16b348b6874p-10, 0x1.a00eb9ac43ccp-16,
+                                 -0x1.23c97dd8844d7p-22};
+static const double sc_sin[5] = {-0x1.5555555551cd9p-3, 0x1.1111110c2688bp-7,
+                                 -0x1.a019f8b4bd1f9p-13, 0x1.71d7264e6b5b4p-19,
+                                 -0x1.a947e1674b58ap-26};
+static const double sc_pio2[6] = {0.0, 0x1.921fb54442d18p+0, 0x1.921fb54442d18p+1,
+                                  0x1.2d97c7f3321d2p+2, 0x1.921fb54442d18p+2,
+                                  0x1.f6a7a2955385ep+2};
+static const double sc_invpio4[8] = {0.0,           0x1.45f306cp+0,  0x1.c9c882ap-28,
+                                     0x1.4fe13a8p-58, 0x1.f47d4d0p-85, 0x1.bb81b6cp-112,
+                                     0x1.4acc9e0p-142, 0x1.0e4107cp-169};
+
+static double sc_sin_poly(double t, double t2)
+{
+    double p = fma(sc_sin[4], t2, sc_sin[3]);
+    for (int k = 2; k >= 0; --k)
+        p = fma(t2, p, sc_sin[k]);
+    return fma(t * t2, p, t);
+}
+
+static double sc_cos_poly(double t2)
+{
+    double p = fma(sc_cos[4], t2, sc_cos[3]);
+    for (int k = 2; k >= 0; --k)
+        p = fma(t2, p, sc_cos[k]);
+    return fma(t2, p, 1.0);
+}
+
+/* t: reduced |x|; n = trunc(|x| / (pi/4)) + 1 selects the form and sign. */
+static void sc_reduced(double t, uint32_t n, unsigned negative, float *s, float *c)
+{
+    const double t2 = t * t;
+    const double sv = (n & 2) == 0 ? sc_sin_poly(t, t2) : sc_cos_poly(t2);
+    const uint32_t m = n + 2;
+    const double cv = (m & 2) == 0 ? sc_sin_poly(t, t2) : sc_cos_poly(t2);
+    *s = (float)((((n >> 2) & 1) ^ negative) ? -sv : sv);
+    *c = (float)(((m >> 2) & 1) ? -cv : cv);
+}
+
+static void glibc228_sincosf(float x, float *s, float *c)
+{
+    const double pi_4 = 0x1.921fb54442d18p-1, inv_pi_4 = 0x1.45f306dc9c883p+0;
+    const double t = (double)x, at = fabs(t);
+    if (at < pi_4) {
+        if (at >= 0x1p-5) {
+            const double t2 = t * t;
+            *s = (float)sc_sin_poly(t, t2);
+            *c = (float)sc_cos_poly(t2);
+            return;
+        }
+        if (at >= 0x1p-27) {
+            const double t2 = t * t, t3 = t * t2;
+            *c = (float)fma(t2, fma(t3, 0x1.55514b178dac5p-5, -0x1.fffffff5cc6fdp-2), 1.0);
+            *s = (float)fma(t3, fma(t2, 0x1.110f475cec8c5p-7, -0x1.555555543d49dp-3), t);
+            return;
+        }
+        *s = (float)(t != 0.0 ? fma(-t, 0x1p-50, t) : t);
+        *c = (float)(1.0 - at);
+        return;
+    }
+    const unsigned negative = x < 0.0f;
+    if (at < 0x1.c463abeccb2bbp+2) { /* 9 pi/4 */
+        const uint32_t n = (uint32_t)fma(at, inv_pi_4, 1.0);
+        sc_reduced(at - sc_pio2[n / 2], n, negative, s, c);
+        return;
+    }
+    if (!isfinite(at)) {
+        *s = *c = x - x;
+        return;
+    }
+    if (at < 0x1p23) {
+        const uint32_t n = (uint32_t)(at * inv_pi_4) + 1;
+        const double k = (double)(n / 2);
+        const double r = fma(-k, 0x1.0b4611a626332p-34, fma(-k, 0x1.921fb544p+0, at));
+        sc_reduced(r, n, negative, s, c);
+        return;
+    }
+    /* |x| >= 2^23: the product of |x| with four 28-bit pieces of 4/pi from
+     * the piece that keeps the integer part below 2^53 */
+    uint32_t bits;
+    const float ax = fabsf(x);
+    memcpy(&bits, &ax, 4);
+    const int e = ((int)(bits >> 23) - 127 + 3) / 28;
+    double a = sc_invpio4[e] * at;
+    const double b = sc_invpio4[e + 1] * at, cc = sc_invpio4[e + 2] * at,
+                 d = sc_invpio4[e + 3] * at;
+    uint64_t l = (uint64_t)a;
+    l &= ~(uint64_t)7;
+    a -= (double)l;
+    double f = a + b;
+    l = (uint64_t)f;
+    f = a - (double)l;
+    if (l & 1) {
+        f -= 1.0;
+        f = d + (cc + (b + f));
+    } else {
+        f = d + (cc + (b + f));
+        if (f > 1.0) {
+            l += 1;
+            f -= 2.0;
+        }
+    }
+    sc_reduced(f * pi_4, (uint32_t)l + 1, negative, s, c);
+}
+
 /* p9_ref_rope (reference.rs:277-318). */
 bool oracle_rope(const float *x, size_t heads, size_t dim, size_t position, float base,
                  const float *factors, float *out)
@@ -398,7 +512,7 @@ bool oracle_rope(const float *x, size_t heads, size_t dim, size_t position, floa
         if (!isfinite(angle))
             return false;
         float s, c;
-        sincosf(angle, &s, &c);
+        glibc228_sincosf(angle, &s, &c);
         for (size_t h = 0; h < heads; ++h) {
             const size_t a = h * dim + i, b = h * dim + i + half;
             const float xa = x[a], xb = x[b];
@@ -440,7 +554,7 @@ uint64_t oracle_libm_digest(int which)
         for (uint64_t k = 0; k <= 0xffffffffULL / 61; ++k) {
             const float x = from_bits((uint32_t)(k * 61));
             float s, c;
-            sincosf(x, &s, &c);
+            glibc228_sincosf(x, &s, &c);
             h = fnv(fnv(h, digest_bits(s, isnan(x))), digest_bits(c, isnan(x)));
         }
         return h;

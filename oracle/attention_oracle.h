@@ -122,12 +122,14 @@ void oracle_cache_commit(oracle_layer_cache *c);
  * inv = 1 / sqrt(sum / n + eps) in f64, out = f32(x * inv) [* scale in f32]. */
 void oracle_rms_norm(const float *x, const float *scale, size_t n, float eps, float *out);
 /* p9_ref_rope (reference.rs:277-318): NeoX pairs (i, i + dim/2), f32
- * frequencies 1 / powf(base, 2i/dim) [/ factor_i], f32 angles, the C
- * library's sincosf; false on a non-finite angle. */
+ * frequencies 1 / powf(base, 2i/dim) [/ factor_i], f32 angles, glibc 2.28's
+ * sincosf (the reference's libm::sincosf, src/libm.rs:350); false on a
+ * non-finite angle. */
 bool oracle_rope(const float *x, size_t heads, size_t dim, size_t position, float base,
                  const float *factors, float *out);
-/* FNV-1a digests of the C library's powf (which = 0) or sincosf (which = 1)
- * over the inputs of the reference's libm digest tests
+/* FNV-1a digests of the C library's powf (which = 0) or the glibc 2.28
+ * sincosf of oracle_rope (which = 1) over the inputs of the reference's libm
+ * digest tests
  * (src/libm/tests.rs:20-62, 87-136); NaNs that an invalid operation
  * generates are counted with the positive default-NaN bits of the
  * reference's platform. */

@@ -10,7 +10,8 @@
 // Q and K then rotate pairs (j, j + dim/2) (p9_ref_rope, reference.rs:277-318):
 //   y_j' = y_j*c - y_{j+h}*s,  y_{j+h}' = y_{j+h}*c + y_j*s   (f32, unfused),
 // with (s, c) = sincosf(f32(position) * f32(1 / powf(base, 2j/dim)) / factor_j)
-// from a host-built table (the C library's powf and sincosf). V is normalised
+// from a host-built table (the C library's powf; glibc 2.28's sincosf, which
+// the reference's libm reproduces, from host_sincosf.hpp). V is normalised
 // without scale and not rotated; a global layer without a V projection uses
 // the raw K as V (attention.rs:121-129).
 //
@@ -22,6 +23,7 @@
 // step's heads run on many CUs at once.
 #include "attention_device.hpp"
 #include "context.hpp"
+#include "host_sincosf.hpp"
 #include "pcl_attention.h"
 
 #include <algorithm>
@@ -235,7 +237,8 @@ bool finite_all(const float *x, int64_t n)
 
 // (sin, cos) of every pair of positions [from, to): p9_ref_rope's
 // frequencies and angles in f32 (reference.rs:294-305), the C library's
-// powf and sincosf. False on a non-finite angle.
+// powf (equal to the reference's libm powf on its digest inputs) and glibc
+// 2.28's sincosf. False on a non-finite angle.
 bool rope_rows(const pcl_head_transform *t, int64_t from, int64_t to, float *out)
 {
     const int64_t half = t->dim / 2;
@@ -252,7 +255,7 @@ bool rope_rows(const pcl_head_transform *t, int64_t from, int64_t to, float *out
             if (!std::isfinite(angle))
                 return false;
             float s, c;
-            sincosf(angle, &s, &c);
+            pcl::sincosf_glibc228(angle, &s, &c);
             out[2 * ((p - from) * half + i)] = s;
             out[2 * ((p - from) * half + i) + 1] = c;
         }

@@ -3,14 +3,16 @@ HeadTransform (src/engine/attention.rs:51-243).
 
 CPU tests pin the oracle's restatement of p9_ref_rms_norm and p9_ref_rope
 (src/kernels/portable/reference.rs:11-33, 277-318) with the reference's own
-known answers (src/kernels/reference/tests.rs:4-11, 79-113), its libm digest
-for powf (src/libm/tests.rs:77, 134-137), closed forms (the RMS of a
+known answers (src/kernels/reference/tests.rs:4-11, 79-113), its libm digests
+for powf and sincosf (src/libm/tests.rs:20-92, 136), closed forms (the RMS of a
 normalised row, the rotation's invariant pair norms, f64 angles) and the
 prepare() structure (V unscaled and not rotated, K as V for global layers).
 GPU tests compare the device transform with the oracle bit for bit, alone,
 fused into the cache append, and end to end through attention.
 """
 import math
+import os
+import subprocess
 
 import numpy as np
 import pytest
@@ -18,6 +20,8 @@ import pytest
 from helpers import normals
 
 POWF_DIGEST = 0xE03CB0D507CDCB95  # src/libm/tests.rs:77
+SINCOSF_DIGEST = 0x684C340564E05BFC  # src/libm/tests.rs:71
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 # ---- oracle pinning (CPU) --------------------------------------------------
@@ -26,6 +30,51 @@ def test_powf_matches_the_reference_libm_digest(oracle):
     # the rotary frequencies' powf gives the reference's bits on all 2^22
     # digest inputs (src/libm/tests.rs:53-62, 134-137)
     assert oracle.libm_digest(0) == POWF_DIGEST
+
+
+def test_sincosf_matches_the_reference_libm_digest(oracle):
+    # the rotation's (sin, cos) give the reference's bits on every 61st
+    # binary32 pattern (src/libm/tests.rs:20-22, 86-92): glibc 2.28's sincosf, which
+    # the reference's libm ports (the newer C library here differs)
+    assert oracle.libm_digest(1) == SINCOSF_DIGEST
+
+
+HOST_DIGEST_MAIN = r"""
+#include "host_sincosf.hpp"
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+static uint64_t fnv(uint64_t h, uint32_t v) { return (h ^ v) * 0x100000001b3ULL; }
+static uint32_t bits_of(float r, bool input_nan) {
+    uint32_t b; std::memcpy(&b, &r, 4);
+    return (!input_nan && std::isnan(r)) ? 0x7fc00000u : b;
+}
+int main() {
+    uint64_t h = 0xcbf29ce484222325ULL;
+    for (uint64_t k = 0; k <= 0xffffffffULL / 61; ++k) {
+        const uint32_t u = (uint32_t)(k * 61);
+        float x; std::memcpy(&x, &u, 4);
+        float s, c;
+        pcl::sincosf_glibc228(x, &s, &c);
+        h = fnv(fnv(h, bits_of(s, std::isnan(x))), bits_of(c, std::isnan(x)));
+    }
+    std::printf("%llx\n", (unsigned long long)h);
+}
+"""
+
+
+def test_product_rotation_table_sincosf_matches_the_reference_digest(tmp_path):
+    # the product's host sincosf (the rotation table's), compiled on its own
+    # with the library's no-contraction flag, over the same digest inputs
+    src = tmp_path / "digest.cpp"
+    src.write_text(HOST_DIGEST_MAIN)
+    exe = tmp_path / "digest"
+    subprocess.run(["g++", "-O2", "-std=c++17", "-ffp-contract=off",
+                    "-I", os.path.join(ROOT, "power-cpu-llm_amd", "csrc"), str(src), "-o",
+                    str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+    assert int(out.strip(), 16) == SINCOSF_DIGEST
 
 
 def test_direct_rms_scale_and_unscaled_normalization(oracle):
