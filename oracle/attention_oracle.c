@@ -7,10 +7,14 @@
  *
  * Build with -O2 -ffp-contract=off (oracle/Makefile): the reference is Rust,
  * which never contracts a*b+c, and uses an FMA only where it writes mul_add.
- * Transcendentals come from the host libm (exp, expf). The reference links
- * bit-exact ports of glibc 2.28's IBM exp and POWER8 expf (src/libm.rs:92,
- * 294); host glibc agrees with them to within an ulp, so this oracle matches
- * the reference to the last bit except where such an ulp decides a rounding.
+ * The reference links bit-exact ports of glibc 2.28's libm (src/libm.rs).
+ * The binary32 twin's expf and the rotation's sincosf are restated here from
+ * the same glibc 2.28 algorithms and reproduce the reference's libm digests
+ * (src/libm/tests.rs:70-92); powf is the host's, which reproduces its digest
+ * too. The exact path's f64 exp is the host's: the reference's (glibc 2.28's
+ * correctly rounded IBM exp) differs from it by an ulp on about 0.1 % of
+ * inputs, so the exact path matches the reference to the last bit except
+ * where such an ulp decides a rounding.
  */
 #include "attention_oracle.h"
 
@@ -18,6 +22,9 @@
 #include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
+
+/* glibc 2.28's POWER8 expf, restated below (the binary32 twin's softmax). */
+static float power8_expf(float x);
 
 /* p9_ref_attention_heads (src/kernels/portable/reference.rs:327-393). */
 bool oracle_ref_attention_heads(const float *query, const float *keys, const float *values,
@@ -76,7 +83,7 @@ static bool oracle_softmax_f32(float *scores, size_t n, const uint8_t *allowed)
     }
     float sum = 0.0f;
     for (size_t t = 0; t < n; ++t) {
-        const float e = (allowed && allowed[t] == 0) ? 0.0f : expf(scores[t] - max);
+        const float e = (allowed && allowed[t] == 0) ? 0.0f : power8_expf(scores[t] - max);
         scores[t] = e;
         sum += e;
     }
@@ -385,6 +392,89 @@ void oracle_rms_norm(const float *x, const float *scale, size_t n, float eps, fl
     }
 }
 
+static float from_bits(uint32_t b);
+
+/* expf of glibc 2.28 on POWER8 (sysdeps/powerpc/powerpc64/power8/fpu/e_expf.S),
+ * which the reference ports bit for bit (libm::expf, src/libm.rs:292-345) for
+ * the binary32 twin's softmax: x = (64n + j) ln2/64 + y, e^x = 2^n 2^(j/64)
+ * (1 + P(y)) in f64 with the table 2^(j/64) (correctly rounded; generated
+ * with 60-digit decimals), rounded once to binary32. The multiply-adds fuse
+ * where the reference's mul_add calls do. */
+static const double ex_t[64] = {
+    0x1.0000000000000p+0, 0x1.02c9a3e778061p+0, 0x1.059b0d3158574p+0,
+    0x1.0874518759bc8p+0, 0x1.0b5586cf9890fp+0, 0x1.0e3ec32d3d1a2p+0,
+    0x1.11301d0125b51p+0, 0x1.1429aaea92de0p+0, 0x1.172b83c7d517bp+0,
+    0x1.1a35beb6fcb75p+0, 0x1.1d4873168b9aap+0, 0x1.2063b88628cd6p+0,
+    0x1.2387a6e756238p+0, 0x1.26b4565e27cddp+0, 0x1.29e9df51fdee1p+0,
+    0x1.2d285a6e4030bp+0, 0x1.306fe0a31b715p+0, 0x1.33c08b26416ffp+0,
+    0x1.371a7373aa9cbp+0, 0x1.3a7db34e59ff7p+0, 0x1.3dea64c123422p+0,
+    0x1.4160a21f72e2ap+0, 0x1.44e086061892dp+0, 0x1.486a2b5c13cd0p+0,
+    0x1.4bfdad5362a27p+0, 0x1.4f9b2769d2ca7p+0, 0x1.5342b569d4f82p+0,
+    0x1.56f4736b527dap+0, 0x1.5ab07dd485429p+0, 0x1.5e76f15ad2148p+0,
+    0x1.6247eb03a5585p+0, 0x1.6623882552225p+0, 0x1.6a09e667f3bcdp+0,
+    0x1.6dfb23c651a2fp+0, 0x1.71f75e8ec5f74p+0, 0x1.75feb564267c9p+0,
+    0x1.7a11473eb0187p+0, 0x1.7e2f336cf4e62p+0, 0x1.82589994cce13p+0,
+    0x1.868d99b4492edp+0, 0x1.8ace5422aa0dbp+0, 0x1.8f1ae99157736p+0,
+    0x1.93737b0cdc5e5p+0, 0x1.97d829fde4e50p+0, 0x1.9c49182a3f090p+0,
+    0x1.a0c667b5de565p+0, 0x1.a5503b23e255dp+0, 0x1.a9e6b5579fdbfp+0,
+    0x1.ae89f995ad3adp+0, 0x1.b33a2b84f15fbp+0, 0x1.b7f76f2fb5e47p+0,
+    0x1.bcc1e904bc1d2p+0, 0x1.c199bdd85529cp+0, 0x1.c67f12e57d14bp+0,
+    0x1.cb720dcef9069p+0, 0x1.d072d4a07897cp+0, 0x1.d5818dcfba487p+0,
+    0x1.da9e603db3285p+0, 0x1.dfc97337b9b5fp+0, 0x1.e502ee78b3ff6p+0,
+    0x1.ea4afa2a490dap+0, 0x1.efa1bee615a27p+0, 0x1.f50765b6e4540p+0,
+    0x1.fa7c1819e90d8p+0
+};
+
+static float ex_reduce(float x, int near_limit)
+{
+    const double xd = (double)x;
+    const double kd = fma(xd, 0x1.71547652b82fep+6, 0x1.8p+23); /* 64/ln2, 2^23 + 2^22 */
+    const float k = (float)kd;
+    uint32_t kb;
+    memcpy(&kb, &k, 4);
+    const uint32_t j = kb & 63;
+    const double y = fma((double)(k - 12582912.0f), -0x1.62e42fefa39efp-7, xd); /* -ln2/64 */
+    const double z = y * y;
+    const double p = fma(y, fma(0x1.55550da752d4fp-3, z, 0x1.fffffffffe7c6p-1),
+                         fma(0x1.56420eb78fa85p-5, z, 0x1.00000008d6118p-1) * z);
+    const double t = ex_t[j];
+    const double r = fma(p, t, t);
+    const uint32_t n = kb & ~63u;
+    double scale;
+    if (near_limit) {
+        const uint64_t sb = ((uint64_t)(uint32_t)(n + 0xffc0u) & 0x1ffffu) << 46;
+        memcpy(&scale, &sb, 8);
+    } else {
+        const uint32_t sb = ((n + 0x1fc0u) & 0x3fffu) << 17;
+        float sf;
+        memcpy(&sf, &sb, 4);
+        scale = (double)sf;
+    }
+    return (float)(scale * r);
+}
+
+static float power8_expf(float x)
+{
+    uint32_t bits;
+    memcpy(&bits, &x, 4);
+    const uint32_t a = bits & 0x7fffffffu;
+    if (a >= 0x42ad496bu) { /* |x| >= 125 ln 2 */
+        const int negative = (bits >> 31) != 0;
+        if (a <= (negative ? 0x42cff1b4u : 0x42b17217u))
+            return ex_reduce(x, 1);
+        if (a >= 0x7f800000u) {
+            if (a != 0x7f800000u)
+                return (float)((double)x + (double)x); /* NaN */
+            return negative ? 0.0f : INFINITY;
+        }
+        const float s = from_bits(negative ? 0x0d800000u : 0x71800000u);
+        return s * s; /* underflow or overflow, rounded once */
+    }
+    if (a < 0x31800000u) /* |x| < 2^-28 */
+        return x + 1.0f;
+    return ex_reduce(x, 0);
+}
+
 /* sincosf of glibc 2.28's generic s_sincosf.c / s_sincosf.h, which the
  * reference ports bit for bit (libm::sincosf, src/libm.rs:350-497): |x| is
  * reduced by k*pi/2 (a table below 9pi/4, two pi/2 pieces below 2^23, 28-bit
@@ -550,6 +640,13 @@ static uint32_t digest_bits(float r, int inputs_nan)
 uint64_t oracle_libm_digest(int which)
 {
     uint64_t h = 0xcbf29ce484222325ULL;
+    if (which == 2) {
+        for (uint64_t k = 0; k <= 0xffffffffULL / 61; ++k) {
+            const float x = from_bits((uint32_t)(k * 61));
+            h = fnv(h, digest_bits(power8_expf(x), isnan(x)));
+        }
+        return h;
+    }
     if (which == 1) {
         for (uint64_t k = 0; k <= 0xffffffffULL / 61; ++k) {
             const float x = from_bits((uint32_t)(k * 61));

@@ -37,7 +37,8 @@ bool oracle_ref_attention_heads(const float *query, const float *keys, const flo
 
 /* a3/a4 — binary32 attention: pa_attention_f32_heads + softmax
  * (src/kernels/portable/attention.rs:14-112). 16 FMA score lanes reduced as a
- * fixed tree, f32 softmax (libm expf), FMA PV chain from +0. scratch [nkeys]. */
+ * fixed tree, f32 softmax (glibc 2.28's POWER8 expf, the reference's
+ * libm::expf), FMA PV chain from +0. scratch [nkeys]. */
 bool oracle_pa_attention_f32_heads(const float *query, const float *keys, const float *values,
                                    size_t qheads, size_t kvheads, size_t dim, size_t nkeys,
                                    const uint8_t *allowed, float *scratch, float *out,
@@ -127,9 +128,10 @@ void oracle_rms_norm(const float *x, const float *scale, size_t n, float eps, fl
  * non-finite angle. */
 bool oracle_rope(const float *x, size_t heads, size_t dim, size_t position, float base,
                  const float *factors, float *out);
-/* FNV-1a digests of the C library's powf (which = 0) or the glibc 2.28
- * sincosf of oracle_rope (which = 1) over the inputs of the reference's libm
- * digest tests
+/* FNV-1a digests of the C library's powf (which = 0), the glibc 2.28
+ * sincosf of oracle_rope (which = 1) or the glibc 2.28 POWER8 expf of the
+ * binary32 twin (which = 2) over the inputs of the reference's libm digest
+ * tests
  * (src/libm/tests.rs:20-62, 87-136); NaNs that an invalid operation
  * generates are counted with the positive default-NaN bits of the
  * reference's platform. */

@@ -296,3 +296,10 @@ def test_c_xorshift_stream_equals_the_python_generator(oracle):
     r = Rng(1)
     r.units_c(1)
     assert r.state == 0x40822041
+
+
+def test_binary32_twin_expf_matches_the_reference_libm_digest(oracle):
+    # the twin's softmax exponential gives the reference's bits on every 61st
+    # binary32 pattern (src/libm/tests.rs:20-22, 70, 80-84): glibc 2.28's
+    # POWER8 expf, which the reference's libm ports
+    assert oracle.libm_digest(2) == 0xFE568FD438D7D408
