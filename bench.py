@@ -457,7 +457,17 @@ def cpu_baseline(name, host, threads, budget_s=20.0):
         t0 = time.perf_counter()
         orc.threaded(q, nq, k, v, qh, kvh, dim, nkeys, causal, 0, fq, window, threads=1)
         one.append(time.perf_counter() - t0)
-    return med, len(times), maxerr, float(np.median(one))
+    # the binary32 twin (port of pa_attention_f32_heads, the portable-int8
+    # backends' path) with the same threads (median of 5)
+    b32 = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        ok, _ = orc.threaded(q, nq, k, v, qh, kvh, dim, nkeys, causal, 0, fq, window,
+                             threads=threads, binary32=True)
+        b32.append(time.perf_counter() - t0)
+        if not ok:
+            raise RuntimeError("oracle error")
+    return med, len(times), maxerr, float(np.median(one)), float(np.median(b32))
 
 
 def cpu_model():
@@ -551,7 +561,8 @@ def main():
     cpu = None
     if not args.no_cpu and head in hosts:
         threads = min(16, len(os.sched_getaffinity(0)))
-        med, runs, maxerr, med1 = cpu_baseline(head, hosts[head], threads, args.cpu_budget)
+        med, runs, maxerr, med1, med32 = cpu_baseline(head, hosts[head], threads,
+                                                      args.cpu_budget)
         flops, bytes_, _ = work(head)
 
         def rate(sec):
@@ -564,6 +575,9 @@ def main():
                          % (runs, head, med),
                "value_1core": rate(med1),
                "sample_1core": "5 whole calls on one thread, median %.3f s" % med1,
+               "value_binary32": rate(med32),
+               "sample_binary32": "5 whole calls of the binary32 twin (pa_attention_f32 "
+                                  "path), %d threads, median %.3f s" % (threads, med32),
                "cpu": cpu_model(),
                "gpu_vs_oracle_maxabs": maxerr}
     qh, kvh, dim, nq, nkeys, causal, window, fq, _, _ = WORKLOADS[head]
