@@ -11,10 +11,10 @@
  * The binary32 twin's expf and the rotation's sincosf are restated here from
  * the same glibc 2.28 algorithms and reproduce the reference's libm digests
  * (src/libm/tests.rs:70-92); powf is the host's, which reproduces its digest
- * too. The exact path's f64 exp is the host's: the reference's (glibc 2.28's
- * correctly rounded IBM exp) differs from it by an ulp on about 0.1 % of
- * inputs, so the exact path matches the reference to the last bit except
- * where such an ulp decides a rounding.
+ * too. The exact path's f64 exp is the host's; the reference's (glibc 2.28's
+ * table-driven IBM exp) differs from it in the last bit on some inputs, so
+ * the exact path matches the reference to the last bit except where such an
+ * ulp decides a rounding.
  */
 #include "attention_oracle.h"
 
