@@ -289,8 +289,9 @@ int pcl_head_transform_create(pcl_context *ctx, int64_t qheads, int64_t kvheads,
                               pcl_head_transform **out);
 void pcl_head_transform_destroy(pcl_head_transform *transform);
 /* HeadTransform::prepare (attention.rs:102-156) for n tokens. The rotation
- * table is built on the host (the C library's powf and sincosf) for positions
- * up to the largest seen so far and kept on the device; PCL_NON_FINITE_VALUE
+ * table is built on the host (the C library's powf; glibc 2.28's sincosf, as
+ * the reference's libm::sincosf, src/libm.rs:350) for positions up to the
+ * largest seen so far and kept on the device; PCL_NON_FINITE_VALUE
  * for a non-finite angle, PCL_RESOURCE_LIMIT beyond 2^24 positions. */
 int pcl_head_transform_prepare(pcl_head_transform *transform, const float *raw_q,
                                const float *raw_k, const float *raw_v, int64_t n,
