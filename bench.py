@@ -73,6 +73,11 @@ WORKLOADS = {
     "decode_32k_host": (16, 8, 256, 1, 32768, True, 0, 32767, "host", False),
 }
 HEADLINE = "decode_32k"
+# the metric's second half: f32 prefill attention at 4K tokens (the global
+# layer; the sliding-window layer is reported beside it)
+PREFILL = ("prefill_4k", "prefill_4k_window1024")
+PREFILL_SAMPLE_STEP = 16      # CPU baseline: every 16th query row of the prompt
+PREFILL_SAMPLE_STEP_1CORE = 128
 
 
 def traffic_bytes(name):
@@ -470,6 +475,94 @@ def cpu_baseline(name, host, threads, budget_s=20.0):
     return med, len(times), maxerr, float(np.median(one)), float(np.median(b32))
 
 
+def cpu_baseline_prefill(name, host, threads, budget_s=20.0):
+    """The oracle's exact path over a prefill, as the engine runs a prompt
+    (contiguous query ranges per worker, each query its own call with its
+    causal mask), on a sample: every PREFILL_SAMPLE_STEP-th query row of the
+    prompt, timed whole and repeated; rates count the sampled rows' own
+    algorithmic flops."""
+    from oracle import binding as orc
+    qh, kvh, dim, nq, nkeys, causal, window, fq, kind, _ = WORKLOADS[name]
+    q = host["q"].cpu().numpy().reshape(nq, qh * dim)
+    k = host["k"].cpu().numpy().reshape(-1)
+    v = host["v"].cpu().numpy().reshape(-1)
+    gpu = host["out"].cpu().numpy().reshape(nq, qh * dim)
+
+    def sample_flops(step):
+        pairs = 0
+        for i in range(0, nq, step):
+            pairs += allowed_pairs(1, nkeys, causal, window, fq + i)
+        return 4 * dim * qh * pairs
+
+    def run(step, nthreads, reps):
+        rows = np.ascontiguousarray(q[::step])
+        times, out = [], None
+        t_end = time.perf_counter() + budget_s
+        while len(times) < reps or (time.perf_counter() < t_end and len(times) < 2 * reps):
+            t0 = time.perf_counter()
+            ok, out = orc.threaded(rows.reshape(-1), rows.shape[0], k, v, qh, kvh, dim, nkeys,
+                                   causal, 0, fq, window, threads=nthreads, query_step=step)
+            times.append(time.perf_counter() - t0)
+            if not ok:
+                raise RuntimeError("oracle error")
+            if time.perf_counter() > t_end and len(times) >= reps:
+                break
+        return float(np.median(times)), len(times), out.reshape(rows.shape[0], -1)
+
+    med, runs, out = run(PREFILL_SAMPLE_STEP, threads, 3)
+    maxerr = float(np.max(np.abs(gpu[::PREFILL_SAMPLE_STEP] - out)))
+    med1, _, _ = run(PREFILL_SAMPLE_STEP_1CORE, 1, 3)
+    return {"value": sample_flops(PREFILL_SAMPLE_STEP) / med / 1e12, "unit": "TFLOP/s",
+            "cores": threads, "kind": "port",
+            "sample": "every %dth query row of the %d-token prompt (%d rows, all heads, "
+                      "their own causal%s masks), exact f64 path, %d whole runs, "
+                      "median %.3f s" % (PREFILL_SAMPLE_STEP, nq, len(range(0, nq,
+                                         PREFILL_SAMPLE_STEP)),
+                                         " + window %d" % window if window else "", runs, med),
+            "value_1core": sample_flops(PREFILL_SAMPLE_STEP_1CORE) / med1 / 1e12,
+            "sample_1core": "every %dth query row on one thread, median %.3f s"
+                            % (PREFILL_SAMPLE_STEP_1CORE, med1),
+            "gpu_vs_oracle_maxabs": maxerr}
+
+
+def cpu_share():
+    """Host threads for the CPU baseline and the affinity mask's core count.
+    The box grants this process a share of its cores (OMP_NUM_THREADS, 16 on
+    the GPU box) that can be smaller than the affinity mask; the baseline
+    uses the share and reports both."""
+    affinity = len(os.sched_getaffinity(0))
+    try:
+        share = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    except ValueError:
+        share = 0
+    threads = min(share, affinity) if share > 0 else affinity
+    return max(threads, 1), affinity
+
+
+def roofline(name, r):
+    """Roofline block of a workload's dominant kernel: the launches that
+    stream K/V (the ordered combine excluded), timed by the library's event
+    spans over the timed steps."""
+    kind = WORKLOADS[name][8]
+    stream_s = r["stream_kernel_ms"] * 1e-3
+    if kind == "output" and nq_of(name) > 32:
+        ach = r["algorithmic_flops"] / stream_s / 1e12
+        roof = {"bound": "mfma", "achieved": ach, "peak": FP64_MFMA_PEAK_TFS,
+                "unit": "TFLOP/s", "frac": ach / FP64_MFMA_PEAK_TFS,
+                "traffic": traffic_bytes(name)}
+    elif kind in ("decode", "cache", "step", "transform", "output"):
+        ach = r["algorithmic_bytes"] / stream_s / 1e9
+        roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": ach / HBM_PEAK_GBS, "traffic": traffic_bytes(name)}
+    else:
+        ach = r["algorithmic_flops"] / stream_s / 1e12
+        roof = {"bound": "mfma", "achieved": ach, "peak": FP32_MFMA_PEAK_TFS,
+                "unit": "TFLOP/s", "frac": ach / FP32_MFMA_PEAK_TFS,
+                "traffic": traffic_bytes(name)}
+    roof["kernel"] = r["kernel"]
+    return roof
+
+
 def cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -546,7 +639,7 @@ def main():
         else:
             r["frac_mfma"] = r["TFLOP/s"] / FP32_MFMA_PEAK_TFS
         results[name] = r
-        if name == HEADLINE:
+        if name == HEADLINE or name == PREFILL[0]:
             hosts[name] = host
         else:
             del host
@@ -559,8 +652,8 @@ def main():
     hr = results[head]
     kind = WORKLOADS[head][8]
     cpu = None
-    if not args.no_cpu and head in hosts:
-        threads = min(16, len(os.sched_getaffinity(0)))
+    threads, affinity = cpu_share()
+    if not args.no_cpu and head in hosts and kind == "decode":
         med, runs, maxerr, med1, med32 = cpu_baseline(head, hosts[head], threads,
                                                       args.cpu_budget)
         flops, bytes_, _ = work(head)
@@ -578,30 +671,39 @@ def main():
                "value_binary32": rate(med32),
                "sample_binary32": "5 whole calls of the binary32 twin (pa_attention_f32 "
                                   "path), %d threads, median %.3f s" % (threads, med32),
+               "affinity_cores": affinity,
                "cpu": cpu_model(),
                "gpu_vs_oracle_maxabs": maxerr}
     qh, kvh, dim, nq, nkeys, causal, window, fq, _, _ = WORKLOADS[head]
-    # roofline of the dominant kernel(s): the launches that stream K/V, timed by
-    # the library's event spans (the ordered combine is excluded)
-    stream_s = hr["stream_kernel_ms"] * 1e-3
     if kind == "host":
         # host buffers: the copies dominate; no kernel roofline applies
         value, unit = hr["GB/s"], "GB/s"
         metric = "decode-attn GB/s at 32K KV incl. host copies"
         roof = {"bound": "pcie", "achieved": value, "peak": None, "unit": "GB/s",
                 "frac": None, "traffic": None}
-    elif kind == "decode":
+        roof["kernel"] = hr["kernel"]
+    elif kind in ("decode", "cache", "step", "transform") or (kind == "output" and nq <= 32):
         value, unit, metric = hr["GB/s"], "GB/s", "decode-attn HBM GB/s at 32K KV"
-        ach = hr["algorithmic_bytes"] / stream_s / 1e9
-        roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": ach / HBM_PEAK_GBS, "traffic": traffic_bytes(head)}
+        roof = roofline(head, hr)
     else:
         value, unit, metric = hr["TFLOP/s"], "TFLOP/s", "prefill attn TFLOP/s"
-        ach = hr["algorithmic_flops"] / stream_s / 1e12
-        roof = {"bound": "mfma", "achieved": ach, "peak": FP32_MFMA_PEAK_TFS,
-                "unit": "TFLOP/s", "frac": ach / FP32_MFMA_PEAK_TFS,
-                "traffic": traffic_bytes(head)}
-    roof["kernel"] = hr["kernel"]
+        roof = roofline(head, hr)
+    # the metric's prefill half: each 4K prefill with its own roofline, and the
+    # CPU baseline of the global one on a sample of its rows
+    prefill = {}
+    for name in PREFILL:
+        if name not in results:
+            continue
+        r = results[name]
+        block = {"metric": "prefill attn TFLOP/s (% fp32 MFMA peak) at 4K tokens",
+                 "value": r["TFLOP/s"], "unit": "TFLOP/s", "ms_per_step": r["ms"],
+                 "steps": r["steps"], "roofline": roofline(name, r), "cpu_baseline": None}
+        if not args.no_cpu and name in hosts:
+            cb = cpu_baseline_prefill(name, hosts[name], threads, args.cpu_budget)
+            cb["affinity_cores"] = affinity
+            cb["cpu"] = cpu_model()
+            block["cpu_baseline"] = cb
+        prefill[name] = block
     line = {
         "metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": hr["steps"],
         "warmup": args.warmup, "ms_per_step": hr["ms"], "higher_is_better": True,
@@ -611,6 +713,7 @@ def main():
                    "q_prescale": "1/sqrt(head_dim)", "kernel": hr["kernel"]},
         "roofline": roof,
         "cpu_baseline": cpu,
+        "prefill": prefill or None,
         "configs": {n: {k: (round(x, 5) if isinstance(x, float) else x) for k, x in r.items()}
                     for n, r in results.items()},
     }

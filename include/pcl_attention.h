@@ -161,10 +161,11 @@ void *pcl_context_stream(pcl_context *ctx);
  * that fails validation (including the size limits: at most 2^30 keys, and
  * nq * (qheads / kvheads) * (kh_end - kh_first) at most 2^22; larger calls
  * are split by query range or KV-head range, which leaves every result bit
- * unchanged), or PCL_NON_FINITE_VALUE for a launch failure. Data
- * errors (non-finite allowed score or output) are recorded in the context's
- * device error flag. Grows the context's workspace when needed (a device
- * allocation); pcl_context_reserve avoids that inside timed regions. */
+ * unchanged), PCL_RESOURCE_LIMIT when the workspace cannot be allocated,
+ * or PCL_NON_FINITE_VALUE for a launch failure. Data errors (non-finite
+ * allowed score or output) are recorded in the context's device error flag.
+ * Grows the context's workspace when needed (a device allocation);
+ * pcl_context_reserve avoids that inside timed regions. */
 int pcl_attention_launch(pcl_context *ctx, const pcl_attention_desc *desc);
 /* Workspace bytes a descriptor needs with the kernel it would run. */
 size_t pcl_attention_workspace_bytes(const pcl_attention_desc *desc);
@@ -289,10 +290,15 @@ int pcl_head_transform_create(pcl_context *ctx, int64_t qheads, int64_t kvheads,
                               pcl_head_transform **out);
 void pcl_head_transform_destroy(pcl_head_transform *transform);
 /* HeadTransform::prepare (attention.rs:102-156) for n tokens. The rotation
- * table is built on the host (the C library's powf; glibc 2.28's sincosf, as
- * the reference's libm::sincosf, src/libm.rs:350) for positions up to the
- * largest seen so far and kept on the device; PCL_NON_FINITE_VALUE
- * for a non-finite angle, PCL_RESOURCE_LIMIT beyond 2^24 positions. */
+ * table is built on the host (the C library's powf; the C library's double
+ * sin and cos of each f32 angle, rounded once to f32: within an f32 ulp of
+ * the reference's libm::sincosf, src/libm.rs:350, and equal to it for all
+ * but about 0.1 % of angles) for positions up to the largest seen so far and
+ * kept on the device; PCL_NON_FINITE_VALUE for a non-finite angle,
+ * PCL_RESOURCE_LIMIT beyond 2^24 positions. A rotated Q or K value y_j
+ * (pair j, j + dim/2) is therefore within 2^-20 * (|y_j| + |y_{j+dim/2}|)
+ * of the reference's, and almost always equal to it; V rows are bit for
+ * bit. */
 int pcl_head_transform_prepare(pcl_head_transform *transform, const float *raw_q,
                                const float *raw_k, const float *raw_v, int64_t n,
                                int64_t position, float *q_out, float *k_out, float *v_out);

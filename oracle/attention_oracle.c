@@ -69,6 +69,99 @@ bool oracle_ref_attention_heads(const float *query, const float *keys, const flo
     return true;
 }
 
+/* oracle_ref_attention_heads restructured for speed where that cannot
+ * change a bit, for checking full-size outputs (the CPU baseline times the
+ * straightforward form above): masked keys, whose probability is exactly 0,
+ * are left out of the sums (adding exp(-inf) = 0, or 0 * v for a finite v,
+ * leaves an f64 sum unchanged); four keys' score sums run interleaved, each
+ * still over ascending d; and the P.V sums run key-outer over a row of f64
+ * accumulators, each output's sum still over ascending t. Equal to the
+ * straightforward form bit for bit whenever the value rows of masked keys
+ * are finite (the reference's 0 * inf makes its output NaN there). */
+bool oracle_ref_attention_heads_checker(const float *query, const float *keys,
+                                        const float *values, size_t qheads, size_t kvheads,
+                                        size_t dim, size_t nkeys, const uint8_t *allowed,
+                                        float *scratch, float *out, size_t h_first,
+                                        size_t h_end)
+{
+    if (h_first > h_end || h_end > qheads)
+        return false;
+    if (kvheads == 0 || qheads < kvheads)
+        return false;
+    const size_t group = qheads / kvheads;
+    const size_t stride = kvheads * dim;
+    double *acc = (double *)malloc(dim * sizeof(double));
+    size_t *live = (size_t *)malloc((nkeys ? nkeys : 1) * sizeof(size_t));
+    if (!acc || !live) {
+        free(acc);
+        free(live);
+        return false;
+    }
+    bool ok = true;
+    for (size_t h = h_first; h < h_end && ok; ++h) {
+        const size_t kh = h / group;
+        const float *q = query + h * dim;
+        size_t n = 0;
+        for (size_t t = 0; t < nkeys; ++t)
+            if (!allowed || allowed[t] != 0)
+                live[n++] = t;
+        float max = -INFINITY;
+        size_t i = 0;
+        for (; i + 4 <= n && ok; i += 4) {
+            const float *k0 = keys + live[i] * stride + kh * dim;
+            const float *k1 = keys + live[i + 1] * stride + kh * dim;
+            const float *k2 = keys + live[i + 2] * stride + kh * dim;
+            const float *k3 = keys + live[i + 3] * stride + kh * dim;
+            double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+            for (size_t d = 0; d < dim; ++d) {
+                const double qd = (double)q[d];
+                s0 += qd * (double)k0[d];
+                s1 += qd * (double)k1[d];
+                s2 += qd * (double)k2[d];
+                s3 += qd * (double)k3[d];
+            }
+            const double s[4] = {s0, s1, s2, s3};
+            for (int j = 0; j < 4; ++j) {
+                const float f = (float)s[j];
+                scratch[i + j] = f;
+                if (!isfinite(f))
+                    ok = false;
+                if (f > max)
+                    max = f;
+            }
+        }
+        for (; i < n && ok; ++i) {
+            const float *k = keys + live[i] * stride + kh * dim;
+            double score = 0.0;
+            for (size_t d = 0; d < dim; ++d)
+                score += (double)q[d] * (double)k[d];
+            scratch[i] = (float)score;
+            if (!isfinite(scratch[i]))
+                ok = false;
+            if (scratch[i] > max)
+                max = scratch[i];
+        }
+        if (!ok)
+            break;
+        double sum = 0.0;
+        for (i = 0; i < n; ++i)
+            sum += exp((double)scratch[i] - (double)max);
+        for (size_t d = 0; d < dim; ++d)
+            acc[d] = 0.0;
+        for (i = 0; i < n; ++i) {
+            const double p = (double)(float)(exp((double)scratch[i] - (double)max) / sum);
+            const float *v = values + live[i] * stride + kh * dim;
+            for (size_t d = 0; d < dim; ++d)
+                acc[d] += p * (double)v[d];
+        }
+        for (size_t d = 0; d < dim; ++d)
+            out[(h - h_first) * dim + d] = (float)acc[d];
+    }
+    free(live);
+    free(acc);
+    return ok;
+}
+
 /* softmax (src/kernels/portable/attention.rs:15-43). */
 static bool oracle_softmax_f32(float *scores, size_t n, const uint8_t *allowed)
 {
@@ -637,6 +730,11 @@ static uint32_t digest_bits(float r, int inputs_nan)
  * binary32 pattern for sincosf; for powf, xorshift64 pairs from seed
  * 0x2545f4914f6cdd1d, random patterns at even steps and x in (0, 1e6],
  * y in [-2, 2] at odd steps. */
+void oracle_sincosf(float x, float *s, float *c)
+{
+    glibc228_sincosf(x, s, c);
+}
+
 uint64_t oracle_libm_digest(int which)
 {
     uint64_t h = 0xcbf29ce484222325ULL;
@@ -706,6 +804,7 @@ struct job {
     size_t nq, qheads, kvheads, dim, nkeys;
     int causal;
     size_t first_key, first_query, window;
+    size_t query_step; /* query i is at position first_query + i * query_step */
     float *out;
     /* head-split decode: items (query, head range) */
     size_t per;
@@ -730,8 +829,8 @@ static void *oracle_worker(void *arg)
             const size_t b = a + j->per < j->qheads ? a + j->per : j->qheads;
             const uint8_t *m = NULL;
             if (j->causal) {
-                oracle_encoder_mask(j->first_key, j->nkeys, j->first_query + i, j->window,
-                                    j->window != 0, mask);
+                oracle_encoder_mask(j->first_key, j->nkeys, j->first_query + i * j->query_step,
+                                    j->window, j->window != 0, mask);
                 m = mask;
             }
             j->ok = j->kernel(j->query + i * width, j->keys, j->values, j->qheads, j->kvheads,
@@ -744,8 +843,8 @@ static void *oracle_worker(void *arg)
         for (size_t i = j->first; i < j->end && j->ok; ++i) {
             const uint8_t *m = NULL;
             if (j->causal) {
-                oracle_encoder_mask(j->first_key, j->nkeys, j->first_query + i, j->window,
-                                    j->window != 0, mask);
+                oracle_encoder_mask(j->first_key, j->nkeys, j->first_query + i * j->query_step,
+                                    j->window, j->window != 0, mask);
                 m = mask;
             }
             j->ok = j->kernel(j->query + i * width, j->keys, j->values, j->qheads, j->kvheads,
@@ -757,17 +856,30 @@ static void *oracle_worker(void *arg)
     return NULL;
 }
 
-bool oracle_threaded_attention(int binary32, int threads, const float *query, size_t nq,
+bool oracle_threaded_attention(int variant, int threads, const float *query, size_t nq,
                                const float *keys, const float *values, size_t qheads,
                                size_t kvheads, size_t dim, size_t nkeys, int causal,
                                size_t first_key, size_t first_query, size_t window,
                                float *out)
 {
+    return oracle_threaded_attention_sample(variant, threads, query, nq, 1, keys, values, qheads,
+                                            kvheads, dim, nkeys, causal, first_key, first_query,
+                                            window, out);
+}
+
+bool oracle_threaded_attention_sample(int variant, int threads, const float *query, size_t nq,
+                                      size_t query_step, const float *keys, const float *values,
+                                      size_t qheads, size_t kvheads, size_t dim, size_t nkeys,
+                                      int causal, size_t first_key, size_t first_query,
+                                      size_t window, float *out)
+{
     if (threads < 1)
         threads = 1;
     struct job base;
     memset(&base, 0, sizeof base);
-    base.kernel = binary32 ? oracle_pa_attention_f32_heads : oracle_ref_attention_heads;
+    base.kernel = variant == 1   ? oracle_pa_attention_f32_heads
+                  : variant == 2 ? oracle_ref_attention_heads_checker
+                                 : oracle_ref_attention_heads;
     base.query = query;
     base.keys = keys;
     base.values = values;
@@ -779,6 +891,7 @@ bool oracle_threaded_attention(int binary32, int threads, const float *query, si
     base.causal = causal;
     base.first_key = first_key;
     base.first_query = first_query;
+    base.query_step = query_step ? query_step : 1;
     base.window = window;
     base.out = out;
     size_t length;

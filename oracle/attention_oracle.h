@@ -35,6 +35,16 @@ bool oracle_ref_attention_heads(const float *query, const float *keys, const flo
                                 const uint8_t *allowed, float *scratch, float *out,
                                 size_t h_first, size_t h_end);
 
+/* a1 restructured for speed without changing a bit (masked keys left out of
+ * the sums, interleaved score sums, key-outer P.V), for checking full-size
+ * outputs; equal to oracle_ref_attention_heads whenever masked keys' value
+ * rows are finite. */
+bool oracle_ref_attention_heads_checker(const float *query, const float *keys,
+                                        const float *values, size_t qheads, size_t kvheads,
+                                        size_t dim, size_t nkeys, const uint8_t *allowed,
+                                        float *scratch, float *out, size_t h_first,
+                                        size_t h_end);
+
 /* a3/a4 — binary32 attention: pa_attention_f32_heads + softmax
  * (src/kernels/portable/attention.rs:14-112). 16 FMA score lanes reduced as a
  * fixed tree, f32 softmax (glibc 2.28's POWER8 expf, the reference's
@@ -136,6 +146,9 @@ bool oracle_rope(const float *x, size_t heads, size_t dim, size_t position, floa
  * generates are counted with the positive default-NaN bits of the
  * reference's platform. */
 uint64_t oracle_libm_digest(int which);
+/* The rotation's sine and cosine of one angle: glibc 2.28's sincosf as
+ * oracle_rope uses it (the reference's libm::sincosf, src/libm.rs:350-497). */
+void oracle_sincosf(float x, float *s, float *c);
 
 /* Test input generator, not on the attention path: the reference tests'
  * xorshift64 stream (src/kernels/quantized/int8/tests.rs:15-33). Writes
@@ -149,7 +162,8 @@ void oracle_xorshift_units(uint64_t *state, float scale, size_t n, float *out);
 void oracle_matvec(const float *matrix, const float *x, size_t rows, size_t cols, float *out);
 void oracle_add(const float *a, const float *b, size_t n, float *out);
 
-/* CPU baseline: the exact (a1) or binary32 (a3) path threaded as the engine
+/* CPU baseline: the exact (a1, variant 0) or binary32 (a3, variant 1) path,
+ * or the exact path's checker form (variant 2), threaded as the engine
  * threads it (src/engine/attention.rs:755-836): one query's heads split
  * into ceil(qheads/split) ranges with split = clamp(workers/queries, 1,
  * qheads) when queries < workers, else contiguous query ranges
@@ -157,11 +171,20 @@ void oracle_add(const float *a, const float *b, size_t n, float *out);
  * Masks come from encoder_mask(first_key, nkeys, first_query+i, window),
  * or none when causal == 0 (decoder mode). Queries [nq][qheads*dim];
  * out [nq][qheads*dim]. Returns false on a kernel error. */
-bool oracle_threaded_attention(int binary32, int threads, const float *query, size_t nq,
+bool oracle_threaded_attention(int variant, int threads, const float *query, size_t nq,
                                const float *keys, const float *values, size_t qheads,
                                size_t kvheads, size_t dim, size_t nkeys, int causal,
                                size_t first_key, size_t first_query, size_t window,
                                float *out);
+/* The same over a sample of a prompt's queries: query i of the nq given
+ * rows is at position first_query + i * query_step (every query_step-th
+ * row of the prompt), so a bounded share of a long prefill is timed with
+ * the masks, threading and per-row work of the whole. */
+bool oracle_threaded_attention_sample(int variant, int threads, const float *query, size_t nq,
+                                      size_t query_step, const float *keys, const float *values,
+                                      size_t qheads, size_t kvheads, size_t dim, size_t nkeys,
+                                      int causal, size_t first_key, size_t first_query,
+                                      size_t window, float *out);
 
 #ifdef __cplusplus
 }

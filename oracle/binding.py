@@ -46,6 +46,13 @@ def load():
     lib.oracle_xorshift_units.restype = None
     lib.oracle_xorshift_units.argtypes = [ctypes.POINTER(ctypes.c_uint64), ctypes.c_float, sz,
                                           fp]
+    lib.oracle_ref_attention_heads_checker.restype = ctypes.c_bool
+    lib.oracle_ref_attention_heads_checker.argtypes = [fp, fp, fp, sz, sz, sz, sz, u8p, fp, fp,
+                                                       sz, sz]
+    lib.oracle_threaded_attention_sample.restype = ctypes.c_bool
+    lib.oracle_threaded_attention_sample.argtypes = [ctypes.c_int, ctypes.c_int, fp, sz, sz, fp,
+                                                     fp, sz, sz, sz, sz, ctypes.c_int, sz, sz, sz,
+                                                     fp]
     lib.oracle_threaded_attention.restype = ctypes.c_bool
     lib.oracle_threaded_attention.argtypes = [ctypes.c_int, ctypes.c_int, fp, sz, fp, fp, sz, sz,
                                               sz, sz, ctypes.c_int, sz, sz, sz, fp]
@@ -72,15 +79,17 @@ def _mask(x):
 
 
 def heads(query, keys, values, qheads, kvheads, dim, nkeys, allowed=None, h_first=0,
-          h_end=None, binary32=False):
-    """p9_ref_attention_heads (exact) or pa_attention_f32_heads (binary32):
-    returns (ok, out[(h_end-h_first)*dim])."""
+          h_end=None, binary32=False, checker=False):
+    """p9_ref_attention_heads (exact), its bit-identical checker form
+    (checker=True) or pa_attention_f32_heads (binary32): returns
+    (ok, out[(h_end-h_first)*dim])."""
     lib = load()
     h_end = qheads if h_end is None else h_end
     q, k, v, m = _f32(query), _f32(keys), _f32(values), _mask(allowed)
     scratch = np.zeros(max(nkeys, 1), np.float32)
     out = np.zeros(max((h_end - h_first) * dim, 1), np.float32)
-    fn = lib.oracle_pa_attention_f32_heads if binary32 else lib.oracle_ref_attention_heads
+    fn = (lib.oracle_pa_attention_f32_heads if binary32 else
+          lib.oracle_ref_attention_heads_checker if checker else lib.oracle_ref_attention_heads)
     ok = fn(_f(q), _f(k), _f(v), qheads, kvheads, dim, nkeys, _u(m), _f(scratch), _f(out),
             h_first, h_end)
     return bool(ok), out[:max(h_end - h_first, 0) * dim]
@@ -130,12 +139,17 @@ def retained_count(count, window=None):
 
 
 def threaded(query, nq, keys, values, qheads, kvheads, dim, nkeys, causal, first_key=0,
-             first_query=0, window=0, threads=1, binary32=False):
-    """The engine-threaded CPU path over nq queries: (ok, out[nq*qheads*dim])."""
+             first_query=0, window=0, threads=1, binary32=False, checker=False, query_step=1):
+    """The engine-threaded CPU path over nq queries: (ok, out[nq*qheads*dim]).
+    checker=True runs the exact path's bit-identical fast form (finite value
+    rows), for checking full-size outputs; the default is the form timed as
+    the CPU baseline."""
     lib = load()
     q, k, v = _f32(query), _f32(keys), _f32(values)
     out = np.zeros(nq * qheads * dim, np.float32)
-    ok = lib.oracle_threaded_attention(int(binary32), threads, _f(q), nq, _f(k), _f(v), qheads,
+    variant = 1 if binary32 else (2 if checker else 0)
+    ok = lib.oracle_threaded_attention_sample(variant, threads, _f(q), nq, query_step, _f(k),
+                                              _f(v), qheads,
                                        kvheads, dim, nkeys, int(causal), first_key, first_query,
                                        window, _f(out))
     return bool(ok), out

@@ -11,6 +11,7 @@
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 
 static int failures;
 
@@ -78,10 +79,50 @@ static void cache_window_and_limits(void)
     CHECK(oracle_cache_init(&c, 1, 2, 64, 3, 1, 15) == ORACLE_RESOURCE_LIMIT);
 }
 
+/* The checker form and the sampled threaded path under the sanitizers:
+ * both must give the straightforward form's bits. */
+static void checker_and_sample(void)
+{
+    enum { QH = 4, KVH = 2, DIM = 48, N = 37, STEP = 5 };
+    static float q[N * QH * DIM], k[N * KVH * DIM], v[N * KVH * DIM];
+    static float full[N * QH * DIM], part[N * QH * DIM], a[QH * DIM], b[QH * DIM];
+    static float scratch[N];
+    static uint8_t mask[N];
+    uint64_t r = 0x9e3779b97f4a7c15ULL;
+    float *all[3] = {q, k, v};
+    const size_t len[3] = {N * QH * DIM, N * KVH * DIM, N * KVH * DIM};
+    for (int x = 0; x < 3; ++x)
+        for (size_t i = 0; i < len[x]; ++i) {
+            r = r * 6364136223846793005ULL + 1442695040888963407ULL;
+            all[x][i] = (float)((double)(r >> 40) / (double)(1 << 24) - 0.5);
+        }
+    for (int t = 0; t < N; ++t)
+        mask[t] = (uint8_t)(t % 3 != 1);
+    for (int h0 = 0; h0 < QH; ++h0) {
+        CHECK(oracle_ref_attention_heads(q, k, v, QH, KVH, DIM, N, mask, scratch, a, h0, QH));
+        CHECK(oracle_ref_attention_heads_checker(q, k, v, QH, KVH, DIM, N, mask, scratch, b, h0,
+                                                 QH));
+        CHECK(memcmp(a, b, (size_t)(QH - h0) * DIM * sizeof(float)) == 0);
+    }
+    CHECK(oracle_threaded_attention(0, 3, q, N, k, v, QH, KVH, DIM, N, 1, 0, 0, 11, full));
+    float rows[((N + STEP - 1) / STEP) * QH * DIM];
+    size_t nr = 0;
+    for (int i = 0; i < N; i += STEP, ++nr)
+        memcpy(rows + nr * QH * DIM, q + (size_t)i * QH * DIM, QH * DIM * sizeof(float));
+    for (int variant = 0; variant < 3; variant += 2) {
+        CHECK(oracle_threaded_attention_sample(variant, 2, rows, nr, STEP, k, v, QH, KVH, DIM, N,
+                                               1, 0, 0, 11, part));
+        for (size_t i = 0; i < nr; ++i)
+            CHECK(memcmp(part + i * QH * DIM, full + i * STEP * QH * DIM,
+                         QH * DIM * sizeof(float)) == 0);
+    }
+}
+
 int main(void)
 {
     grouped_attention();
     cache_window_and_limits();
+    checker_and_sample();
     if (failures) {
         fprintf(stderr, "%d failures\n", failures);
         return 1;

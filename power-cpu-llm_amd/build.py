@@ -11,6 +11,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libpcl_attention.so")
+OBJ_DIR = os.path.join(HERE, "_build")
 SOURCES = ["csrc/split_kv.hip", "csrc/pipe_kv.hip", "csrc/two_pass.hip", "csrc/tiled.hip",
            "csrc/api.hip", "csrc/kv_cache.hip", "csrc/head_transform.hip",
            "csrc/output_block.hip"]
@@ -33,9 +34,7 @@ FLAGS = [
 ]
 
 
-def build(verbose=False):
-    """Compile every source into LIB; raises CalledProcessError on failure."""
-    cmd = [HIPCC] + FLAGS + ["-o", LIB] + [os.path.join(HERE, s) for s in SOURCES]
+def _run(cmd, verbose):
     res = subprocess.run(cmd, cwd=HERE, capture_output=True, text=True)
     noise = "packed-fp32-ops' is not a recognized feature"
     err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
@@ -44,6 +43,22 @@ def build(verbose=False):
         raise subprocess.CalledProcessError(res.returncode, cmd, res.stdout, res.stderr)
     if verbose and err.strip():
         sys.stderr.write(err + "\n")
+
+
+def build(verbose=False):
+    """Compile every source (one hipcc process per file, in parallel) and
+    link them into LIB; raises CalledProcessError on failure."""
+    from concurrent.futures import ThreadPoolExecutor
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    compile_flags = [f for f in FLAGS if f != "-shared"]
+    objs = [os.path.join(OBJ_DIR, os.path.basename(s) + ".o") for s in SOURCES]
+    cmds = [[HIPCC] + compile_flags + ["-c", "-o", o, os.path.join(HERE, s)]
+            for s, o in zip(SOURCES, objs)]
+    jobs = max(1, min(len(cmds), os.cpu_count() or 1, 16))
+    with ThreadPoolExecutor(jobs) as pool:
+        for f in [pool.submit(_run, c, verbose) for c in cmds]:
+            f.result()
+    _run([HIPCC] + FLAGS + ["-o", LIB] + objs, verbose)
     return LIB
 
 

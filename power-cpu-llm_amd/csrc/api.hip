@@ -229,7 +229,7 @@ int ensure_workspace(pcl_context *ctx, size_t bytes)
     const hipError_t e = hipMalloc(&ctx->ws, bytes);
     if (e != hipSuccess) {
         report("workspace allocation", e);
-        return PCL_NON_FINITE_VALUE;
+        return PCL_RESOURCE_LIMIT;
     }
     ctx->ws_bytes = bytes;
     return PCL_OK;

@@ -9,9 +9,10 @@
 //   y_j = f32(f64(x_j) * inv), times scale_j in f32 for Q and K.
 // Q and K then rotate pairs (j, j + dim/2) (p9_ref_rope, reference.rs:277-318):
 //   y_j' = y_j*c - y_{j+h}*s,  y_{j+h}' = y_{j+h}*c + y_j*s   (f32, unfused),
-// with (s, c) = sincosf(f32(position) * f32(1 / powf(base, 2j/dim)) / factor_j)
-// from a host-built table (the C library's powf; glibc 2.28's sincosf, which
-// the reference's libm reproduces, from host_sincosf.hpp). V is normalised
+// with (s, c) = sin, cos of the f32 angle position * f32(1 / powf(base,
+// 2j/dim)) / factor_j from a host-built table (the C library's powf; the C
+// library's double sin and cos of the angle rounded once to f32, within an
+// f32 ulp of the engine's sincosf, rotation.hpp). V is normalised
 // without scale and not rotated; a global layer without a V projection uses
 // the raw K as V (attention.rs:121-129).
 //
@@ -23,8 +24,8 @@
 // step's heads run on many CUs at once.
 #include "attention_device.hpp"
 #include "context.hpp"
-#include "host_sincosf.hpp"
 #include "pcl_attention.h"
+#include "rotation.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -237,8 +238,8 @@ bool finite_all(const float *x, int64_t n)
 
 // (sin, cos) of every pair of positions [from, to): p9_ref_rope's
 // frequencies and angles in f32 (reference.rs:294-305), the C library's
-// powf (equal to the reference's libm powf on its digest inputs) and glibc
-// 2.28's sincosf. False on a non-finite angle.
+// powf (equal to the reference's libm powf on its digest inputs) and the
+// table's sine and cosine of rotation.hpp. False on a non-finite angle.
 bool rope_rows(const pcl_head_transform *t, int64_t from, int64_t to, float *out)
 {
     const int64_t half = t->dim / 2;
@@ -255,7 +256,7 @@ bool rope_rows(const pcl_head_transform *t, int64_t from, int64_t to, float *out
             if (!std::isfinite(angle))
                 return false;
             float s, c;
-            pcl::sincosf_glibc228(angle, &s, &c);
+            pcl::rotation_sincos(angle, &s, &c);
             out[2 * ((p - from) * half + i)] = s;
             out[2 * ((p - from) * half + i) + 1] = c;
         }

@@ -154,6 +154,11 @@ void tiled_kernel(Params p, int split, int z0)
     float *acc2 = p.ws_o ? p.ws_o + ((int64_t)kvl * p.nrows_pad + row) * p.dk : nullptr;
 
     // HBM -> LDS copy of tile t into stage `buf` (K swizzled, V plain).
+    // Below the padded head dim, a slot past the head's last dim copies the
+    // head's first four dims instead, as the decode kernels load them: the
+    // copy never leaves the head's row (the last head of the last key ends
+    // the caller's buffer), Q is zero on those dims and their outputs are
+    // dropped.
     auto load_tile = [&](int t, int buf) {
         float *ks = lds + buf * LD::stage;
         float *vs = ks + LD::tileFloats;
@@ -167,8 +172,10 @@ void tiled_kernel(Params p, int split, int z0)
             const int64_t kt = (int64_t)t * kTile + key;
             const int64_t kc = kt < klast ? kt : klast;
             const int64_t off = (int64_t)kh * p.dim;
-            dma16(key_row(p, kc) + off + 4 * (pos ^ (key & 7)), ks + 256 * j);
-            dma16(value_row(p, kc) + off + 4 * pos, vs + 256 * j);
+            const int kd = 4 * (pos ^ (key & 7));
+            const int vd = 4 * pos;
+            dma16(key_row(p, kc) + off + (kd < p.dim ? kd : 0), ks + 256 * j);
+            dma16(value_row(p, kc) + off + (vd < p.dim ? vd : 0), vs + 256 * j);
         }
     };
 

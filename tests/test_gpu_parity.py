@@ -50,8 +50,9 @@ def assert_parity(got, want, dim, tol=TOL):
     assert np.all(np.isfinite(got))
     err = float(np.max(np.abs(got - want))) if got.size else 0.0
     assert err <= tol, "max abs error %.3g" % err
-    ok, margin = row_argmax_agree(got, want, dim, tol)
-    assert ok, "argmax differs with top-1/top-2 margin %.3g" % margin
+    ok, mismatches = row_argmax_agree(got, want, dim)
+    assert ok, "argmax differs in %d rows (row, top-1 minus top-2 margin): %s" % (
+        len(mismatches), mismatches[:20])
     return err
 
 
@@ -521,6 +522,45 @@ def test_device_error_flags(torch, ctx):
         assert err == 0
 
 
+@pytest.mark.parametrize("dim", [48, 80, 144, 208])
+def test_padded_head_dims_read_only_the_callers_rows(torch, ctx, oracle, dim):
+    """Head dims below the kernels' padded size (64, 128, 256): K and V end
+    where a NaN-filled tail of their allocation begins, so any read past the
+    last key row's last head would turn a score or an output non-finite.
+    Every kernel stays finite, error-free and bitwise equal."""
+    qheads, kvh, nq, nkeys = 8, 2, 160, 300
+    g = np.random.default_rng(dim)
+    q = prescale(g.standard_normal((nq, qheads * dim), dtype=np.float32), dim)
+    k = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+    v = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+    n = nkeys * kvh * dim
+    kbuf = torch.full((n + 4096,), float("nan"), device="cuda:0")
+    vbuf = torch.full((n + 4096,), float("nan"), device="cuda:0")
+    kbuf[:n] = torch.from_numpy(k.reshape(-1)).to("cuda:0")
+    vbuf[:n] = torch.from_numpy(v.reshape(-1)).to("cuda:0")
+    tq = torch.from_numpy(q).to("cuda:0")
+    outs = {}
+    for kernel in (2, 3, 1, 4, 5):
+        out = torch.full((nq, qheads * dim), float("nan"), device="cuda:0")
+        d = ctx.desc(q=tq.data_ptr(), q_stride=qheads * dim, nq=nq, k0=kbuf.data_ptr(),
+                     v0=vbuf.data_ptr(), n0=nkeys, qheads=qheads, kvheads=kvh, dim=dim,
+                     kh_first=0, kh_end=kvh, causal=1, window=0, first_key=0,
+                     first_query=nkeys - nq, out=out.data_ptr(), o_stride=qheads * dim,
+                     kernel=kernel)
+        ctx.reserve(ctx.workspace_bytes(d))
+        ctx.launch(d)
+        assert ctx.sync() == 0, kernel
+        outs[kernel] = out.cpu().numpy()
+        assert np.all(np.isfinite(outs[kernel])), kernel
+    for kernel in (3, 1, 4, 5):
+        assert np.array_equal(bits(outs[2]), bits(outs[kernel])), kernel
+    for i in (0, nq - 1):
+        m = oracle.encoder_mask(0, nkeys, nkeys - nq + i, None)
+        ok, want = oracle.heads(q[i], k, v, qheads, kvh, dim, nkeys, m)
+        assert ok
+        assert_parity(outs[2][i], want, dim)
+
+
 # ---- BASELINE.json configs ---------------------------------------------------
 
 def gpu_normals(torch, seed, shape):
@@ -575,13 +615,17 @@ def test_config3_global_decode_131072_d512(torch, ctx, oracle):
 
 @pytest.mark.parametrize("window", [1024, 0], ids=["window1024", "global"])
 def test_config4_prefill_4096(torch, ctx, oracle, window):
+    """Both 4K prefills (sliding window 1024 and global) compared elementwise
+    with the exact oracle: every one of the 4096 x 16 rows within 1e-4, the
+    same argmax in every row. The oracle runs its bit-identical checker form
+    on the host's threads."""
     qheads, kvh, dim, n = 16, 8, 256, 4096
     seed = 0x5EED0004
     q = gpu_normals(torch, seed, (n, qheads, dim)) * float(np.float32(1.0 / 16.0))
     k = gpu_normals(torch, seed + 1, (n, kvh, dim))
     v = gpu_normals(torch, seed + 2, (n, kvh, dim))
     outs = {}
-    for kernel in (2, 1):
+    for kernel in (0, 2, 1):
         out = torch.empty((n, qheads, dim), device="cuda:0")
         d = ctx.desc(q=q.data_ptr(), q_stride=qheads * dim, nq=n, k0=k.data_ptr(),
                      v0=v.data_ptr(), n0=n, qheads=qheads, kvheads=kvh, dim=dim, kh_first=0,
@@ -591,26 +635,30 @@ def test_config4_prefill_4096(torch, ctx, oracle, window):
         ctx.launch(d)
         assert ctx.sync() == 0
         outs[kernel] = out.cpu().numpy()
-    # the whole 4096 x 16 x 256 output: both kernels agree bitwise
+    # the whole output: the automatic choice, tiled and split-KV agree bitwise
+    assert np.array_equal(bits(outs[0]), bits(outs[2]))
     assert np.array_equal(bits(outs[1]), bits(outs[2]))
-    qn, kn, vn = (x.cpu().numpy() for x in (q, k, v))
-    rows = sorted(set(list(range(4)) + list(range(1020, 1030)) + list(range(4090, 4096)) +
-                  list(np.random.default_rng(4).choice(n, 24, replace=False))))
-    for i in rows:
-        m = oracle.encoder_mask(0, n, i, window or None)
-        ok, want = oracle.heads(qn[i].reshape(-1), kn.reshape(-1), vn.reshape(-1), qheads, kvh,
-                                dim, n, m)
-        assert ok
-        assert_parity(outs[2][i], want, dim)
+    qn, kn, vn = (x.cpu().numpy().reshape(-1) for x in (q, k, v))
+    ok, want = oracle.threaded(qn, n, kn, vn, qheads, kvh, dim, n, True, 0, 0, window,
+                               threads=THREADS, checker=True)
+    assert ok
+    assert_parity(outs[0], want, dim)
 
 
-def test_config5_canvas_48_denoising_steps(torch, ctx, oracle):
+CANVAS_STEP_GROUPS = [range(0, 12), range(12, 24), range(24, 36), range(36, 48)]
+
+
+@pytest.mark.parametrize("steps", CANVAS_STEP_GROUPS, ids=lambda r: "steps%d-%d" % (r[0], r[-1]))
+def test_config5_canvas_48_denoising_steps(torch, ctx, oracle, steps):
+    """The DiffusionGemma canvas: 256 canvas rows attend non-causally to a
+    fixed 2048-token prefix and to the step's own canvas K/V (a second
+    segment). Every row of every step is compared elementwise with the exact
+    oracle (1e-4, same argmax); the 48 steps run as four groups of 12."""
     qheads, kvh, dim, prefix, canvas = 16, 8, 256, 2048, 256
     kp = gpu_normals(torch, 0x5EED0005, (prefix, kvh, dim))
     vp = gpu_normals(torch, 0x5EED0105, (prefix, kvh, dim))
     kpn, vpn = kp.cpu().numpy(), vp.cpu().numpy()
-    rng = np.random.default_rng(48)
-    for step in range(48):
+    for step in steps:
         seed = 0x5EED0500 + step
         q = gpu_normals(torch, seed, (canvas, qheads, dim)) * float(np.float32(1.0 / 16.0))
         kc = gpu_normals(torch, seed + 1000, (canvas, kvh, dim))
@@ -626,9 +674,8 @@ def test_config5_canvas_48_denoising_steps(torch, ctx, oracle):
         got = out.cpu().numpy()
         kn = np.concatenate([kpn, kc.cpu().numpy()]).reshape(-1)
         vn = np.concatenate([vpn, vc.cpu().numpy()]).reshape(-1)
-        qn = q.cpu().numpy()
-        for i in rng.choice(canvas, 3, replace=False):
-            ok, want = oracle.heads(qn[i].reshape(-1), kn, vn, qheads, kvh, dim,
-                                    prefix + canvas)
-            assert ok
-            assert_parity(got[i], want, dim)
+        qn = q.cpu().numpy().reshape(-1)
+        ok, want = oracle.threaded(qn, canvas, kn, vn, qheads, kvh, dim, prefix + canvas, False,
+                                   threads=THREADS, checker=True)
+        assert ok, step
+        assert_parity(got, want, dim)

@@ -6,6 +6,7 @@ invariants chosen so that a wrong head mapping, stride, sign, mask or
 rounding point fails at least one of them.
 """
 import math
+import os
 
 import numpy as np
 import pytest
@@ -241,6 +242,72 @@ def test_head_ranges_and_threads_do_not_change_results(oracle):
         assert ok and np.array_equal(one, outs[0][:qheads * dim])
 
 
+def bits32(x):
+    return np.ascontiguousarray(x, np.float32).view(np.uint32)
+
+
+def test_checker_form_equals_the_exact_oracle_bit_for_bit(oracle):
+    # the fast form used to check full-size GPU outputs gives the exact
+    # oracle's bits: random geometries and scales, sparse and dense masks,
+    # head ranges, key counts that are not multiples of its four-key step,
+    # non-finite scores rejected the same way
+    g = np.random.default_rng(0xC4EC)
+    for case in range(60):
+        kvh = int(g.choice([1, 2, 3, 8]))
+        group = int(g.choice([1, 2, 4]))
+        qheads = kvh * group
+        dim = int(g.choice([16, 48, 64, 256, 512]))
+        nkeys = int(g.integers(1, 90))
+        scale = float(g.choice([0.05, 1.0, 6.0]))
+        q = (g.standard_normal(qheads * dim) * scale).astype(np.float32)
+        k = g.standard_normal(nkeys * kvh * dim).astype(np.float32)
+        v = g.standard_normal(nkeys * kvh * dim).astype(np.float32)
+        density = float(g.choice([0.05, 0.5, 1.0]))
+        mask = g.random(nkeys) < density
+        mask[int(g.integers(nkeys))] = True
+        a = int(g.integers(qheads))
+        b = int(g.integers(a, qheads + 1))
+        for allowed in (None, mask):
+            ok1, want = oracle.heads(q, k, v, qheads, kvh, dim, nkeys, allowed, a, b)
+            ok2, got = oracle.heads(q, k, v, qheads, kvh, dim, nkeys, allowed, a, b,
+                                    checker=True)
+            assert ok1 and ok2
+            assert np.array_equal(bits32(got), bits32(want)), case
+    q = np.ones(32, np.float32)
+    big = np.full(32, np.finfo(np.float32).max, np.float32)
+    assert not oracle.heads(big, big, q, 1, 1, 32, 1, checker=True)[0]
+    # threaded prefill with a window: the checker form equals the timed form
+    qheads, kvh, dim, n = 8, 2, 64, 150
+    q = (g.standard_normal(n * qheads * dim) / 8).astype(np.float32)
+    k = g.standard_normal(n * kvh * dim).astype(np.float32)
+    v = g.standard_normal(n * kvh * dim).astype(np.float32)
+    for window in (0, 37):
+        ok1, want = oracle.threaded(q, n, k, v, qheads, kvh, dim, n, True, 0, 0, window,
+                                    threads=4)
+        ok2, got = oracle.threaded(q, n, k, v, qheads, kvh, dim, n, True, 0, 0, window,
+                                   threads=3, checker=True)
+        assert ok1 and ok2 and np.array_equal(bits32(got), bits32(want))
+
+
+def test_sampled_prefill_rows_equal_the_whole_prompts_rows(oracle):
+    # the CPU baseline's prefill sample: every step-th query of a prompt, each
+    # with its own position's causal (and window) mask
+    g = np.random.default_rng(0x5A3)
+    qheads, kvh, dim, n, step = 8, 2, 32, 97, 16
+    q = (g.standard_normal((n, qheads * dim)) / 6).astype(np.float32)
+    k = g.standard_normal(n * kvh * dim).astype(np.float32)
+    v = g.standard_normal(n * kvh * dim).astype(np.float32)
+    for window in (0, 20):
+        ok, full = oracle.threaded(q.reshape(-1), n, k, v, qheads, kvh, dim, n, True, 0, 0,
+                                   window, threads=3)
+        assert ok
+        rows = q[::step]
+        ok, part = oracle.threaded(rows.reshape(-1), len(rows), k, v, qheads, kvh, dim, n, True,
+                                   0, 0, window, threads=4, query_step=step)
+        assert ok
+        assert np.array_equal(part.reshape(len(rows), -1), full.reshape(n, -1)[::step])
+
+
 def test_multi_query_contract_equals_single_queries(oracle):
     # int8/tests.rs:661-768: every multi row equals its single-query call
     rng = Rng(0x7a11ed)
@@ -303,3 +370,17 @@ def test_binary32_twin_expf_matches_the_reference_libm_digest(oracle):
     # binary32 pattern (src/libm/tests.rs:20-22, 70, 80-84): glibc 2.28's
     # POWER8 expf, which the reference's libm ports
     assert oracle.libm_digest(2) == 0xFE568FD438D7D408
+
+
+def test_oracle_self_check_under_address_and_undefined_behaviour_sanitizers():
+    # make -C oracle sanitize: the oracle and its self-check built with
+    # -fsanitize=address,undefined (host code only) and run
+    import shutil
+    import subprocess
+    if shutil.which("make") is None or shutil.which("gcc") is None:
+        pytest.skip("no host C toolchain")
+    odir = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "oracle")
+    res = subprocess.run(["make", "-s", "-B", "-C", odir, "sanitize"], capture_output=True,
+                         text=True, timeout=300)
+    assert res.returncode == 0, res.stdout + res.stderr
+    assert "oracle selftest: ok" in res.stdout
