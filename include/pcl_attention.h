@@ -169,6 +169,30 @@ void *pcl_context_stream(pcl_context *ctx);
 int pcl_attention_launch(pcl_context *ctx, const pcl_attention_desc *desc);
 /* Workspace bytes a descriptor needs with the kernel it would run. */
 size_t pcl_attention_workspace_bytes(const pcl_attention_desc *desc);
+
+/* Bytes of the per-GPU scratch array of pcl_attention_launch_noalloc. */
+#define PCL_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* pcl_attention_launch without any allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The same kernels and results as pcl_attention_launch, bit for
+ * bit, but the chunk and span partials live in a file-scope device array of
+ * PCL_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends; its
+ * address is looked up once per device when the first context on that
+ * device is created) instead of the context's workspace. A descriptor whose
+ * pcl_attention_workspace_bytes exceeds that size returns
+ * PCL_RESOURCE_LIMIT (for example a prefill of more than 4096 keys with
+ * more than 64 Mi floats of running totals; the 32K and 128K decodes, the
+ * 4K prefills and the 256 x 2304 canvas fit). Calls no hipMalloc, hipFree
+ * or other allocating routine and records no timing spans. Every call on
+ * one GPU shares that GPU's array, which keeps the last call's contents (no
+ * part of it needs to start at zero: each launch writes every partial
+ * before its combine reads it): calls that overlap on one GPU, on
+ * different streams or contexts, race and must be serialised by the
+ * caller. PCL_NON_FINITE_VALUE if the scratch address could not be taken
+ * for this context's device. */
+int pcl_attention_launch_noalloc(pcl_context *ctx, const pcl_attention_desc *desc);
 int pcl_context_reserve(pcl_context *ctx, size_t bytes);
 /* Wait for the stream; *device_error receives the error flag (bit 0: a
  * non-finite allowed score, bit 1: a non-finite output, bit 2: a non-finite

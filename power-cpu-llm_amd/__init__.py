@@ -51,6 +51,7 @@ EXPORTS = (
     "pcl_context_destroy",
     "pcl_context_stream",
     "pcl_attention_launch",
+    "pcl_attention_launch_noalloc",
     "pcl_attention_workspace_bytes",
     "pcl_context_reserve",
     "pcl_context_sync",
@@ -160,6 +161,8 @@ def load():
     lib.pcl_context_stream.argtypes = [vp]
     lib.pcl_attention_launch.restype = ctypes.c_int
     lib.pcl_attention_launch.argtypes = [vp, ctypes.POINTER(PclDesc)]
+    lib.pcl_attention_launch_noalloc.restype = ctypes.c_int
+    lib.pcl_attention_launch_noalloc.argtypes = [vp, ctypes.POINTER(PclDesc)]
     lib.pcl_attention_workspace_bytes.restype = sz
     lib.pcl_attention_workspace_bytes.argtypes = [ctypes.POINTER(PclDesc)]
     lib.pcl_context_reserve.restype = ctypes.c_int
@@ -371,6 +374,14 @@ class Context:
 
     def launch(self, desc):
         rc = self.lib.pcl_attention_launch(self.handle, ctypes.byref(desc))
+        if rc != OK:
+            raise AttentionError(rc)
+
+    def launch_noalloc(self, desc):
+        """pcl_attention_launch_noalloc: the same launch with the partials in
+        the GPU's fixed scratch array (no allocation; calls on one GPU must
+        not overlap)."""
+        rc = self.lib.pcl_attention_launch_noalloc(self.handle, ctypes.byref(desc))
         if rc != OK:
             raise AttentionError(rc)
 

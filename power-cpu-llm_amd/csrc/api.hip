@@ -275,17 +275,12 @@ void close_span(pcl_context *ctx, int idx)
         (void)hipEventRecord(ctx->spans[idx].stop, ctx->stream);
 }
 
-int run_plan(pcl_context *ctx, Plan &plan)
+// Launches a plan with its workspace at `ws` (plan.ws_floats floats).
+int run_plan_ws(pcl_context *ctx, Plan &plan, float *ws)
 {
-    if (plan.empty)
-        return PCL_OK;
     Params &p = plan.p;
     p.err = ctx->err;
     if (plan.ws_floats) {
-        const int rc = ensure_workspace(ctx, plan.ws_floats * sizeof(float));
-        if (rc != PCL_OK)
-            return rc;
-        float *ws = static_cast<float *>(ctx->ws);
         if (plan.ws_floats > plan.rec_floats) {
             const size_t o_floats = (size_t)p.nkv * p.nrows_pad * p.nch * p.dk;
             const size_t ml_floats = (size_t)p.nkv * p.nrows_pad * p.nch * 2;
@@ -335,6 +330,53 @@ int run_plan(pcl_context *ctx, Plan &plan)
         return PCL_NON_FINITE_VALUE;
     }
     return PCL_OK;
+}
+
+int run_plan(pcl_context *ctx, Plan &plan)
+{
+    if (plan.empty)
+        return PCL_OK;
+    if (plan.ws_floats) {
+        const int rc = ensure_workspace(ctx, plan.ws_floats * sizeof(float));
+        if (rc != PCL_OK)
+            return rc;
+    }
+    return run_plan_ws(ctx, plan, static_cast<float *>(ctx->ws));
+}
+
+// ---- the allocation-free entry's scratch ------------------------------------
+//
+// A file-scope device array, one copy per GPU, held until the process ends.
+// Host code never passes the array's name to a kernel (on the host it is a
+// stand-in, not a device address): each device's address comes from
+// hipGetSymbolAddress, taken once per device when the first context on that
+// device is created, and the kernels receive it as their workspace.
+constexpr size_t kNoAllocScratchBytes = PCL_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kMaxScratchDevices];
+bool g_scratch_done[kMaxScratchDevices];
+
+// This device's scratch address (the device must be current), or null when
+// its lookup failed.
+void *noalloc_scratch(int device)
+{
+    if (device < 0 || device >= kMaxScratchDevices)
+        return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_done[device]) {
+        void *ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) {
+            report("scratch address", e);
+            ptr = nullptr;
+        }
+        g_scratch_ptr[device] = ptr;
+        g_scratch_done[device] = true;
+    }
+    return g_scratch_ptr[device];
 }
 
 // ---- host-pointer entries: one shared context, one call at a time ----------
@@ -479,6 +521,9 @@ static int context_create(int device, bool own, void *stream, pcl_context **out)
         pcl_context_destroy(ctx);
         return PCL_NON_FINITE_VALUE;
     }
+    // the allocation-free entry's scratch on this device (null: that entry
+    // reports the failure; every other entry works without it)
+    ctx->noalloc_scratch = noalloc_scratch(device);
     *out = ctx;
     return PCL_OK;
 }
@@ -570,6 +615,33 @@ int pcl_attention_launch(pcl_context *ctx, const pcl_attention_desc *desc)
         return rc;
     (void)hipSetDevice(ctx->device);
     return run_plan(ctx, plan);
+}
+
+int pcl_attention_launch_noalloc(pcl_context *ctx, const pcl_attention_desc *desc)
+{
+    if (!ctx || !desc)
+        return PCL_INVALID_SHAPE;
+    if (desc->kvheads <= 0 || desc->qheads % desc->kvheads != 0)
+        return PCL_INVALID_SHAPE;
+    const int64_t group = desc->qheads / desc->kvheads;
+    Plan plan;
+    const int rc = make_plan(*desc, desc->kh_first * group, desc->kh_end * group,
+                             desc->kh_first * group, &plan);
+    if (rc != PCL_OK)
+        return rc;
+    if (plan.empty)
+        return PCL_OK;
+    if (plan.ws_floats * sizeof(float) > kNoAllocScratchBytes)
+        return PCL_RESOURCE_LIMIT;
+    if (!ctx->noalloc_scratch)
+        return PCL_NON_FINITE_VALUE;
+    (void)hipSetDevice(ctx->device);
+    // no timing spans here: recording them creates events and grows a list
+    const bool timing = ctx->timing;
+    ctx->timing = false;
+    const int out = run_plan_ws(ctx, plan, static_cast<float *>(ctx->noalloc_scratch));
+    ctx->timing = timing;
+    return out;
 }
 
 int pcl_context_set_timing(pcl_context *ctx, int enable)

@@ -20,6 +20,8 @@ struct pcl_context {
     void *ws = nullptr;
     size_t ws_bytes = 0;
     int *err = nullptr;
+    // this device's scratch of pcl_attention_launch_noalloc (never freed)
+    void *noalloc_scratch = nullptr;
     // Staging buffers of the host-pointer entries (grow-only).
     void *stage[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
     size_t stage_bytes[5] = {0, 0, 0, 0, 0};
