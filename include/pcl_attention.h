@@ -112,6 +112,10 @@ enum pcl_kernel {
                                    pairs, head dim <= 256) + ordered combine */
     PCL_KERNEL_TWO_PASS = 5,    /* split-KV decode as a K-streaming pass and a
                                    V-streaming pass + ordered combine */
+    PCL_KERNEL_SPREAD_KV = 6,   /* split-KV decode with each key chunk spread
+                                   over head_dim/32 workgroups that exchange
+                                   raw scores (head dim <= 256, short
+                                   launches) + ordered combine */
 };
 
 /* Attention of nq query positions over keys [0, n0+n1): keys 0..n0-1 come

@@ -35,10 +35,10 @@ OK, INVALID_SHAPE, INVALID_PARAMETER, NON_FINITE_VALUE, RESOURCE_LIMIT = 0, 1, 2
 ERROR_NAMES = {INVALID_SHAPE: "InvalidShape", INVALID_PARAMETER: "InvalidParameter",
                NON_FINITE_VALUE: "NonFiniteValue", RESOURCE_LIMIT: "ResourceLimit"}
 (KERNEL_AUTO, KERNEL_SPLIT_KV, KERNEL_TILED, KERNEL_TILED_SPLIT, KERNEL_PIPE_KV,
- KERNEL_TWO_PASS) = 0, 1, 2, 3, 4, 5
+ KERNEL_TWO_PASS, KERNEL_SPREAD_KV) = 0, 1, 2, 3, 4, 5, 6
 KERNEL_NAMES = {KERNEL_SPLIT_KV: "split_kv", KERNEL_TILED: "tiled",
                 KERNEL_TILED_SPLIT: "tiled_split", KERNEL_PIPE_KV: "pipe_kv",
-                KERNEL_TWO_PASS: "two_pass"}
+                KERNEL_TWO_PASS: "two_pass", KERNEL_SPREAD_KV: "spread_kv"}
 
 # Every symbol include/pcl_attention.h declares.
 EXPORTS = (

@@ -4,6 +4,7 @@
 #include "pcl_attention.h"
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -16,8 +17,13 @@ hipError_t launch_combine(const Params &p, hipStream_t stream);
 hipError_t launch_pipe_kv(const Params &p, hipStream_t stream);
 hipError_t launch_tiled(const Params &p, int split, hipStream_t stream);
 hipError_t launch_two_pass(const Params &p, hipStream_t stream);
+hipError_t launch_spread_kv(const Params &p, hipStream_t stream);
 int tiled_rows(int dk);
 int rec_floats();
+int spread_slices(int dk);
+// published score words (64-bit) of one spread item: 16 key blocks x 4 x 64
+// lanes
+constexpr size_t kSpreadWordsPerItem = 2 * kTilesPerChunk * 4 * 64;
 } // namespace pcl
 
 using pcl::Params;
@@ -40,6 +46,32 @@ constexpr int kPipeMaxDk = 512;
 // Up to head dim 256 the pipelined kernel was as fast or faster at every
 // size tried (16 to 1024 items, d64/128/256).
 constexpr int64_t kPipeMinItemsWide = 512;
+// The spread decode's workgroups (dk/32 per item, two waves and 48 KiB of
+// LDS each, so three per CU) all fit on the chip at once up to this many:
+// 256 CUs x 3. Its workgroups wait for each other, so it is chosen only
+// within that bound and within the items its score-word region holds
+// (requested beyond them, the pipelined kernel runs).
+constexpr int64_t kSpreadMaxWorkgroups = 768;
+// Every non-empty workspace begins with the spread decode's region of
+// published score words, room for kSpreadMaxItems (chunk, unit, KV head)
+// items; no other data ever lands there, so a stale word carries an earlier
+// launch's epoch and never the current one.
+constexpr int64_t kSpreadMaxItems = 128;
+constexpr size_t kTagFloats = (size_t)kSpreadMaxItems * pcl::kSpreadWordsPerItem * 2;
+
+// Epochs of spread launches, per device: every launch on a device takes a
+// new one (shared by all contexts and the allocation-free scratch).
+constexpr int kMaxEpochDevices = 64;
+std::atomic<uint32_t> g_epoch[kMaxEpochDevices];
+
+uint32_t next_epoch(int device)
+{
+    std::atomic<uint32_t> &e = g_epoch[device >= 0 && device < kMaxEpochDevices ? device : 0];
+    uint32_t v = e.fetch_add(1, std::memory_order_relaxed) + 1;
+    while (v == 0) // 0 is the value of a flag never written
+        v = e.fetch_add(1, std::memory_order_relaxed) + 1;
+    return v;
+}
 
 void report(const char *what, hipError_t e)
 {
@@ -60,8 +92,12 @@ int64_t round_up(int64_t x, int64_t m)
 struct Plan {
     Params p;
     int kernel = PCL_KERNEL_SPLIT_KV;
+    // workspace floats: the spread decode's score words, then chunk and
+    // span partials (or the tiled kernel's running totals) and the two-pass
+    // tile records
     size_t ws_floats = 0;
-    size_t rec_floats = 0; // two-pass tile records (after the partials)
+    size_t part_floats = 0;
+    size_t rec_floats = 0;
     bool empty = false;    // nothing to compute
 };
 
@@ -81,8 +117,24 @@ void chunk_range(const pcl_attention_desc &d, int64_t nkeys, int64_t *c_lo, int6
     *c_hi = (k_hi + pcl::kChunk - 1) / pcl::kChunk;
 }
 
+// Workgroups of a spread launch, or 0 when the head dim has no spread form.
+int64_t spread_workgroups(int dk, int64_t nrows, int64_t nkv, int64_t nch)
+{
+    if (dk > 256)
+        return 0;
+    const int64_t units = (nrows + pcl::kRows - 1) / pcl::kRows;
+    if (nch * nkv * units > kSpreadMaxItems)
+        return 0;
+    return nch * nkv * units * pcl::spread_slices(dk);
+}
+
 int choose_kernel(int requested, int dk, int64_t nrows, int64_t nkv, int64_t nch)
 {
+    const int64_t spread = spread_workgroups(dk, nrows, nkv, nch);
+    const bool spread_fits = spread > 0 && spread <= kSpreadMaxWorkgroups;
+    if (requested == PCL_KERNEL_SPREAD_KV)
+        return spread_fits ? requested : dk <= kPipeMaxDk ? PCL_KERNEL_PIPE_KV
+                                                           : PCL_KERNEL_SPLIT_KV;
     if (requested == PCL_KERNEL_TILED || requested == PCL_KERNEL_TILED_SPLIT)
         return dk <= kTiledMaxDk ? requested : PCL_KERNEL_SPLIT_KV;
     if (requested == PCL_KERNEL_SPLIT_KV)
@@ -92,8 +144,11 @@ int choose_kernel(int requested, int dk, int64_t nrows, int64_t nkv, int64_t nch
     if (requested == PCL_KERNEL_TWO_PASS)
         return requested;
     if (dk > kTiledMaxDk || nrows < 64) {
-        // decode: the pipelined kernel; at head dim 512 short launches (few
+        // decode: short launches spread each chunk over several workgroups;
+        // otherwise the pipelined kernel; at head dim 512 short launches (few
         // workgroups, so latency-bound) take the four-phase kernel
+        if (spread_fits)
+            return PCL_KERNEL_SPREAD_KV;
         const int64_t units = (nrows + pcl::kRows - 1) / pcl::kRows;
         if (dk > 256 && nch * nkv * units < kPipeMinItemsWide)
             return PCL_KERNEL_SPLIT_KV;
@@ -115,7 +170,7 @@ int make_plan(const pcl_attention_desc &d, int64_t h_lo, int64_t h_hi, int64_t h
         d.dim % 16 != 0 || d.dim > kMaxDim || d.nq < 0 || d.n0 < 0 || d.n1 < 0 ||
         d.kh_first < 0 || d.kh_first > d.kh_end || d.kh_end > d.kvheads || d.window < 0)
         return PCL_INVALID_SHAPE;
-    if (d.kernel < PCL_KERNEL_AUTO || d.kernel > PCL_KERNEL_TWO_PASS)
+    if (d.kernel < PCL_KERNEL_AUTO || d.kernel > PCL_KERNEL_SPREAD_KV)
         return PCL_INVALID_PARAMETER;
     const int64_t group = d.qheads / d.kvheads;
     const int64_t nkeys = d.n0 + d.n1;
@@ -199,21 +254,31 @@ int make_plan(const pcl_attention_desc &d, int64_t h_lo, int64_t h_hi, int64_t h
     const bool partials = plan->kernel == PCL_KERNEL_TILED_SPLIT ||
                           ((plan->kernel == PCL_KERNEL_SPLIT_KV ||
                             plan->kernel == PCL_KERNEL_PIPE_KV ||
-                            plan->kernel == PCL_KERNEL_TWO_PASS) && nch > 1);
-    plan->ws_floats = 0;
+                            plan->kernel == PCL_KERNEL_TWO_PASS ||
+                            plan->kernel == PCL_KERNEL_SPREAD_KV) && nch > 1);
+    plan->part_floats = 0;
     if (partials) {
-        plan->ws_floats = (size_t)nkv * p.nrows_pad * nch * (dk + 2);
+        plan->part_floats = (size_t)nkv * p.nrows_pad * nch * (dk + 2);
         if (p.nspan > 1)
-            plan->ws_floats += (size_t)nkv * p.nrows_pad * p.nspan * (dk + 2);
+            plan->part_floats += (size_t)nkv * p.nrows_pad * p.nspan * (dk + 2);
     } else if (plan->kernel == PCL_KERNEL_TILED && p.nspan > 1) {
         // the tiled kernel's running totals across spans
-        plan->ws_floats = (size_t)nkv * p.nrows_pad * dk;
+        plan->part_floats = (size_t)nkv * p.nrows_pad * dk;
     }
-    if (plan->kernel == PCL_KERNEL_TWO_PASS) {
+    plan->part_floats = round_up((int64_t)plan->part_floats, 4);
+    plan->rec_floats = 0;
+    if (plan->kernel == PCL_KERNEL_TWO_PASS)
         plan->rec_floats = (size_t)nkv * p.units * nch * pcl::rec_floats();
-        plan->ws_floats = round_up((int64_t)plan->ws_floats, 4) + plan->rec_floats;
-    }
+    const size_t body = plan->part_floats + plan->rec_floats;
+    plan->ws_floats = body || plan->kernel == PCL_KERNEL_SPREAD_KV ? kTagFloats + body : 0;
     return PCL_OK;
+}
+
+__global__ void zero_words_kernel(uint32_t *words, int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n)
+        words[i] = 0;
 }
 
 int ensure_workspace(pcl_context *ctx, size_t bytes)
@@ -226,12 +291,24 @@ int ensure_workspace(pcl_context *ctx, size_t bytes)
         ctx->ws = nullptr;
         ctx->ws_bytes = 0;
     }
-    const hipError_t e = hipMalloc(&ctx->ws, bytes);
+    hipError_t e = hipMalloc(&ctx->ws, bytes);
     if (e != hipSuccess) {
+        ctx->ws = nullptr;
         report("workspace allocation", e);
         return PCL_RESOURCE_LIMIT;
     }
     ctx->ws_bytes = bytes;
+    // a new buffer's score-word region starts at zero, an epoch no launch
+    // takes (a fill kernel rather than a memset node, should a caller
+    // capture this)
+    const int nwords = (int)std::min<size_t>(kTagFloats, bytes / sizeof(uint32_t));
+    zero_words_kernel<<<(nwords + 255) / 256, 256, 0, ctx->stream>>>(
+        static_cast<uint32_t *>(ctx->ws), nwords);
+    e = hipGetLastError();
+    if (e != hipSuccess) {
+        report("workspace score words", e);
+        return PCL_NON_FINITE_VALUE;
+    }
     return PCL_OK;
 }
 
@@ -281,10 +358,11 @@ int run_plan_ws(pcl_context *ctx, Plan &plan, float *ws)
     Params &p = plan.p;
     p.err = ctx->err;
     if (plan.ws_floats) {
-        if (plan.ws_floats > plan.rec_floats) {
+        float *body = ws + kTagFloats;
+        if (plan.part_floats) {
             const size_t o_floats = (size_t)p.nkv * p.nrows_pad * p.nch * p.dk;
             const size_t ml_floats = (size_t)p.nkv * p.nrows_pad * p.nch * 2;
-            p.ws_o = ws;
+            p.ws_o = body;
             p.ws_ml = p.ws_o + o_floats;
             if (p.nspan > 1) {
                 p.ws2_o = p.ws_ml + ml_floats;
@@ -292,12 +370,17 @@ int run_plan_ws(pcl_context *ctx, Plan &plan, float *ws)
             }
         }
         if (plan.rec_floats)
-            p.ws_rec = ws + (plan.ws_floats - plan.rec_floats);
+            p.ws_rec = body + plan.part_floats;
+        if (plan.kernel == PCL_KERNEL_SPREAD_KV) {
+            p.ws_tag = reinterpret_cast<uint64_t *>(ws);
+            p.epoch = next_epoch(ctx->device);
+        }
     }
     hipError_t e = hipSuccess;
     const bool combine = plan.kernel == PCL_KERNEL_TILED_SPLIT ||
                          ((plan.kernel == PCL_KERNEL_SPLIT_KV || plan.kernel == PCL_KERNEL_PIPE_KV ||
-                           plan.kernel == PCL_KERNEL_TWO_PASS) &&
+                           plan.kernel == PCL_KERNEL_TWO_PASS ||
+                           plan.kernel == PCL_KERNEL_SPREAD_KV) &&
                           p.ws_o);
     int span = open_span(ctx, 0);
     switch (plan.kernel) {
@@ -315,6 +398,9 @@ int run_plan_ws(pcl_context *ctx, Plan &plan, float *ws)
         break;
     case PCL_KERNEL_TILED_SPLIT:
         e = pcl::launch_tiled(p, 1, ctx->stream);
+        break;
+    case PCL_KERNEL_SPREAD_KV:
+        e = pcl::launch_spread_kv(p, ctx->stream);
         break;
     default:
         return PCL_INVALID_SHAPE;

@@ -54,8 +54,10 @@ constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kNegInf = -__builtin_huge_valf();
 
 // Device error flag bits: a non-finite allowed score, a non-finite output, a
-// non-finite head-transform value.
-enum ErrorBits { kErrScore = 1, kErrOutput = 2, kErrTransform = 4 };
+// non-finite head-transform value, (8: the output block's non-finite value,)
+// a workgroup that gave up waiting for the scores of the other workgroups of
+// its chunk (its results are not valid).
+enum ErrorBits { kErrScore = 1, kErrOutput = 2, kErrTransform = 4, kErrWait = 16 };
 
 // Launch parameters shared by every kernel (host fills, passed by value).
 struct Params {
@@ -101,6 +103,10 @@ struct Params {
     int dk;        // padded head dim of the launch
     // tile records of the two-pass decode: [nkv][units][nch][kRecFloats]
     float *ws_rec;
+    // the spread decode's published scores, [items][16 blocks][4][64 lanes]
+    // words of (epoch, score bits), and the launch's epoch
+    uint64_t *ws_tag;
+    uint32_t epoch;
     int *err;
 };
 
@@ -181,6 +187,83 @@ __device__ __forceinline__ bool allowed(const Params &p, int row, int64_t t)
     const int64_t kp = p.first_key + t;
     const int64_t qp = p.first_query + query;
     return kp <= qp && (p.window == 0 || qp - kp < p.window);
+}
+
+// allowed() for one row over the keys [base, base + kChunk), with the row's
+// constants hoisted out of the key loop: a key's test is then a range check
+// against two per-lane bounds (chunk-relative), and, with an explicit mask,
+// a byte of the row's mask read only for keys inside the range (so never
+// past the mask row). Equal to allowed() for every key of the range.
+struct RowKeys {
+    int64_t lo, hi; // keys t with lo <= t <= hi pass the range
+    gu8_cptr mask;  // the row's mask bytes, or null
+};
+
+struct ChunkKeys {
+    int lo, hi;    // chunk-relative keys k with lo <= k <= hi pass the range
+    gu8_cptr mask; // the row's mask byte of the chunk's first key, or null
+};
+
+__device__ __forceinline__ RowKeys row_keys(const Params &p, int row)
+{
+    const bool in = row < p.nrows;
+    const int query = in ? row / p.group : 0;
+    RowKeys r;
+    r.lo = 0;
+    r.hi = in ? p.nkeys - 1 : -1;
+    if (!p.mask && p.causal) {
+        // kp <= qp and qp - kp < window with kp = first_key + t, qp = first_query + query
+        const int64_t rel = p.first_query + query - p.first_key;
+        r.hi = r.hi < rel ? r.hi : rel;
+        if (p.window)
+            r.lo = rel - p.window + 1;
+    }
+    r.mask = p.mask ? (gu8_cptr)p.mask + (int64_t)query * p.mask_stride : nullptr;
+    return r;
+}
+
+// The keys [base, base + kChunk) of a row.
+__device__ __forceinline__ ChunkKeys chunk_of(const RowKeys &r, int64_t base)
+{
+    const int64_t lo = r.lo - base, hi = r.hi - base;
+    ChunkKeys c;
+    c.lo = (int)(lo < 0 ? 0 : lo > kChunk ? kChunk : lo);
+    c.hi = (int)(hi < -1 ? -1 : hi > kChunk - 1 ? kChunk - 1 : hi);
+    c.mask = r.mask ? r.mask + base : nullptr;
+    return c;
+}
+
+__device__ __forceinline__ ChunkKeys chunk_keys(const Params &p, int row, int64_t base)
+{
+    return chunk_of(row_keys(p, row), base);
+}
+
+// Allowed flags of keys k0 + 4g + r (r = 0..3) of a chunk; true when any is.
+__device__ __forceinline__ bool block_keys(const ChunkKeys &c, int k0, int g, bool ok[4])
+{
+    bool any = false;
+    uint8_t m[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int k = k0 + 4 * g + r;
+        ok[r] = k >= c.lo && k <= c.hi;
+        m[r] = c.mask && ok[r] ? c.mask[k] : (uint8_t)1;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        ok[r] = ok[r] && m[r] != 0;
+        any |= ok[r];
+    }
+    return any;
+}
+
+// Allowed flags of the lane's eight keys of tile t (chunk-relative keys
+// 32t + 16b + 4g + r); true when any is.
+__device__ __forceinline__ bool tile_keys(const ChunkKeys &c, int t, int g, bool ok[2][4])
+{
+    const bool a0 = block_keys(c, t * kTile, g, ok[0]);
+    const bool a1 = block_keys(c, t * kTile + 16, g, ok[1]);
+    return a0 || a1;
 }
 
 // Butterflies across the four 16-lane groups: each lane combined with lane ^

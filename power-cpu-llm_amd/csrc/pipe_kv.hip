@@ -180,19 +180,13 @@ __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, i
             }
     };
     load_k(0, 0, 0);
+    const ChunkKeys ck = chunk_keys(p, row, cbase);
     float m = kNegInf;
     bool bad = false;
 #pragma unroll
     for (int t = 0; t < kTilesPerChunk; ++t) {
         bool ok[2][4];
-        bool any = false;
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                ok[b][r] = allowed(p, row, cbase + t * kTile + 16 * b + 4 * g + r);
-                any |= ok[b][r];
-            }
+        const bool any = tile_keys(ck, t, g, ok);
         const bool tile_any = __any(any);
         f4 acc[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
@@ -372,13 +366,9 @@ __device__ __forceinline__ void score_wave_dual(const Params &p, int unit, int k
         return acc;
     };
     // whether any key of this wave's block of tile t is allowed for the unit
+    const ChunkKeys ck = chunk_keys(p, row, cbase);
     auto block_any = [&](int t, bool ok[4]) {
-        bool any = false;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            ok[r] = allowed(p, row, cbase + t * kTile + 16 * ROLE + 4 * g + r);
-            any |= ok[r];
-        }
+        const bool any = block_keys(ck, t * kTile + 16 * ROLE, g, ok);
         return (bool)__any(any);
     };
 
@@ -411,13 +401,8 @@ __device__ __forceinline__ void score_wave_dual(const Params &p, int unit, int k
 #pragma unroll 1
     for (int t = 0; t < kTilesPerChunk; ++t) {
         bool ok[2][4];
-        bool any1 = false;
         const bool any0 = block_any(t, ok[0]);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            ok[1][r] = allowed(p, row, cbase + t * kTile + 16 + 4 * g + r);
-            any1 |= ok[1][r];
-        }
+        const bool any1 = block_keys(ck, t * kTile + 16, g, ok[1]);
         const bool tile_any = any0 || __any(any1);
         const f4 acc0 = chain(t, any0);
         float pr[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};

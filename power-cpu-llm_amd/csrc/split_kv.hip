@@ -105,17 +105,10 @@ __global__ __launch_bounds__(DK, SplitCfg<DK>::waves_per_eu) void split_kv_kerne
     // Masks of this wave's tiles.
     bool ok[TPW][2][4];
     bool wave_any[TPW];
+    const ChunkKeys ck = chunk_keys(p, row, cbase);
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
-        const int64_t kbase = cbase + (w * TPW + i) * kTile;
-        bool any = false;
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                ok[i][b][r] = allowed(p, row, kbase + 16 * b + 4 * g + r);
-                any |= ok[i][b][r];
-            }
+        const bool any = tile_keys(ck, w * TPW + i, g, ok[i]);
         wave_any[i] = __any(any);
     }
 

@@ -1,0 +1,321 @@
+// Spread split-KV decode for gfx950: one 256-key chunk over S = DK/32
+// workgroups, for short decodes whose (chunk, 16-row unit, KV head) items
+// are too few to fill the chip (a 2K decode has 64 of them on 256 CUs).
+//
+// Workgroup j of an item runs two waves and takes
+//   the scores of 16 / S of the chunk's 16 key blocks (one 16-key block per
+//   wave at head dim 256): the canonical score chain of attention_device.hpp
+//   on K read straight into MFMA operands, published to the workspace;
+//   output dims [32j, 32j + 32) (16 per wave): V for those dims and all 256
+//   keys is copied into LDS, requested right behind the wave's K.
+// The two waves then read the chunk's raw scores back (half each, shared
+// through LDS) and each runs the
+// tile-by-tile online softmax and the P.V chain for its own dims exactly as
+// the other kernels do (every workgroup of the item derives the same m, l
+// and probabilities, bit for bit). So each workgroup reads 1/S of the
+// chunk's K and 1/S of its V, and a 2K decode runs 512 workgroups.
+//
+// Publication needs no flag and no fence: every score is stored as one
+// 64-bit word (the launch's epoch, the score's bits) with a device-coherent
+// store, which lands whole, and a reader takes a word only when it carries
+// the current epoch. The words live in a region at the start of the
+// workspace that holds nothing else (zero when allocated; epochs are never
+// zero), so a stale word carries an earlier epoch.
+//
+// The wait is bounded: after kMaxPolls reads a wave gives up, sets kErrWait
+// in the error flag and finishes (its results are then not valid and the
+// host reports the failure), so every wave exits. The host picks this kernel
+// only for launches whose workgroups all fit on the chip at once, and a wave
+// waits only for the workgroups of its own item, adjacent in dispatch order.
+//
+// Output: for a launch of a single chunk, the output itself; otherwise the
+// chunk partial (m, l, O) for the combine kernel (split_kv.hip). (Merging
+// the partials in the kernel instead, by the last workgroup of each slice to
+// finish, was measured slower on MI355X: its chain of dependent memory round
+// trips outlasts the separate combine launch.)
+#include "attention_device.hpp"
+
+namespace pcl {
+
+constexpr int kSpreadWaves = 2;
+constexpr int kSpreadSliceDims = 32;
+constexpr int kBlocksPerChunk = 2 * kTilesPerChunk; // 16-key blocks
+constexpr int kMaxPolls = 1 << 16;                  // about 0.1 s of polling
+
+typedef __attribute__((address_space(1))) uint64_t *gu64_ptr;
+typedef __attribute__((address_space(3))) void *spread_lptr_t;
+typedef const __attribute__((address_space(1))) void *spread_gptr_t;
+
+__device__ __forceinline__ void publish(uint64_t *p, uint32_t epoch, float v)
+{
+    const uint64_t word = ((uint64_t)epoch << 32) | (uint64_t)__float_as_uint(v);
+    __hip_atomic_store((gu64_ptr)p, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t take(const uint64_t *p)
+{
+    return __hip_atomic_load((gu64_ptr)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+
+template <int DK, bool FULL>
+__global__ __launch_bounds__(64 * kSpreadWaves, 2) void spread_kv_kernel(Params p)
+{
+    constexpr int S = DK / kSpreadSliceDims;                  // workgroups per item
+    constexpr int BPW = kBlocksPerChunk / (S * kSpreadWaves); // score blocks per wave
+    constexpr int NU = DK / 32;                               // score chain steps
+    static_assert(BPW >= 1 && BPW * S * kSpreadWaves == kBlocksPerChunk, "whole blocks");
+
+    // V of each wave's 16 dims for the chunk's 256 keys, 1 KiB per 16-key
+    // block: slot j of a block (64 bytes, 16 dims) holds key 4(j % 4) + j / 4
+    // of the block, so the four keys 4g + r an MFMA step reads sit in four
+    // different 64-byte bank groups
+    __shared__ float vlds[kSpreadWaves][kBlocksPerChunk][16][16];
+    // the chunk's raw scores, [block][r][lane], gathered by both waves
+    __shared__ float slds[kBlocksPerChunk][4][64];
+    const int slice = blockIdx.x;
+    const int ci = blockIdx.y; // the launch's chunk index
+    const int c = p.c_lo + ci;
+    const int unit = blockIdx.z % p.units;
+    const int kvl = blockIdx.z / p.units;
+    const int64_t item = ((int64_t)blockIdx.z * p.nch + ci);
+    const int w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int col = lane & 15;
+    const int g = lane >> 4;
+    const int kh = p.kh_first + kvl;
+    const int row = unit * kRows + col;
+    const bool rin = row < p.nrows;
+    const int64_t cbase = (int64_t)c * kChunk;
+    const int64_t klast = p.nkeys - 1;
+    const int64_t hoff = (int64_t)kh * p.dim;
+    // the item's words: [block][r][lane]
+    uint64_t *words = p.ws_tag + item * (kBlocksPerChunk * 64 * 4);
+    const int d0 = kSpreadSliceDims * slice + 16 * w; // the wave's output dims
+
+    {
+        // Q^T B operands: Q[row][32u + 8g + jj] * q_scale (0 for padding rows).
+        float q[NU][8];
+        const int query = rin ? row / p.group : 0;
+        const int h = kh * p.group + (rin ? row % p.group : 0);
+        const float *qp = p.q + (int64_t)query * p.q_stride + (int64_t)h * p.dim;
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int d = 32 * u + 8 * g + 4 * hh;
+                const bool din = FULL || d < p.dim;
+                const f4 x = ldg4(qp + (din ? d : 0)) * p.q_scale;
+                const f4 v = (rin && din) ? x : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    q[u][4 * hh + j] = v[j];
+            }
+        // K of this wave's score blocks, straight into MFMA A operands
+        const int blk0 = (slice * kSpreadWaves + w) * BPW;
+        f4 kb[BPW][NU][2];
+#pragma unroll
+        for (int i = 0; i < BPW; ++i) {
+            const int64_t key = cbase + 16 * (blk0 + i) + col;
+            const float *kp = key_row(p, key < klast ? key : klast) + hoff;
+#pragma unroll
+            for (int u = 0; u < NU; ++u)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int d = 32 * u + 8 * g + 4 * hh;
+                    const bool din = FULL || d < p.dim;
+                    const f4 x = ldg4_stream(kp + (din ? d : 0));
+                    kb[i][u][hh] = din ? x : f4{0.f, 0.f, 0.f, 0.f};
+                }
+        }
+        // V of the wave's 16 dims, HBM -> LDS with no register staging,
+        // requested behind K so that it streams while the scores are formed:
+        // lane L of block i's copy moves 16 bytes (dims d0 + 4(L % 4) ..)
+        // of key 16i + 4(s % 4) + s / 4 into slot s = L / 4. A dim past the
+        // head's last copies the head's first dims instead (that output is
+        // dropped).
+        {
+            const int sl = lane >> 2;
+            const int kin = 4 * (sl & 3) + (sl >> 2);
+            const int vd = 4 * (lane & 3);
+            const int dv = FULL || d0 + vd < p.dim ? d0 + vd : 0;
+            float *vl = &vlds[w][0][0][0];
+#pragma unroll
+            for (int i = 0; i < kBlocksPerChunk; ++i) {
+                const int64_t key = cbase + 16 * i + kin;
+                const float *vp = value_row(p, key < klast ? key : klast) + hoff + dv;
+                __builtin_amdgcn_global_load_lds((spread_gptr_t)vp,
+                                                 (spread_lptr_t)(vl + i * 256), 16, 0, 0);
+            }
+        }
+        // the score chains, each block published
+#pragma unroll
+        for (int i = 0; i < BPW; ++i) {
+            f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < NU; ++u)
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj)
+                    acc = mfma(kb[i][u][jj >> 2][jj & 3], q[u][jj], acc);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                publish(words + ((blk0 + i) * 4 + r) * 64 + lane, p.epoch, acc[r]);
+        }
+    }
+
+    // The chunk's raw scores once every word carries this launch's epoch
+    // (bounded): each wave takes half of the blocks and leaves them in LDS.
+    {
+        constexpr int HB = kBlocksPerChunk / kSpreadWaves;
+        uint64_t x[HB][4];
+        for (int polls = 0;;) {
+            // an opaque base each pass: the loads' addresses are formed here
+            // from it (otherwise the compiler keeps them all live across the
+            // loop)
+            const uint64_t *base = words + (w * HB * 4) * 64 + lane;
+            asm volatile("" : "+v"(base));
+            bool fresh = true;
+#pragma unroll
+            for (int b = 0; b < HB; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    x[b][r] = take(base + (b * 4 + r) * 64);
+                    fresh &= (uint32_t)(x[b][r] >> 32) == p.epoch;
+                }
+            if (__all(fresh))
+                break;
+            if (++polls >= kMaxPolls) {
+                if (lane == 0)
+                    atomicOr(p.err, kErrWait);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+#pragma unroll
+        for (int b = 0; b < HB; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                slds[w * HB + b][r][lane] = __uint_as_float((uint32_t)x[b][r]);
+    }
+    // the V copies have landed (s_waitcnt covers the LDS copies too) and both
+    // halves of the scores are in LDS
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+
+    // Online softmax and the P.V chain of this wave's 16 dims, tile by tile.
+    float m = kNegInf, l = 0.f;
+    f4 O = f4{0.f, 0.f, 0.f, 0.f};
+    bool bad = false;
+    const ChunkKeys ck = chunk_keys(p, row, cbase);
+#pragma unroll
+    for (int t = 0; t < kTilesPerChunk; ++t) {
+        // A tile that every real row of the unit sees whole needs no per-key
+        // test (padding rows then count as allowed: their columns never
+        // reach a real row's state, and any non-finite score they see a
+        // real row sees too).
+        bool ok[2][4];
+        bool tile_any;
+        if (!p.mask && __all(!rin || (ck.lo <= t * kTile && ck.hi >= t * kTile + kTile - 1))) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    ok[b][r] = true;
+            tile_any = true;
+        } else {
+            const bool any = tile_keys(ck, t, g, ok);
+            tile_any = __any(any);
+        }
+        float pr[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        float alpha, rs = 0.f;
+        if (tile_any) {
+            float sv[2][4];
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    sv[b][r] = slds[2 * t + b][r][lane];
+            bad |= bad_scores(sv, ok);
+            const float mn = fmaxf(m, tile_max(sv, ok));
+            const float ms = safe_max(mn);
+            alpha = fexp(m - ms);
+            rs = tile_probs(sv, ok, ms, pr);
+            m = mn;
+        } else {
+            // nothing allowed for the unit: alpha = exp(m - safe(m)), rs = 0
+            alpha = fexp(m - safe_max(m));
+        }
+        l = __builtin_fmaf(l, alpha, rs);
+        if (tile_any) {
+            O = O * alpha;
+#pragma unroll
+            for (int br = 0; br < 8; ++br) {
+                // key 16b + 4g + r of block 2t + b sits in slot 4r + g
+                const int b = br >> 2, r = br & 3;
+                O = mfma(vlds[w][2 * t + b][4 * r + g][col], pr[b][r], O);
+            }
+        }
+    }
+    if (bad && slice == 0 && w == 0)
+        atomicOr(p.err, kErrScore);
+
+    // O[i] is dim d0 + 4g + i of row `row`.
+    const int d = d0 + 4 * g;
+    const bool dout = rin && (FULL || d < p.dim);
+    if (p.ws_o == nullptr) { // the launch's only chunk: final output
+        if (!rin)
+            return;
+        const int query = row / p.group;
+        const int h = kh * p.group + row % p.group;
+        if (h < p.h_lo || h >= p.h_hi || !dout)
+            return;
+        float *o = p.out + (int64_t)query * p.o_stride + (int64_t)(h - p.h_base) * p.dim;
+        f4 v;
+        bool nonfinite = false;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = O[i] / l;
+            nonfinite |= !is_finite(v[i]);
+        }
+        stg4(o + d, v);
+        if (nonfinite)
+            atomicOr(p.err, kErrOutput);
+        return;
+    }
+
+    const int64_t slot = ((int64_t)kvl * p.nrows_pad + row) * p.nch + ci;
+    if (dout)
+        stg4(p.ws_o + slot * p.dk + d, O);
+    if (rin && slice == 0 && w == 0 && g == 0) {
+        stg(p.ws_ml + 2 * slot, m);
+        stg(p.ws_ml + 2 * slot + 1, l);
+    }
+}
+
+int spread_slices(int dk)
+{
+    return dk / kSpreadSliceDims;
+}
+
+template <int DK>
+static hipError_t launch_dk(const Params &p, hipStream_t stream)
+{
+    const dim3 grid(DK / kSpreadSliceDims, p.nch, p.nkv * p.units);
+    if (p.dim == DK)
+        spread_kv_kernel<DK, true><<<grid, 64 * kSpreadWaves, 0, stream>>>(p);
+    else
+        spread_kv_kernel<DK, false><<<grid, 64 * kSpreadWaves, 0, stream>>>(p);
+    return hipGetLastError();
+}
+
+hipError_t launch_spread_kv(const Params &p, hipStream_t stream)
+{
+    switch (p.dk) {
+    case 64: return launch_dk<64>(p, stream);
+    case 128: return launch_dk<128>(p, stream);
+    case 256: return launch_dk<256>(p, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+} // namespace pcl

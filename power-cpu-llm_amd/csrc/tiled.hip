@@ -104,6 +104,7 @@ void tiled_kernel(Params p, int split, int z0)
     // rows that are written (others are computed and dropped)
     const bool rout = rin && head >= p.h_lo && head < p.h_hi;
 
+    const RowKeys rk = row_keys(p, row); // the row's allowed keys (boundary tiles)
     // Key range the workgroup can see.
     int64_t k_lo = 0, k_hi = p.nkeys;
     if (!p.mask && p.causal) {
@@ -287,13 +288,7 @@ void tiled_kernel(Params p, int split, int z0)
                     ok[b][r] = true;
             any = true;
         } else {
-#pragma unroll
-            for (int b = 0; b < 2; ++b)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    ok[b][r] = allowed(p, row, (int64_t)t * kTile + 16 * b + 4 * g + r);
-                    any |= ok[b][r];
-                }
+            any = tile_keys(chunk_of(rk, (int64_t)t * kTile), 0, g, ok);
         }
         if (__any(any)) {
             // score chain, the next u-step's K operands read ahead of the MFMAs

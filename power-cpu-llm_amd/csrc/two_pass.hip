@@ -127,12 +127,11 @@ __global__ __launch_bounds__(64) void score_pass_kernel(Params p)
     // block (wave-uniform); the others' scores are never read, so their MFMAs
     // are skipped.
     uint32_t live = 0;
+    const ChunkKeys ck = chunk_keys(p, row, cbase);
 #pragma nounroll
     for (int blk = 0; blk < 16; ++blk) {
-        bool any = false;
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            any |= allowed(p, row, cbase + 16 * blk + 4 * g + r);
+        bool ok[4];
+        const bool any = block_keys(ck, 16 * blk, g, ok);
         live |= (uint32_t)__any(any) << blk;
     }
     live = __builtin_amdgcn_readfirstlane(live);
@@ -223,17 +222,11 @@ __global__ __launch_bounds__(64 * value_waves<DK>()) void value_pass_kernel(Para
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             O[a][j] = f4{0.f, 0.f, 0.f, 0.f};
+    const ChunkKeys ck = chunk_keys(p, row, cbase);
 #pragma unroll
     for (int t = 0; t < kTilesPerChunk; ++t) {
         bool ok[2][4];
-        bool any = false;
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                ok[b][r] = allowed(p, row, cbase + t * kTile + 16 * b + 4 * g + r);
-                any |= ok[b][r];
-            }
+        const bool any = tile_keys(ck, t, g, ok);
         const bool tile_any = __any(any);
         float pr[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
         float alpha, rs = 0.f;

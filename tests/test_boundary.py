@@ -94,8 +94,9 @@ def test_descriptor_validation_on_the_host(pcl):
     d.window = 1024  # five chunks per head: short, so at d512 the four-phase kernel
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_SPLIT_KV
     d.dim, d.q_stride, d.o_stride = 256, 16 * 256, 16 * 256
-    # up to head dim 256 every decode streams through the pipelined kernel
-    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
+    # up to head dim 256 a short decode (4 chunks x 8 KV heads) spreads each
+    # chunk over 8 workgroups
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_SPREAD_KV
     d.kernel = pcl.KERNEL_PIPE_KV  # forced choices are kept where the kernel exists
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
     d.kernel = pcl.KERNEL_TWO_PASS
@@ -103,7 +104,15 @@ def test_descriptor_validation_on_the_host(pcl):
     d.kernel = pcl.KERNEL_PIPE_KV
     d.dim, d.q_stride, d.o_stride = 512, 16 * 512, 16 * 512
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
-    d.kernel = 6  # no such kernel
+    d.kernel = pcl.KERNEL_SPREAD_KV  # no spread form at head dim 512: pipelined
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
+    d.dim, d.q_stride, d.o_stride, d.window = 256, 16 * 256, 16 * 256, 0
+    # 128 chunks x 8 KV heads is beyond the spread bound: pipelined
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
+    d.window = 1024
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_SPREAD_KV
+    d.dim, d.q_stride, d.o_stride = 512, 16 * 512, 16 * 512
+    d.kernel = 7  # no such kernel
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == -1
     d.kernel, d.dim, d.q_stride, d.o_stride = 0, 256, 16 * 256, 16 * 256
     d.dim = 24

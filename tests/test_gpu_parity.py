@@ -378,11 +378,11 @@ def test_every_kernel_gives_identical_bits(torch, ctx, oracle, case):
     k = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
     v = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
     outs = {}
-    for kernel in (1, 2, 3, 4, 5):
+    for kernel in (1, 2, 3, 4, 5, 6):
         outs[kernel], err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel, causal,
                                      window, 0, fq)
         assert err == 0
-    for kernel in (2, 3, 4, 5):
+    for kernel in (2, 3, 4, 5, 6):
         assert np.array_equal(bits(outs[1]), bits(outs[kernel])), kernel
     for i in sorted({0, nq // 2, nq - 1}):
         m = oracle.encoder_mask(0, nkeys, fq + i, window or None) if causal else None
@@ -405,14 +405,14 @@ def test_split_launch_tail_with_masks_segments_and_kv_ranges(torch, ctx, oracle)
     mask = g.random((nq, nkeys)) < 0.7
     mask[:, -1] = True
     outs = {}
-    for kernel in (1, 2, 3, 4, 5):
+    for kernel in (1, 2, 3, 4, 5, 6):
         for kv in [(0, kvh), (2, 7)]:
             out, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel, mask=mask,
                                 split_at=nkeys - nq, kv=kv)
             assert err == 0
             outs[(kernel, kv)] = out
     for kv in [(0, kvh), (2, 7)]:
-        for kernel in (2, 3, 4, 5):
+        for kernel in (2, 3, 4, 5, 6):
             assert np.array_equal(bits(outs[(1, kv)]), bits(outs[(kernel, kv)])), (kernel, kv)
     group = qheads // kvh
     for i in (0, nq - 1):
@@ -434,7 +434,7 @@ def test_explicit_masks_segments_scale_and_kv_ranges_keep_bits(torch, ctx):
     scale = np.float32(1.0 / 16.0)
     base, err = run_desc(torch, ctx, prescale(q, dim), k, v, qheads, kvh, dim, 1, 1, 300, 0, fq)
     assert err == 0
-    for kernel in (1, 2, 3, 4, 5):
+    for kernel in (1, 2, 3, 4, 5, 6):
         # explicit byte masks equal the descriptor's causal window
         got, err = run_desc(torch, ctx, prescale(q, dim), k, v, qheads, kvh, dim, kernel,
                             mask=mask)
@@ -465,7 +465,7 @@ def test_long_launch_combines_agree_across_kernels(torch, ctx, oracle):
     k = gpu_normals(torch, 0x5EED0778, (nkeys, kvh, dim))
     v = gpu_normals(torch, 0x5EED0779, (nkeys, kvh, dim))
     outs = {}
-    for kernel in (1, 2, 3, 4, 5):
+    for kernel in (1, 2, 3, 4, 5, 6):
         out = torch.full((nq, qheads, dim), float("nan"), device="cuda:0")
         d = ctx.desc(q=q.data_ptr(), q_stride=qheads * dim, nq=nq, k0=k.data_ptr(),
                      v0=v.data_ptr(), n0=nkeys, qheads=qheads, kvheads=kvh, dim=dim, kh_first=0,
@@ -475,7 +475,7 @@ def test_long_launch_combines_agree_across_kernels(torch, ctx, oracle):
         ctx.launch(d)
         assert ctx.sync() == 0
         outs[kernel] = out.cpu().numpy()
-    for kernel in (2, 3, 4, 5):
+    for kernel in (2, 3, 4, 5, 6):
         assert np.array_equal(bits(outs[1]), bits(outs[kernel])), kernel
     qn, kn, vn = (x.cpu().numpy().reshape(-1) for x in (q, k, v))
     for i in (0, nq - 1):
@@ -513,7 +513,7 @@ def test_device_error_flags(torch, ctx):
     bad_k[10, 1, 5] = np.nan
     bad_v = v.copy()
     bad_v[20, 0, 3] = np.inf
-    for kernel in (1, 2, 3, 4, 5):
+    for kernel in (1, 2, 3, 4, 5, 6):
         _, err = run_desc(torch, ctx, q, bad_k, v, qheads, kvh, dim, kernel)
         assert err & 1
         _, err = run_desc(torch, ctx, q, k, bad_v, qheads, kvh, dim, kernel)
@@ -540,7 +540,7 @@ def test_padded_head_dims_read_only_the_callers_rows(torch, ctx, oracle, dim):
     vbuf[:n] = torch.from_numpy(v.reshape(-1)).to("cuda:0")
     tq = torch.from_numpy(q).to("cuda:0")
     outs = {}
-    for kernel in (2, 3, 1, 4, 5):
+    for kernel in (2, 3, 1, 4, 5, 6):
         out = torch.full((nq, qheads * dim), float("nan"), device="cuda:0")
         d = ctx.desc(q=tq.data_ptr(), q_stride=qheads * dim, nq=nq, k0=kbuf.data_ptr(),
                      v0=vbuf.data_ptr(), n0=nkeys, qheads=qheads, kvheads=kvh, dim=dim,
@@ -552,7 +552,7 @@ def test_padded_head_dims_read_only_the_callers_rows(torch, ctx, oracle, dim):
         assert ctx.sync() == 0, kernel
         outs[kernel] = out.cpu().numpy()
         assert np.all(np.isfinite(outs[kernel])), kernel
-    for kernel in (3, 1, 4, 5):
+    for kernel in (3, 1, 4, 5, 6):
         assert np.array_equal(bits(outs[2]), bits(outs[kernel])), kernel
     for i in (0, nq - 1):
         m = oracle.encoder_mask(0, nkeys, nkeys - nq + i, None)
@@ -577,7 +577,7 @@ def decode_config(torch, ctx, oracle, qheads, kvh, dim, nkeys, window, seed, uni
         k = k / k.norm(dim=-1, keepdim=True)
     outs = {}
     # the automatic choice, then every split-KV kernel: all bitwise equal
-    for kernel in (0, 1, 4, 5):
+    for kernel in (0, 1, 4, 5, 6):
         out = torch.full((1, qheads, dim), float("nan"), device="cuda:0")
         d = ctx.desc(q=q.data_ptr(), q_stride=qheads * dim, nq=1, k0=k.data_ptr(),
                      v0=v.data_ptr(), n0=nkeys, qheads=qheads, kvheads=kvh, dim=dim, kh_first=0,

@@ -397,13 +397,14 @@ def test_speculative_verify_over_a_long_cache(pcl, torch, ctx, oracle, nq, windo
     cache.commit()
     pending = cache.append(k[cached:].data_ptr(), v[cached:].data_ptr(), nq)
     outs = {}
-    for kernel in (0, 1, 2, 4, 5):
+    for kernel in (0, 1, 2, 4, 5, 6):
         out = torch.full((nq, qheads * dim), float("nan"), device="cuda:0")
         d = cache.encoder_desc(pending, q=q.data_ptr(), q_stride=qheads * dim, nq=nq,
                                qheads=qheads, kh_first=0, kh_end=kvh, out=out.data_ptr(),
                                o_stride=qheads * dim, kernel=kernel)
         if kernel == 0:
-            assert ctx.resolve_kernel(d) in (pcl.KERNEL_SPLIT_KV, pcl.KERNEL_PIPE_KV)
+            assert ctx.resolve_kernel(d) in (pcl.KERNEL_SPLIT_KV, pcl.KERNEL_PIPE_KV,
+                                             pcl.KERNEL_SPREAD_KV)
         ctx.reserve(ctx.workspace_bytes(d))
         ctx.launch(d)
         assert ctx.sync() == 0
