@@ -207,25 +207,8 @@ __global__ __launch_bounds__(64 * kSpreadWaves, 2) void spread_kv_kernel(Params 
     f4 O = f4{0.f, 0.f, 0.f, 0.f};
     bool bad = false;
     const ChunkKeys ck = chunk_keys(p, row, cbase);
-#pragma unroll
-    for (int t = 0; t < kTilesPerChunk; ++t) {
-        // A tile that every real row of the unit sees whole needs no per-key
-        // test (padding rows then count as allowed: their columns never
-        // reach a real row's state, and any non-finite score they see a
-        // real row sees too).
-        bool ok[2][4];
-        bool tile_any;
-        if (!p.mask && __all(!rin || (ck.lo <= t * kTile && ck.hi >= t * kTile + kTile - 1))) {
-#pragma unroll
-            for (int b = 0; b < 2; ++b)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    ok[b][r] = true;
-            tile_any = true;
-        } else {
-            const bool any = tile_keys(ck, t, g, ok);
-            tile_any = __any(any);
-        }
+    // one tile: ok the lane's allowed keys, tile_any whether the unit has any
+    auto tile_step = [&](int t, const bool ok[2][4], bool tile_any) {
         float pr[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
         float alpha, rs = 0.f;
         if (tile_any) {
@@ -254,6 +237,24 @@ __global__ __launch_bounds__(64 * kSpreadWaves, 2) void spread_kv_kernel(Params 
                 const int b = br >> 2, r = br & 3;
                 O = mfma(vlds[w][2 * t + b][4 * r + g][col], pr[b][r], O);
             }
+        }
+    };
+    // A chunk that every real row of the unit sees whole (the usual decode
+    // chunk) needs no per-key test and runs its tiles as one branch-free
+    // sequence (padding rows then count as allowed: their columns never
+    // reach a real row's state, and any non-finite score they see a real row
+    // sees too).
+    if (!p.mask && __all(!rin || (ck.lo <= 0 && ck.hi >= kChunk - 1))) {
+        const bool ok[2][4] = {{true, true, true, true}, {true, true, true, true}};
+#pragma unroll
+        for (int t = 0; t < kTilesPerChunk; ++t)
+            tile_step(t, ok, true);
+    } else {
+#pragma unroll
+        for (int t = 0; t < kTilesPerChunk; ++t) {
+            bool ok[2][4];
+            const bool any = tile_keys(ck, t, g, ok);
+            tile_step(t, ok, __any(any));
         }
     }
     if (bad && slice == 0 && w == 0)
