@@ -51,6 +51,10 @@ WORKLOADS = {
     "prefill_4k_window1024": (16, 8, 256, 4096, 4096, True, 1024, 0, "prefill", False),
     "prefill_4k": (16, 8, 256, 4096, 4096, True, 0, 0, "prefill", False),
     "canvas_256x2304": (16, 8, 256, 256, 2304, False, 0, 2048, "canvas", False),
+    # the global-layer geometry of Gemma-4 / DiffusionGemma (16 query heads,
+    # 2 KV heads, head dim 512) through the same prefill and canvas paths
+    "prefill_4k_d512": (16, 2, 512, 4096, 4096, True, 0, 0, "prefill", True),
+    "canvas_256x2304_d512": (16, 2, 512, 256, 2304, False, 0, 2048, "canvas", True),
     # speculative verification (encode_speculative: the previous token and 7
     # drafts, causal over the cache and themselves)
     "verify_32k_q8": (16, 8, 256, 8, 32768, True, 0, 32760, "decode", False),

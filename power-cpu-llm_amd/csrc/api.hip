@@ -35,7 +35,7 @@ namespace {
 constexpr int kMaxDim = 512;
 constexpr int64_t kMaxKeys = (int64_t)1 << 30;
 constexpr int64_t kMaxRowsTimesKvHeads = (int64_t)1 << 22;
-constexpr int kTiledMaxDk = 256;
+constexpr int kTiledMaxDk = 512;
 constexpr int kPipeMaxDk = 512;
 // Decode launches take the pipelined kernel, except at head dims above 256
 // with fewer than this many (chunk, unit, KV head) items: there each

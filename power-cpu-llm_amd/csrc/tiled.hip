@@ -474,9 +474,13 @@ template <int DK> static hipError_t launch_tiled_dk(const Params &p, int split, 
     return launch_pipe_kv_chunks(p, p.nch - tail, tail, stream);
 }
 
-int tiled_rows(int)
+hipError_t launch_tiled_wide(const Params &p, int split, hipStream_t stream);
+int tiled_wide_rows();
+
+// Rows of one workgroup: 128 up to head dim 256; 64 at 512 (tiled_wide.hip).
+int tiled_rows(int dk)
 {
-    return kTiledRows;
+    return dk > 256 ? tiled_wide_rows() : kTiledRows;
 }
 
 hipError_t launch_tiled(const Params &p, int split, hipStream_t stream)
@@ -485,6 +489,7 @@ hipError_t launch_tiled(const Params &p, int split, hipStream_t stream)
     case 64: return launch_tiled_dk<64>(p, split, stream);
     case 128: return launch_tiled_dk<128>(p, split, stream);
     case 256: return launch_tiled_dk<256>(p, split, stream);
+    case 512: return launch_tiled_wide(p, split, stream);
     default: return hipErrorInvalidValue;
     }
 }

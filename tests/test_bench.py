@@ -27,6 +27,9 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     ("prefill_4k", 137_472_507_904, None, 8_390_656),
     # config 5: 256 canvas queries over 2304 keys, non-causal (per step)
     ("canvas_256x2304", 9_663_676_416, 46_137_344, None),
+    # the same prefill and canvas at the global-layer geometry (16/2, d 512)
+    ("prefill_4k_d512", 274_945_015_808, None, 8_390_656),
+    ("canvas_256x2304_d512", 19_327_352_832, None, None),
 ])
 def test_algorithmic_work_matches_the_configs(name, flops, bytes_, pairs):
     f, b, p = bench.work(name)

@@ -367,6 +367,11 @@ DESC_CASES = [
     # chunk-split kernel runs the last chunk as single-wave workgroups
     (16, 8, 64, 256, 2304, 0, 0, 0),
     (16, 8, 128, 256, 2304, 1, 700, 2048),
+    # head dim 512 (and 320, padded to 512) through the wave-pair tiled
+    # kernel, one pass and one chunk per block
+    (16, 2, 512, 100, 700, 1, 0, 600),
+    (16, 2, 512, 40, 5000, 1, 0, 4960),
+    (8, 2, 320, 70, 400, 1, 130, 330),
 ]
 
 
@@ -679,3 +684,73 @@ def test_config5_canvas_48_denoising_steps(torch, ctx, oracle, steps):
                                    threads=THREADS, checker=True)
         assert ok, step
         assert_parity(got, want, dim)
+
+
+@pytest.mark.parametrize("window", [0, 1024], ids=["global", "window1024"])
+def test_head_dim_512_prefill_4096(torch, ctx, oracle, window):
+    """The Gemma-4 / DiffusionGemma global-layer geometry (16 query heads, 2
+    KV heads, head dim 512) over a 4096-token prompt, K rows unit-norm: the
+    automatic choice (the wave-pair tiled kernel), the chunk-split tiled
+    kernel and the split-KV kernel agree bitwise, and every row matches the
+    exact oracle within 1e-4 with the same argmax."""
+    qheads, kvh, dim, n = 16, 2, 512, 4096
+    seed = 0x5EED0D12
+    q = gpu_normals(torch, seed, (n, qheads, dim)) * float(np.float32(1.0 / math.sqrt(dim)))
+    k = gpu_normals(torch, seed + 1, (n, kvh, dim))
+    k = k / k.norm(dim=-1, keepdim=True)
+    v = gpu_normals(torch, seed + 2, (n, kvh, dim))
+    outs = {}
+    for kernel in (0, 2, 3, 1):
+        out = torch.empty((n, qheads, dim), device="cuda:0")
+        d = ctx.desc(q=q.data_ptr(), q_stride=qheads * dim, nq=n, k0=k.data_ptr(),
+                     v0=v.data_ptr(), n0=n, qheads=qheads, kvheads=kvh, dim=dim, kh_first=0,
+                     kh_end=kvh, causal=1, window=window, first_key=0, first_query=0,
+                     out=out.data_ptr(), o_stride=qheads * dim, kernel=kernel)
+        if kernel == 0:
+            assert ctx.resolve_kernel(d) == 2
+        ctx.reserve(ctx.workspace_bytes(d))
+        ctx.launch(d)
+        assert ctx.sync() == 0
+        outs[kernel] = out.cpu().numpy()
+    for kernel in (2, 3, 1):
+        assert np.array_equal(bits(outs[0]), bits(outs[kernel])), kernel
+    qn, kn, vn = (x.cpu().numpy().reshape(-1) for x in (q, k, v))
+    ok, want = oracle.threaded(qn, n, kn, vn, qheads, kvh, dim, n, True, 0, 0, window,
+                               threads=THREADS, checker=True)
+    assert ok
+    assert_parity(outs[0], want, dim)
+
+
+def test_head_dim_512_canvas(torch, ctx, oracle):
+    """A DiffusionGemma global-layer canvas step: 256 canvas rows over a
+    2048-token prefix and the step's own K/V (second segment), non-causal,
+    16/2 heads at head dim 512: every kernel bitwise equal, every row within
+    1e-4 of the exact oracle with the same argmax."""
+    qheads, kvh, dim, prefix, canvas = 16, 2, 512, 2048, 256
+    kp = gpu_normals(torch, 0x5EED0D15, (prefix, kvh, dim))
+    vp = gpu_normals(torch, 0x5EED0D16, (prefix, kvh, dim))
+    q = gpu_normals(torch, 0x5EED0D17, (canvas, qheads, dim)) * float(
+        np.float32(1.0 / math.sqrt(dim)))
+    kc = gpu_normals(torch, 0x5EED0D18, (canvas, kvh, dim))
+    vc = gpu_normals(torch, 0x5EED0D19, (canvas, kvh, dim))
+    outs = {}
+    for kernel in (0, 2, 3, 4, 1):
+        out = torch.empty((canvas, qheads, dim), device="cuda:0")
+        d = ctx.desc(q=q.data_ptr(), q_stride=qheads * dim, nq=canvas, k0=kp.data_ptr(),
+                     v0=vp.data_ptr(), n0=prefix, k1=kc.data_ptr(), v1=vc.data_ptr(), n1=canvas,
+                     qheads=qheads, kvheads=kvh, dim=dim, kh_first=0, kh_end=kvh, causal=0,
+                     out=out.data_ptr(), o_stride=qheads * dim, kernel=kernel)
+        if kernel == 0:
+            assert ctx.resolve_kernel(d) in (2, 3)
+        ctx.reserve(ctx.workspace_bytes(d))
+        ctx.launch(d)
+        assert ctx.sync() == 0
+        outs[kernel] = out.cpu().numpy()
+    for kernel in (2, 3, 4, 1):
+        assert np.array_equal(bits(outs[0]), bits(outs[kernel])), kernel
+    kn = np.concatenate([kp.cpu().numpy(), kc.cpu().numpy()]).reshape(-1)
+    vn = np.concatenate([vp.cpu().numpy(), vc.cpu().numpy()]).reshape(-1)
+    ok, want = oracle.threaded(q.cpu().numpy().reshape(-1), canvas, kn, vn, qheads, kvh, dim,
+                               prefix + canvas, False, threads=THREADS, checker=True)
+    assert ok
+    assert_parity(outs[0], want, dim)
