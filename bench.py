@@ -75,6 +75,10 @@ WORKLOADS = {
     # pageable host arrays, so each call copies K and V over PCIe (the rate
     # that includes the copies, never the headline)
     "decode_32k_host": (16, 8, 256, 1, 32768, True, 0, 32767, "host", False),
+    # the same call as the engine fans one position out over its workers
+    # (src/engine/attention.rs:755-777): 16 concurrent calls of one query
+    # head each, each copying only the KV head it reads
+    "decode_32k_host_fanout": (16, 8, 256, 1, 32768, True, 0, 32767, "host", False),
 }
 HEADLINE = "decode_32k"
 # the metric's second half: f32 prefill attention at 4K tokens (the global
@@ -248,12 +252,25 @@ def time_host_workload(torch, pcl, name, steps, warmup, seed):
     lib = pcl.load()
     fptr = ctypes.POINTER(ctypes.c_float)
 
-    def call():
+    fanout = name.endswith("_fanout")
+
+    def one(h0, h1):
         # all keys allowed: the decode position is the last key (no mask)
         if not lib.pcl_hip_attention_f32_heads(
                 hq.ctypes.data_as(fptr), hk.ctypes.data_as(fptr), hv.ctypes.data_as(fptr),
-                qh, kvh, dim, nkeys, None, None, out.ctypes.data_as(fptr), 0, qh):
+                qh, kvh, dim, nkeys, None, None,
+                out[h0 * dim:].ctypes.data_as(fptr), h0, h1):
             raise RuntimeError("pcl_hip_attention_f32_heads failed for %s" % name)
+
+    if fanout:
+        import concurrent.futures
+        pool = concurrent.futures.ThreadPoolExecutor(qh)
+
+        def call():
+            list(pool.map(lambda h: one(h, h + 1), range(qh)))
+    else:
+        def call():
+            one(0, qh)
 
     for _ in range(max(warmup, 1)):
         call()
@@ -261,6 +278,8 @@ def time_host_workload(torch, pcl, name, steps, warmup, seed):
     for _ in range(steps):
         call()
     wall = (time.perf_counter() - t0) * 1e3 / steps
+    if fanout:
+        pool.shutdown()
     roles = {"stream_ms": 0.0, "combine_ms": 0.0}
     return wall, wall, "host+auto", {"q": torch.from_numpy(hq)}, roles, 1
 

@@ -500,61 +500,126 @@ void *stage_buffer(pcl_context *ctx, int slot, size_t bytes)
     return ctx->stage[slot];
 }
 
-// Copy inputs to the device, run, copy the output rows back.
+// The full K/V upload the host-pointer entries share: the engine runs one
+// position's heads as concurrent calls from its workers, one head range
+// each, over the same read-only K and V (src/engine/attention.rs:755-777).
+// A call registers for its (keys, values, length) before it queues for the
+// device; while any registered call of that key is pending, the upload
+// stays valid, so the fan-out copies K and V once. Once the last of them
+// returns, the entry is dropped (the caller may then rewrite the buffers).
+// A call whose keys differ from an entry still in use copies privately.
+struct HostUpload {
+    const float *keys = nullptr, *values = nullptr;
+    size_t kv_floats = 0;
+    int users = 0;      // registered calls not yet returned
+    bool valid = false; // the shared staging buffers hold this key's K and V
+};
+std::mutex g_upload_mutex;
+HostUpload g_upload;
+
+enum StageSlot { kStageQ, kStageK, kStageV, kStageMask, kStageOut, kStageKOwn, kStageVOwn };
+
+// Copy the inputs to the device (K and V through the shared upload when
+// possible), run, copy the output rows back. query: nq rows of q_floats
+// (device stride q_stride); h_lo / h_hi / h_base: the written query heads and
+// the output's first head.
 bool run_host(const float *query, size_t q_floats, const float *keys, const float *values,
               size_t kv_floats, const uint8_t *allowed, size_t mask_bytes,
               pcl_attention_desc d, int64_t h_lo, int64_t h_hi, int64_t h_base, float *out,
               size_t out_rows, size_t out_row_floats, size_t out_pitch_floats)
 {
-    std::lock_guard<std::mutex> lock(g_abi_mutex);
-    pcl_context *ctx = abi_context();
-    if (!ctx)
-        return false;
-    (void)hipSetDevice(ctx->device);
-    float *dq = static_cast<float *>(stage_buffer(ctx, 0, q_floats * sizeof(float)));
-    float *dk = static_cast<float *>(stage_buffer(ctx, 1, kv_floats * sizeof(float)));
-    float *dv = static_cast<float *>(stage_buffer(ctx, 2, kv_floats * sizeof(float)));
-    uint8_t *dm = allowed ? static_cast<uint8_t *>(stage_buffer(ctx, 3, mask_bytes)) : nullptr;
-    float *dout = static_cast<float *>(
-        stage_buffer(ctx, 4, out_rows * out_pitch_floats * sizeof(float)));
-    if (!dq || !dk || !dv || (allowed && !dm) || !dout)
-        return false;
-    hipError_t e = hipMemcpyAsync(dq, query, q_floats * sizeof(float), hipMemcpyHostToDevice,
-                                  ctx->stream);
-    if (e == hipSuccess)
-        e = hipMemcpyAsync(dk, keys, kv_floats * sizeof(float), hipMemcpyHostToDevice,
-                           ctx->stream);
-    if (e == hipSuccess)
-        e = hipMemcpyAsync(dv, values, kv_floats * sizeof(float), hipMemcpyHostToDevice,
-                           ctx->stream);
-    if (e == hipSuccess && allowed)
-        e = hipMemcpyAsync(dm, allowed, mask_bytes, hipMemcpyHostToDevice, ctx->stream);
-    if (e != hipSuccess) {
-        report("host to device copy", e);
-        return false;
+    bool shared = false;
+    {
+        std::lock_guard<std::mutex> lock(g_upload_mutex);
+        HostUpload &u = g_upload;
+        if (u.users > 0 && u.keys == keys && u.values == values && u.kv_floats == kv_floats) {
+            ++u.users;
+            shared = true;
+        } else if (u.users == 0) {
+            u.keys = keys;
+            u.values = values;
+            u.kv_floats = kv_floats;
+            u.valid = false;
+            u.users = 1;
+            shared = true;
+        }
     }
-    d.q = dq;
-    d.k0 = dk;
-    d.v0 = dv;
-    d.mask = dm;
-    d.out = dout;
-    d.o_stride = (int64_t)out_pitch_floats;
-    Plan plan;
-    if (make_plan(d, h_lo, h_hi, h_base, &plan) != PCL_OK)
-        return false;
-    if (run_plan(ctx, plan) != PCL_OK)
-        return false;
-    e = hipMemcpy2DAsync(out, out_pitch_floats * sizeof(float), dout,
-                         out_pitch_floats * sizeof(float), out_row_floats * sizeof(float),
-                         out_rows, hipMemcpyDeviceToHost, ctx->stream);
-    if (e != hipSuccess) {
-        report("device to host copy", e);
-        return false;
+    bool ok = false;
+    {
+        std::lock_guard<std::mutex> lock(g_abi_mutex);
+        ok = [&]() {
+            pcl_context *ctx = abi_context();
+            if (!ctx)
+                return false;
+            (void)hipSetDevice(ctx->device);
+            const size_t kv_bytes = kv_floats * sizeof(float);
+            float *dq = static_cast<float *>(stage_buffer(ctx, kStageQ, q_floats * sizeof(float)));
+            uint8_t *dm =
+                allowed ? static_cast<uint8_t *>(stage_buffer(ctx, kStageMask, mask_bytes)) : nullptr;
+            float *dout = static_cast<float *>(
+                stage_buffer(ctx, kStageOut, out_rows * out_pitch_floats * sizeof(float)));
+            bool upload = true;
+            if (shared) {
+                std::lock_guard<std::mutex> ul(g_upload_mutex);
+                upload = !g_upload.valid;
+            }
+            // the shared buffers are only grown (reallocated) by the call
+            // that uploads into them, which no other pending call relies on
+            float *dk = static_cast<float *>(
+                shared && !upload ? ctx->stage[kStageK]
+                                  : stage_buffer(ctx, shared ? kStageK : kStageKOwn, kv_bytes));
+            float *dv = static_cast<float *>(
+                shared && !upload ? ctx->stage[kStageV]
+                                  : stage_buffer(ctx, shared ? kStageV : kStageVOwn, kv_bytes));
+            if (!dq || !dk || !dv || (allowed && !dm) || !dout)
+                return false;
+            hipError_t e = hipMemcpyAsync(dq, query, q_floats * sizeof(float),
+                                          hipMemcpyHostToDevice, ctx->stream);
+            if (e == hipSuccess && upload)
+                e = hipMemcpyAsync(dk, keys, kv_bytes, hipMemcpyHostToDevice, ctx->stream);
+            if (e == hipSuccess && upload)
+                e = hipMemcpyAsync(dv, values, kv_bytes, hipMemcpyHostToDevice, ctx->stream);
+            if (e == hipSuccess && allowed)
+                e = hipMemcpyAsync(dm, allowed, mask_bytes, hipMemcpyHostToDevice, ctx->stream);
+            if (e != hipSuccess) {
+                report("host to device copy", e);
+                return false;
+            }
+            if (shared && upload) {
+                // later calls of this key run after the copies on this stream
+                std::lock_guard<std::mutex> ul(g_upload_mutex);
+                g_upload.valid = true;
+            }
+            d.q = dq;
+            d.k0 = dk;
+            d.v0 = dv;
+            d.mask = dm;
+            d.out = dout;
+            d.o_stride = (int64_t)out_pitch_floats;
+            Plan plan;
+            if (make_plan(d, h_lo, h_hi, h_base, &plan) != PCL_OK)
+                return false;
+            if (run_plan(ctx, plan) != PCL_OK)
+                return false;
+            e = hipMemcpy2DAsync(out, out_pitch_floats * sizeof(float), dout,
+                                 out_pitch_floats * sizeof(float), out_row_floats * sizeof(float),
+                                 out_rows, hipMemcpyDeviceToHost, ctx->stream);
+            if (e != hipSuccess) {
+                report("device to host copy", e);
+                return false;
+            }
+            int derr = 0;
+            if (pcl_context_sync(ctx, &derr) != PCL_OK)
+                return false;
+            return derr == 0;
+        }();
     }
-    int derr = 0;
-    if (pcl_context_sync(ctx, &derr) != PCL_OK)
-        return false;
-    return derr == 0;
+    if (shared) {
+        std::lock_guard<std::mutex> lock(g_upload_mutex);
+        if (--g_upload.users == 0)
+            g_upload.valid = false;
+    }
+    return ok;
 }
 
 bool all_finite(const float *x, size_t n)
@@ -637,7 +702,7 @@ void pcl_context_destroy(pcl_context *ctx)
     }
     for (hipEvent_t e : ctx->free_events)
         (void)hipEventDestroy(e);
-    for (int i = 0; i < 5; ++i)
+    for (int i = 0; i < kStageSlots; ++i)
         if (ctx->stage[i])
             (void)hipFree(ctx->stage[i]);
     if (ctx->ws)

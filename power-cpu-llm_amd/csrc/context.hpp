@@ -13,6 +13,8 @@ struct TimedSpan {
     int role;
 };
 
+constexpr int kStageSlots = 7;
+
 struct pcl_context {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -22,9 +24,10 @@ struct pcl_context {
     int *err = nullptr;
     // this device's scratch of pcl_attention_launch_noalloc (never freed)
     void *noalloc_scratch = nullptr;
-    // Staging buffers of the host-pointer entries (grow-only).
-    void *stage[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
-    size_t stage_bytes[5] = {0, 0, 0, 0, 0};
+    // Staging buffers of the host-pointer entries (grow-only): Q, the shared
+    // K and V upload, the mask, the output, a private K and V.
+    void *stage[kStageSlots] = {};
+    size_t stage_bytes[kStageSlots] = {};
     // per-kernel timing: recorded spans and a pool of free events
     bool timing = false;
     std::vector<TimedSpan> spans;

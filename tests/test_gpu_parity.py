@@ -127,6 +127,34 @@ def test_attention_head_ranges_match_full_attention(kernels, oracle):
                 kernels.attention_heads(query, keys, values, kvh, dim, allowed, (0, qheads + 1))
 
 
+def test_concurrent_head_range_calls_share_one_upload_and_see_rewrites(kernels, oracle):
+    # the engine's fan-out of one position (src/engine/attention.rs:755-777):
+    # concurrent calls, one query head each, over the same read-only K/V;
+    # every head equals the full call bitwise, and after the calls return a
+    # rewrite of the same buffers is seen by the next fan-out
+    import concurrent.futures
+    qheads, kvh, dim, nkeys = 16, 8, 256, 3000
+    g = np.random.default_rng(0xFA11)
+    q = prescale(g.standard_normal(qheads * dim, dtype=np.float32), dim)
+    k = g.standard_normal(nkeys * kvh * dim, dtype=np.float32)
+    v = g.standard_normal(nkeys * kvh * dim, dtype=np.float32)
+    pool = concurrent.futures.ThreadPoolExecutor(qheads)
+    for rewrite in range(3):
+        if rewrite:
+            k[:] = g.standard_normal(k.size, dtype=np.float32)  # same buffers, new contents
+            v[:] = g.standard_normal(v.size, dtype=np.float32)
+        full = kernels.attention(q, k, v, kvh, dim, None)
+        parts = list(pool.map(
+            lambda h: kernels.attention_heads(q, k, v, kvh, dim, None, (h, h + 1)),
+            range(qheads)))
+        got = np.concatenate(parts)
+        assert np.array_equal(bits(got), bits(full)), rewrite
+        ok, want = oracle.heads(q, k, v, qheads, kvh, dim, nkeys)
+        assert ok
+        assert_parity(got, want, dim)
+    pool.shutdown()
+
+
 def test_attention_multi_matches_single_queries(kernels):
     # int8/tests.rs:661-706
     rng = Rng(0x51ed270b)
