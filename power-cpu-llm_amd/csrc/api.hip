@@ -15,7 +15,7 @@ namespace pcl {
 hipError_t launch_split_kv(const Params &p, hipStream_t stream);
 hipError_t launch_combine(const Params &p, hipStream_t stream);
 hipError_t launch_pipe_kv(const Params &p, hipStream_t stream);
-hipError_t launch_tiled(const Params &p, int split, hipStream_t stream);
+hipError_t launch_tiled(const Params &p, int split, hipStream_t stream, bool *merged);
 hipError_t launch_two_pass(const Params &p, hipStream_t stream);
 hipError_t launch_spread_kv(const Params &p, hipStream_t stream);
 int tiled_rows(int dk);
@@ -377,7 +377,7 @@ int run_plan_ws(pcl_context *ctx, Plan &plan, float *ws)
         }
     }
     hipError_t e = hipSuccess;
-    const bool combine = plan.kernel == PCL_KERNEL_TILED_SPLIT ||
+    bool combine = plan.kernel == PCL_KERNEL_TILED_SPLIT ||
                          ((plan.kernel == PCL_KERNEL_SPLIT_KV || plan.kernel == PCL_KERNEL_PIPE_KV ||
                            plan.kernel == PCL_KERNEL_TWO_PASS ||
                            plan.kernel == PCL_KERNEL_SPREAD_KV) &&
@@ -393,12 +393,17 @@ int run_plan_ws(pcl_context *ctx, Plan &plan, float *ws)
     case PCL_KERNEL_TWO_PASS:
         e = pcl::launch_two_pass(p, ctx->stream);
         break;
-    case PCL_KERNEL_TILED:
-        e = pcl::launch_tiled(p, 0, ctx->stream);
+    case PCL_KERNEL_TILED: {
+        bool merged = false;
+        e = pcl::launch_tiled(p, 0, ctx->stream, &merged);
         break;
-    case PCL_KERNEL_TILED_SPLIT:
-        e = pcl::launch_tiled(p, 1, ctx->stream);
+    }
+    case PCL_KERNEL_TILED_SPLIT: {
+        bool merged = false;
+        e = pcl::launch_tiled(p, 1, ctx->stream, &merged);
+        combine = !merged;
         break;
+    }
     case PCL_KERNEL_SPREAD_KV:
         e = pcl::launch_spread_kv(p, ctx->stream);
         break;

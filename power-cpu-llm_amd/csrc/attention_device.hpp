@@ -380,6 +380,41 @@ __device__ __forceinline__ void merge_into4(Merged4 &s, float m, float l, f4 o)
     s.M = f.m;
 }
 
+typedef float f2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f2 ldg2(const float *p)
+{
+    return *(const __attribute__((address_space(1))) f2 *)p;
+}
+
+// The ordered merge of chunks [c0, c1) of one span (launch-relative chunk
+// indices) for four consecutive dims of one row (slot0: the row's first
+// chunk slot), as the combine kernels run it: one batch of loads over the
+// span's kSpanChunks slots (slots past c1 re-read chunk c0 and merge as
+// empty parts, which leave the state bit-unchanged), merged into
+// (-inf, 0, 0) in ascending order.
+__device__ __forceinline__ Merged4 merge_chunks4(const Params &p, int64_t slot0, int d, int c0,
+                                                 int c1)
+{
+    f2 ml[kSpanChunks];
+    f4 ov[kSpanChunks];
+#pragma unroll
+    for (int i = 0; i < kSpanChunks; ++i) {
+        const int64_t cc = slot0 + (c0 + i < c1 ? c0 + i : c0);
+        ml[i] = ldg2(p.ws_ml + 2 * cc);
+        ov[i] = ldg4(p.ws_o + cc * p.dk + d);
+    }
+    Merged4 s = {kNegInf, 0.f, f4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int i = 0; i < kSpanChunks; ++i) {
+        // chunks past the span merge as empty parts (no-ops)
+        const bool in = c0 + i < c1;
+        merge_into4(s, in ? ml[i].x : kNegInf, in ? ml[i].y : 0.f,
+                    in ? ov[i] : f4{0.f, 0.f, 0.f, 0.f});
+    }
+    return s;
+}
+
 // True when any allowed score of the lane is not finite.
 __device__ __forceinline__ bool bad_scores(const float s[2][4], const bool ok[2][4])
 {

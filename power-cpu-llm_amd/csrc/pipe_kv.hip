@@ -444,8 +444,13 @@ __device__ __forceinline__ void score_wave_dual(const Params &p, int unit, int k
     __syncthreads(); // chunk maximum handed over
 }
 
-// Output modes of the pipelined kernel.
-enum PipeMode { kDirect = 0, kPartial = 1 };
+// Output modes of the pipelined kernel: the output of a launch's only
+// chunk; a chunk partial for the combine kernel; or, for the last chunk of
+// a one-span chunk-split launch run after the chunks before it
+// (kMergeOut), the ordered merge of all the launch's chunk partials, this
+// chunk's from registers, into the output: the combine kernel's arithmetic
+// (split_kv.hip) without its launch.
+enum PipeMode { kDirect = 0, kPartial = 1, kMergeOut = 2 };
 
 template <int DK, int MODE, bool FULL, bool WIDE>
 __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, int c,
@@ -631,18 +636,53 @@ void pipe_kv_kernel(Params p, int c0)
     const int unit = blockIdx.y % p.units;
     const int kvl = blockIdx.y / p.units;
     const int wave = threadIdx.x >> 6;
+    // the value waves write a chunk partial in both partial modes
+    constexpr int VMODE = MODE == kMergeOut ? kPartial : MODE;
     if constexpr (pipe_score_waves<DK, WIDE>() == 1) {
         if (wave == 0)
             score_wave<DK, FULL>(p, unit, kvl, c, s);
         else
-            value_wave<DK, MODE, FULL, WIDE>(p, unit, kvl, c, s, wave - 1, ci);
+            value_wave<DK, VMODE, FULL, WIDE>(p, unit, kvl, c, s, wave - 1, ci);
     } else {
         if (wave == 0) {
             score_wave_dual<DK, FULL, 0, WIDE>(p, unit, kvl, c, s);
         } else if (wave == 1) {
             score_wave_dual<DK, FULL, 1, WIDE>(p, unit, kvl, c, s);
         } else {
-            value_wave<DK, MODE, FULL, WIDE>(p, unit, kvl, c, s, wave - 2, ci);
+            value_wave<DK, VMODE, FULL, WIDE>(p, unit, kvl, c, s, wave - 2, ci);
+        }
+    }
+    if constexpr (MODE == kMergeOut) {
+        // The unit's rows, merged by every thread of the workgroup, four
+        // consecutive dims of one row at a time: the launch's chunks (one
+        // span; this chunk's partial just written, the others by the launch
+        // before) in the combine kernel's order and arithmetic.
+        __syncthreads(); // this chunk's partials visible to the workgroup
+        const int q4 = p.dim / 4;
+        const int kh = p.kh_first + kvl;
+        for (int e = threadIdx.x; e < kRows * q4; e += blockDim.x) {
+            const int row = unit * kRows + e / q4;
+            const int d = 4 * (e % q4);
+            if (row >= p.nrows)
+                continue;
+            const int query = row / p.group;
+            const int h = kh * p.group + row % p.group;
+            if (h < p.h_lo || h >= p.h_hi)
+                continue;
+            const int64_t slot0 = ((int64_t)kvl * p.nrows_pad + row) * p.nch;
+            const Merged4 sv = merge_chunks4(p, slot0, d, 0, p.nch);
+            const MergeFactors f = merge_factors(kNegInf, sv.M);
+            const float L = merge_value(0.f, sv.L, f);
+            f4 v;
+            bool nonfinite = false;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[j] = merge_value(0.f, sv.acc[j], f) / L;
+                nonfinite |= !is_finite(v[j]);
+            }
+            stg4(p.out + (int64_t)query * p.o_stride + (int64_t)(h - p.h_base) * p.dim + d, v);
+            if (nonfinite)
+                atomicOr(p.err, kErrOutput);
         }
     }
 }
@@ -680,24 +720,30 @@ hipError_t launch_mode(const Params &p, int c0, int n, hipStream_t stream)
     return hipGetLastError();
 }
 
-template <bool FULL> hipError_t launch_full(const Params &p, int c0, int n, hipStream_t stream)
+template <bool FULL>
+hipError_t launch_full(const Params &p, int c0, int n, bool merge_out, hipStream_t stream)
 {
+    if (merge_out)
+        return launch_mode<kMergeOut, FULL>(p, c0, n, stream);
     return p.ws_o == nullptr ? launch_mode<kDirect, FULL>(p, c0, n, stream)
                              : launch_mode<kPartial, FULL>(p, c0, n, stream);
 }
 
 // Chunks [c0, c0 + n) of the launch, their partials in the launch's chunk
-// slots (the chunk-split prefill runs its last round's chunk this way).
-hipError_t launch_pipe_kv_chunks(const Params &p, int c0, int n, hipStream_t stream)
+// slots (the chunk-split prefill runs its last round's chunk this way); with
+// merge_out (n = 1, the launch's last chunk, one span, the earlier chunks'
+// partials already written) the merged output instead.
+hipError_t launch_pipe_kv_chunks(const Params &p, int c0, int n, bool merge_out,
+                                 hipStream_t stream)
 {
-    return p.dim == p.dk ? launch_full<true>(p, c0, n, stream)
-                         : launch_full<false>(p, c0, n, stream);
+    return p.dim == p.dk ? launch_full<true>(p, c0, n, merge_out, stream)
+                         : launch_full<false>(p, c0, n, merge_out, stream);
 }
 
 // Direct output for a single chunk, chunk partials otherwise.
 hipError_t launch_pipe_kv(const Params &p, hipStream_t stream)
 {
-    return launch_pipe_kv_chunks(p, 0, p.nch, stream);
+    return launch_pipe_kv_chunks(p, 0, p.nch, false, stream);
 }
 
 } // namespace pcl

@@ -499,36 +499,6 @@ hipError_t launch_split_kv(const Params &p, hipStream_t stream)
 // scatter over span lanes, and the slab kernel above (spans in LDS) is faster.
 constexpr int kCombineMaxSpans = 1;
 
-typedef float f2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ f2 ldg2(const float *p)
-{
-    return *(const __attribute__((address_space(1))) f2 *)p;
-}
-
-// Chunks [c0, c1) of the element group (slot0: the row's first chunk slot).
-__device__ __forceinline__ Merged4 merge_chunks4(const Params &p, int64_t slot0, int d, int c0,
-                                                 int c1)
-{
-    f2 ml[kSpanChunks];
-    f4 ov[kSpanChunks];
-#pragma unroll
-    for (int i = 0; i < kSpanChunks; ++i) {
-        const int64_t cc = slot0 + (c0 + i < c1 ? c0 + i : c0);
-        ml[i] = ldg2(p.ws_ml + 2 * cc);
-        ov[i] = ldg4(p.ws_o + cc * p.dk + d);
-    }
-    Merged4 s = {kNegInf, 0.f, f4{0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-    for (int i = 0; i < kSpanChunks; ++i) {
-        // chunks past the span merge as empty parts (no-ops)
-        const bool in = c0 + i < c1;
-        merge_into4(s, in ? ml[i].x : kNegInf, in ? ml[i].y : 0.f,
-                    in ? ov[i] : f4{0.f, 0.f, 0.f, 0.f});
-    }
-    return s;
-}
-
 __global__ __launch_bounds__(64) void combine_kernel(Params p, int span_lanes)
 {
     const int lane = threadIdx.x;

@@ -28,7 +28,8 @@
 
 namespace pcl {
 
-hipError_t launch_pipe_kv_chunks(const Params &p, int c0, int n, hipStream_t stream);
+hipError_t launch_pipe_kv_chunks(const Params &p, int c0, int n, bool merge_out,
+                                 hipStream_t stream);
 
 constexpr int kTiledWaves = 8;
 constexpr int kTiledRows = kTiledWaves * kRows; // 128
@@ -458,7 +459,8 @@ static int tail_chunks(const Params &p, int nqb, int cus)
     return 1;
 }
 
-template <int DK> static hipError_t launch_tiled_dk(const Params &p, int split, hipStream_t stream)
+template <int DK>
+static hipError_t launch_tiled_dk(const Params &p, int split, hipStream_t stream, bool *merged)
 {
     hipError_t e = configure_tiled<DK, kTiledWaves>();
     if (e != hipSuccess)
@@ -471,7 +473,13 @@ template <int DK> static hipError_t launch_tiled_dk(const Params &p, int split, 
     e = hipGetLastError();
     if (e != hipSuccess || !tail)
         return e;
-    return launch_pipe_kv_chunks(p, p.nch - tail, tail, stream);
+    // the tail runs after every other chunk's partial is written: with all
+    // chunks in one span it merges them into the output itself
+    const bool merge_out = p.nspan == 1;
+    e = launch_pipe_kv_chunks(p, p.nch - tail, tail, merge_out, stream);
+    if (e == hipSuccess && merge_out)
+        *merged = true;
+    return e;
 }
 
 hipError_t launch_tiled_wide(const Params &p, int split, hipStream_t stream);
@@ -483,12 +491,15 @@ int tiled_rows(int dk)
     return dk > 256 ? tiled_wide_rows() : kTiledRows;
 }
 
-hipError_t launch_tiled(const Params &p, int split, hipStream_t stream)
+// *merged: set when the launch itself wrote the merged output of a split
+// launch (no combine needed).
+hipError_t launch_tiled(const Params &p, int split, hipStream_t stream, bool *merged)
 {
+    *merged = false;
     switch (p.dk) {
-    case 64: return launch_tiled_dk<64>(p, split, stream);
-    case 128: return launch_tiled_dk<128>(p, split, stream);
-    case 256: return launch_tiled_dk<256>(p, split, stream);
+    case 64: return launch_tiled_dk<64>(p, split, stream, merged);
+    case 128: return launch_tiled_dk<128>(p, split, stream, merged);
+    case 256: return launch_tiled_dk<256>(p, split, stream, merged);
     case 512: return launch_tiled_wide(p, split, stream);
     default: return hipErrorInvalidValue;
     }
