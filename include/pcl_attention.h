@@ -130,6 +130,13 @@ enum pcl_kernel {
  *   otherwise    : every key (decoder/canvas mode, attention.rs:696-698).
  * The query is scaled by q_scale in f32 before the dot products, as the
  * engine's pre-scale (src/engine/nemotron/forward.rs:336-346); 1 = none.
+ * softcap: logit soft-cap, off when 0 (a zero-initialised descriptor). When
+ * > 0 every allowed score s becomes softcap * tanh(s / softcap) in f32 before
+ * the softmax (the form of p9_ref_softcap, src/kernels/portable/reference.rs:
+ * 226-235; the engine itself caps only its final logits, src/engine/text.rs:
+ * 963,979, so it leaves this off). An infinite score then becomes
+ * +-softcap; a NaN one is still an error. Negative, subnormal or non-finite
+ * values are PCL_INVALID_PARAMETER.
  * Output: query i, head h (kh_first*group <= h < kh_end*group) at
  * out + i*o_stride + (h - kh_first*group)*dim. */
 typedef struct pcl_attention_desc {
@@ -151,6 +158,7 @@ typedef struct pcl_attention_desc {
     float *out;
     int64_t o_stride;
     int32_t kernel; /* enum pcl_kernel */
+    float softcap;  /* 0 = off */
 } pcl_attention_desc;
 
 /* Create a context on a device that owns a new non-blocking stream. */

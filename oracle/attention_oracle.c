@@ -26,11 +26,13 @@
 /* glibc 2.28's POWER8 expf, restated below (the binary32 twin's softmax). */
 static float power8_expf(float x);
 
-/* p9_ref_attention_heads (src/kernels/portable/reference.rs:327-393). */
-bool oracle_ref_attention_heads(const float *query, const float *keys, const float *values,
-                                size_t qheads, size_t kvheads, size_t dim, size_t nkeys,
-                                const uint8_t *allowed, float *scratch, float *out,
-                                size_t h_first, size_t h_end)
+/* p9_ref_attention_heads (src/kernels/portable/reference.rs:327-393); with
+ * cap > 0, every score s first becomes f32(cap * tanh(f64(s) / cap)), the
+ * reference's p9_ref_softcap (reference.rs:226-235) applied to the scores. */
+static bool ref_heads(const float *query, const float *keys, const float *values,
+                      size_t qheads, size_t kvheads, size_t dim, size_t nkeys,
+                      const uint8_t *allowed, float *scratch, float *out, size_t h_first,
+                      size_t h_end, double cap)
 {
     if (h_first > h_end || h_end > qheads) /* reference.rs:341-343 */
         return false;
@@ -49,6 +51,8 @@ bool oracle_ref_attention_heads(const float *query, const float *keys, const flo
             for (size_t d = 0; d < dim; ++d)
                 score += (double)query[h * dim + d] * (double)keys[t * stride + kh * dim + d];
             scratch[t] = (float)score;
+            if (cap > 0.0)
+                scratch[t] = (float)(cap * tanh((double)scratch[t] / cap));
             if (!isfinite(scratch[t]))
                 return false;
             if (scratch[t] > max)
@@ -67,6 +71,27 @@ bool oracle_ref_attention_heads(const float *query, const float *keys, const flo
         }
     }
     return true;
+}
+
+bool oracle_ref_attention_heads(const float *query, const float *keys, const float *values,
+                                size_t qheads, size_t kvheads, size_t dim, size_t nkeys,
+                                const uint8_t *allowed, float *scratch, float *out,
+                                size_t h_first, size_t h_end)
+{
+    return ref_heads(query, keys, values, qheads, kvheads, dim, nkeys, allowed, scratch, out,
+                     h_first, h_end, 0.0);
+}
+
+bool oracle_ref_attention_heads_softcap(const float *query, const float *keys,
+                                        const float *values, size_t qheads, size_t kvheads,
+                                        size_t dim, size_t nkeys, const uint8_t *allowed,
+                                        float *scratch, float *out, size_t h_first,
+                                        size_t h_end, float softcap)
+{
+    if (!(softcap > 0.0f))
+        return false;
+    return ref_heads(query, keys, values, qheads, kvheads, dim, nkeys, allowed, scratch, out,
+                     h_first, h_end, (double)softcap);
 }
 
 /* oracle_ref_attention_heads restructured for speed where that cannot

@@ -35,6 +35,16 @@ bool oracle_ref_attention_heads(const float *query, const float *keys, const flo
                                 const uint8_t *allowed, float *scratch, float *out,
                                 size_t h_first, size_t h_end);
 
+/* The exact path with a logit soft-cap (softcap > 0): each score s becomes
+ * f32(softcap * tanh(f64(s) / softcap)) before the softmax, the form of
+ * p9_ref_softcap (src/kernels/portable/reference.rs:226-235). The reference
+ * applies no cap inside attention; this is the checker of the descriptor's
+ * optional softcap field. */
+bool oracle_ref_attention_heads_softcap(const float *query, const float *keys,
+                                        const float *values, size_t qheads, size_t kvheads,
+                                        size_t dim, size_t nkeys, const uint8_t *allowed,
+                                        float *scratch, float *out, size_t h_first,
+                                        size_t h_end, float softcap);
 /* a1 restructured for speed without changing a bit (masked keys left out of
  * the sums, interleaved score sums, key-outer P.V), for checking full-size
  * outputs; equal to oracle_ref_attention_heads whenever masked keys' value

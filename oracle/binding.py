@@ -49,6 +49,9 @@ def load():
     lib.oracle_ref_attention_heads_checker.restype = ctypes.c_bool
     lib.oracle_ref_attention_heads_checker.argtypes = [fp, fp, fp, sz, sz, sz, sz, u8p, fp, fp,
                                                        sz, sz]
+    lib.oracle_ref_attention_heads_softcap.restype = ctypes.c_bool
+    lib.oracle_ref_attention_heads_softcap.argtypes = [fp, fp, fp, sz, sz, sz, sz, u8p, fp, fp,
+                                                       sz, sz, ctypes.c_float]
     lib.oracle_threaded_attention_sample.restype = ctypes.c_bool
     lib.oracle_threaded_attention_sample.argtypes = [ctypes.c_int, ctypes.c_int, fp, sz, sz, fp,
                                                      fp, sz, sz, sz, sz, ctypes.c_int, sz, sz, sz,
@@ -79,19 +82,25 @@ def _mask(x):
 
 
 def heads(query, keys, values, qheads, kvheads, dim, nkeys, allowed=None, h_first=0,
-          h_end=None, binary32=False, checker=False):
+          h_end=None, binary32=False, checker=False, softcap=0.0):
     """p9_ref_attention_heads (exact), its bit-identical checker form
-    (checker=True) or pa_attention_f32_heads (binary32): returns
-    (ok, out[(h_end-h_first)*dim])."""
+    (checker=True), pa_attention_f32_heads (binary32) or the exact path with a
+    logit soft-cap (softcap > 0): returns (ok, out[(h_end-h_first)*dim])."""
     lib = load()
     h_end = qheads if h_end is None else h_end
     q, k, v, m = _f32(query), _f32(keys), _f32(values), _mask(allowed)
     scratch = np.zeros(max(nkeys, 1), np.float32)
     out = np.zeros(max((h_end - h_first) * dim, 1), np.float32)
-    fn = (lib.oracle_pa_attention_f32_heads if binary32 else
-          lib.oracle_ref_attention_heads_checker if checker else lib.oracle_ref_attention_heads)
-    ok = fn(_f(q), _f(k), _f(v), qheads, kvheads, dim, nkeys, _u(m), _f(scratch), _f(out),
-            h_first, h_end)
+    args = [_f(q), _f(k), _f(v), qheads, kvheads, dim, nkeys, _u(m), _f(scratch), _f(out),
+            h_first, h_end]
+    if softcap:
+        assert not (binary32 or checker)
+        ok = lib.oracle_ref_attention_heads_softcap(*args, softcap)
+    else:
+        fn = (lib.oracle_pa_attention_f32_heads if binary32 else
+              lib.oracle_ref_attention_heads_checker if checker else
+              lib.oracle_ref_attention_heads)
+        ok = fn(*args)
     return bool(ok), out[:max(h_end - h_first, 0) * dim]
 
 

@@ -105,7 +105,7 @@ class PclDesc(ctypes.Structure):
         ("first_key", ctypes.c_int64), ("first_query", ctypes.c_int64),
         ("q_scale", ctypes.c_float),
         ("out", ctypes.c_void_p), ("o_stride", ctypes.c_int64),
-        ("kernel", ctypes.c_int32),
+        ("kernel", ctypes.c_int32), ("softcap", ctypes.c_float),
     ]
 
 

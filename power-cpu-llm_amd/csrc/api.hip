@@ -172,6 +172,9 @@ int make_plan(const pcl_attention_desc &d, int64_t h_lo, int64_t h_hi, int64_t h
         return PCL_INVALID_SHAPE;
     if (d.kernel < PCL_KERNEL_AUTO || d.kernel > PCL_KERNEL_SPREAD_KV)
         return PCL_INVALID_PARAMETER;
+    if (!(d.softcap >= 0.0f) || !std::isfinite(d.softcap) ||
+        (d.softcap > 0.0f && !std::isnormal(d.softcap)))
+        return PCL_INVALID_PARAMETER; // negative, NaN, infinite or subnormal cap
     const int64_t group = d.qheads / d.kvheads;
     const int64_t nkeys = d.n0 + d.n1;
     const int64_t nkv = d.kh_end - d.kh_first;
@@ -207,6 +210,10 @@ int make_plan(const pcl_attention_desc &d, int64_t h_lo, int64_t h_hi, int64_t h
     p.q_stride = d.q_stride;
     p.nq = (int)d.nq;
     p.q_scale = d.q_scale;
+    if (d.softcap > 0.0f) {
+        p.softcap = d.softcap;
+        p.inv_softcap = 1.0f / d.softcap;
+    }
     if (d.n0 > 0) {
         p.k0 = d.k0;
         p.v0 = d.v0;

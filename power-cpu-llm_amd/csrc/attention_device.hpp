@@ -66,6 +66,8 @@ struct Params {
     int64_t q_stride;
     int nq;
     float q_scale;
+    // logit soft-cap (0 = off) and its f32 reciprocal
+    float softcap, inv_softcap;
     // keys/values: key t < n0 in segment 0, the rest in segment 1
     const float *k0, *v0;
     int64_t n0;
@@ -413,6 +415,36 @@ __device__ __forceinline__ Merged4 merge_chunks4(const Params &p, int64_t slot0,
                     in ? ov[i] : f4{0.f, 0.f, 0.f, 0.f});
     }
     return s;
+}
+
+// Logit soft-cap: cap * tanh(s / cap) in f32, one definition for every
+// kernel. tanh(t) is an odd Taylor polynomial through t^9 for |t| < 1/4
+// (truncation below 1e-8 relative) and (1 - e) / (1 + e) with e = exp(-2|t|)
+// above (relative error a few 1e-7), so a capped score is within about 1e-6
+// relative of the exact cap; +-inf becomes +-cap and NaN stays NaN.
+__device__ __forceinline__ float soft_cap(float s, float cap, float inv_cap)
+{
+    const float t = s * inv_cap;
+    const float a = fabsf(t);
+    const float t2 = t * t;
+    const float small =
+        t + t * t2 * (-0.333333333f + t2 * (0.133333333f + t2 * (-0.0539682540f +
+                                                                   t2 * 0.0218694885f)));
+    const float e = fexp(-2.0f * a);
+    const float large = copysignf((1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e), t);
+    return cap * (a < 0.25f ? small : large);
+}
+
+// Applies the descriptor's soft-cap (when on) to a tile's raw scores.
+__device__ __forceinline__ void cap_scores(const Params &p, float s[2][4])
+{
+    if (p.softcap > 0.0f) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                s[b][r] = soft_cap(s[b][r], p.softcap, p.inv_softcap);
+    }
 }
 
 // True when any allowed score of the lane is not finite.

@@ -228,6 +228,7 @@ __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, i
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     sc[b][r] = acc[b][r];
+            cap_scores(p, sc);
             bad |= bad_scores(sc, ok);
             const float mn = fmaxf(m, tile_max(sc, ok));
             const float ms = safe_max(mn);
@@ -414,6 +415,7 @@ __device__ __forceinline__ void score_wave_dual(const Params &p, int unit, int k
                 sc[0][r] = acc0[r];
                 sc[1][r] = s.sb[t & 1][r][lane];
             }
+            cap_scores(p, sc);
             bad |= bad_scores(sc, ok);
             const float mn = fmaxf(m, tile_max(sc, ok));
             const float ms = safe_max(mn);

@@ -197,6 +197,7 @@ __global__ __launch_bounds__(DK, SplitCfg<DK>::waves_per_eu) void split_kv_kerne
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     s[i][b][r] = acc[b][r];
+            cap_scores(p, s[i]);
             tm = tile_max(s[i], ok[i]);
             bad |= bad_scores(s[i], ok[i]);
         }

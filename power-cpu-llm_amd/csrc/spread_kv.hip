@@ -218,6 +218,7 @@ __global__ __launch_bounds__(64 * kSpreadWaves, 2) void spread_kv_kernel(Params 
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     sv[b][r] = slds[2 * t + b][r][lane];
+            cap_scores(p, sv);
             bad |= bad_scores(sv, ok);
             const float mn = fmaxf(m, tile_max(sv, ok));
             const float ms = safe_max(mn);

@@ -331,6 +331,7 @@ void tiled_kernel(Params p, int split, int z0)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     s[b][r] = acc[b][r];
+            cap_scores(p, s);
             bad |= bad_scores(s, ok);
             const float mn = fmaxf(m, tile_max(s, ok));
             const float ms = safe_max(mn);

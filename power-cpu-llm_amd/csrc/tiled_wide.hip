@@ -335,6 +335,7 @@ void tiled_wide_kernel(Params p, int split, int z0)
                 s[0][r] = s0[r];
                 s[1][r] = s1[r];
             }
+            cap_scores(p, s);
             if (half == 0)
                 bad |= bad_scores(s, ok);
             const float mn = fmaxf(m, tile_max(s, ok));

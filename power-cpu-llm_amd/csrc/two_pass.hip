@@ -237,6 +237,7 @@ __global__ __launch_bounds__(64 * value_waves<DK>()) void value_pass_kernel(Para
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     sc[b][r] = col < real ? sv[t][b][r] : 0.f;
+            cap_scores(p, sc);
             bad |= bad_scores(sc, ok);
             const float mn = fmaxf(m, tile_max(sc, ok));
             const float ms = safe_max(mn);

@@ -117,6 +117,14 @@ def test_descriptor_validation_on_the_host(pcl):
     d.kernel, d.dim, d.q_stride, d.o_stride = 0, 256, 16 * 256, 16 * 256
     d.dim = 24
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == -1
+    d.dim = 256
+    # the optional logit soft-cap: 0 (either sign) is off, a normal positive
+    # value is on; negative, subnormal and non-finite caps are rejected
+    for cap, valid in ((0.0, True), (-0.0, True), (30.0, True), (1e30, True), (-1.0, False),
+                       (1e-40, False), (float("inf"), False), (float("nan"), False)):
+        d.softcap = cap
+        assert (lib.pcl_attention_resolve_kernel(ctypes.byref(d)) != -1) == valid, cap
+    d.softcap = 0.0
     d.dim, d.nq, d.first_query, d.window, d.n0 = 256, 4096, 0, 0, 4096
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_TILED
     d.first_key = 5000  # no query sees a key

@@ -341,7 +341,7 @@ def test_raw_entries_report_bad_geometry(pcl):
 # ---- device descriptors: every kernel gives the same bits ------------------
 
 def run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel, causal=0, window=0, first_key=0,
-             first_query=0, mask=None, split_at=None, kv=None, q_scale=1.0):
+             first_query=0, mask=None, split_at=None, kv=None, q_scale=1.0, softcap=None):
     """One device launch over numpy inputs; returns (out, error flag)."""
     dev = torch.device("cuda:0")
     nq = q.shape[0]
@@ -355,6 +355,8 @@ def run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel, causal=0, window=0, 
               dim=dim, kh_first=kv[0], kh_end=kv[1], causal=causal, window=window,
               first_key=first_key, first_query=first_query, out=out.data_ptr(), o_stride=olen,
               kernel=kernel, q_scale=q_scale)
+    if softcap is not None:
+        kw["softcap"] = softcap
     keep = [tq, out]
     if split_at is None:
         tk = torch.from_numpy(np.ascontiguousarray(k)).to(dev)
@@ -422,6 +424,66 @@ def test_every_kernel_gives_identical_bits(torch, ctx, oracle, case):
         ok, want = oracle.heads(q[i], k, v, qheads, kvh, dim, nkeys, m)
         assert ok
         assert_parity(outs[1][i], want, dim)
+
+
+SOFTCAP_CASES = [
+    # qheads, kvh, dim, nq, nkeys, causal, window, first_query
+    (16, 8, 256, 1, 2048, 1, 0, 2047),      # short decode (spread under AUTO)
+    (16, 8, 256, 1, 9000, 1, 0, 8999),      # pipelined decode, two spans
+    (16, 2, 512, 1, 3000, 1, 0, 2999),      # head dim 512 decode
+    (16, 8, 256, 300, 300, 1, 0, 0),        # tiled prefill
+    (16, 8, 128, 256, 2304, 1, 700, 2048),  # chunk-split launch with its tail
+    (16, 2, 512, 100, 700, 1, 0, 600),      # wave-pair tiled kernel
+]
+
+
+@pytest.mark.parametrize("cap", [4.0, 1.5])
+@pytest.mark.parametrize("case", SOFTCAP_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_softcap_every_kernel_identical_and_matches_the_oracle(torch, ctx, oracle, case, cap):
+    # the descriptor's optional logit soft-cap: every kernel applies the same
+    # f32 cap to the raw scores (bitwise equal results), within the contract
+    # of the oracle's exact path with the f64 cap, and the cap takes effect
+    qheads, kvh, dim, nq, nkeys, causal, window, fq = case
+    g = np.random.default_rng(sum(case) + int(cap * 10))
+    q = prescale(g.standard_normal((nq, qheads * dim), dtype=np.float32), dim) * np.float32(2.0)
+    k = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+    v = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+    outs = {}
+    for kernel in (0, 1, 2, 3, 4, 5, 6):
+        outs[kernel], err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel, causal,
+                                     window, 0, fq, softcap=cap)
+        assert err == 0
+    for kernel in (1, 2, 3, 4, 5, 6):
+        assert np.array_equal(bits(outs[0]), bits(outs[kernel])), kernel
+    plain, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, 0, causal, window, 0, fq)
+    assert err == 0 and np.max(np.abs(plain - outs[0])) > 1e-3
+    for i in sorted({0, nq // 2, nq - 1}):
+        m = oracle.encoder_mask(0, nkeys, fq + i, window or None) if causal else None
+        ok, want = oracle.heads(q[i], k, v, qheads, kvh, dim, nkeys, m, softcap=cap)
+        assert ok
+        assert_parity(outs[0][i], want, dim)
+
+
+def test_softcap_off_is_bitwise_inert(torch, ctx):
+    # 0 and -0 are off: the same bits as a descriptor that never set the
+    # field, for every kernel; a huge cap stays within rounding of off
+    for case in (SOFTCAP_CASES[0], SOFTCAP_CASES[3], SOFTCAP_CASES[5]):
+        qheads, kvh, dim, nq, nkeys, causal, window, fq = case
+        g = np.random.default_rng(sum(case))
+        q = prescale(g.standard_normal((nq, qheads * dim), dtype=np.float32), dim)
+        k = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+        v = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+        for kernel in (0, 4, 6, 2):
+            base, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel, causal, window,
+                                 0, fq)
+            assert err == 0
+            for cap in (0.0, -0.0):
+                got, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel, causal,
+                                    window, 0, fq, softcap=cap)
+                assert err == 0 and np.array_equal(bits(got), bits(base)), (kernel, cap)
+            huge, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel, causal, window,
+                                 0, fq, softcap=1e30)
+            assert err == 0 and np.max(np.abs(huge - base)) < 1e-6, kernel
 
 
 def test_split_launch_tail_with_masks_segments_and_kv_ranges(torch, ctx, oracle):

@@ -349,6 +349,61 @@ def test_non_finite_inputs_are_errors(oracle):
     assert not oracle.heads(q, bad_k, v, qheads, kvh, dim, nkeys, binary32=True)[0]
 
 
+def test_softcap_oracle_reduces_to_the_exact_path_for_a_huge_cap(oracle):
+    # cap * tanh(s / cap) = s to far below an f32 ulp when s / cap is tiny, so
+    # a cap of 1e30 must leave every bit of the exact path (a misplaced cap,
+    # s * cap inside tanh, or a cap applied after the softmax all fail)
+    rng = np.random.default_rng(41)
+    qheads, kvh, dim, nkeys = 8, 2, 64, 300
+    q = (rng.standard_normal(qheads * dim) * 0.5).astype(np.float32)
+    k = rng.standard_normal(nkeys * kvh * dim).astype(np.float32)
+    v = rng.standard_normal(nkeys * kvh * dim).astype(np.float32)
+    mask = oracle.encoder_mask(0, nkeys, 250, 100)
+    ok, plain = oracle.heads(q, k, v, qheads, kvh, dim, nkeys, mask)
+    ok2, capped = oracle.heads(q, k, v, qheads, kvh, dim, nkeys, mask, softcap=1e30)
+    assert ok and ok2
+    assert np.array_equal(plain.view(np.uint32), capped.view(np.uint32))
+    # and a moderate cap changes results
+    ok3, cap4 = oracle.heads(q, k, v, qheads, kvh, dim, nkeys, mask, softcap=4.0)
+    assert ok3 and not np.array_equal(plain, cap4)
+
+
+def test_softcap_oracle_two_key_sigmoid_closed_form(oracle):
+    # two keys with scores +a and -a: the output is sigma(c1 - c2) v1 +
+    # sigma(c2 - c1) v2 with c = cap tanh(s / cap), a different formula from
+    # the oracle's softmax; capped and uncapped weights differ visibly
+    dim = 16
+    for a, cap in ((3.0, 2.0), (0.5, 30.0), (7.0, 0.75)):
+        q = np.zeros(dim, np.float32)
+        q[0] = a
+        k = np.zeros((2, dim), np.float32)
+        k[0, 0], k[1, 0] = 1.0, -1.0
+        v = np.zeros((2, dim), np.float32)
+        v[0, 1], v[1, 1] = 5.0, -3.0
+        v[0, 2] = 1.0
+        ok, y = oracle.heads(q, k, v, 1, 1, dim, 2, softcap=cap)
+        assert ok
+        c1 = cap * math.tanh(a / cap)
+        w1 = 1.0 / (1.0 + math.exp(-2.0 * c1))
+        assert abs(float(y[1]) - (5.0 * w1 - 3.0 * (1.0 - w1))) < 2e-6
+        assert abs(float(y[2]) - w1) < 1e-6
+        assert y[0] == 0.0
+
+
+def test_softcap_oracle_saturates_to_the_mean_of_values(oracle):
+    # a tiny cap maps every score of 10 caps or more to the same f32 value, so
+    # the weights are exactly uniform: the output is the mean of the values
+    rng = np.random.default_rng(5)
+    dim, nkeys, cap = 32, 37, 0.01
+    k = np.abs(rng.standard_normal((nkeys, dim))).astype(np.float32) + 0.5
+    q = np.full(dim, 1.0, np.float32)  # every score >= 16 >> 10 caps
+    v = rng.standard_normal((nkeys, dim)).astype(np.float32)
+    ok, y = oracle.heads(q, k, v, 1, 1, dim, nkeys, softcap=cap)
+    assert ok
+    assert np.max(np.abs(y - v.astype(np.float64).mean(axis=0))) < 1e-6
+    assert not oracle.heads(q, k, v, 1, 1, dim, nkeys, softcap=-1.0)[0]
+
+
 def test_c_xorshift_stream_equals_the_python_generator(oracle):
     # The reference tests' generator (int8/tests.rs:15-33), whose Python form
     # follows it line by line; the C form feeds the large GPU cases.
