@@ -436,9 +436,12 @@ __device__ __forceinline__ float soft_cap(float s, float cap, float inv_cap)
 }
 
 // Applies the descriptor's soft-cap (when on) to a tile's raw scores.
+// Kernels instantiated per cap setting pass CAP = false for launches without
+// a cap, which removes the code; the others test the launch at run time.
+template <bool CAP = true>
 __device__ __forceinline__ void cap_scores(const Params &p, float s[2][4])
 {
-    if (p.softcap > 0.0f) {
+    if (CAP && p.softcap > 0.0f) {
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll

@@ -58,7 +58,7 @@ __device__ __forceinline__ uint64_t take(const uint64_t *p)
 }
 
 
-template <int DK, bool FULL>
+template <int DK, bool FULL, bool CAP>
 __global__ __launch_bounds__(64 * kSpreadWaves, 2) void spread_kv_kernel(Params p)
 {
     constexpr int S = DK / kSpreadSliceDims;                  // workgroups per item
@@ -218,7 +218,7 @@ __global__ __launch_bounds__(64 * kSpreadWaves, 2) void spread_kv_kernel(Params 
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     sv[b][r] = slds[2 * t + b][r][lane];
-            cap_scores(p, sv);
+            cap_scores<CAP>(p, sv);
             bad |= bad_scores(sv, ok);
             const float mn = fmaxf(m, tile_max(sv, ok));
             const float ms = safe_max(mn);
@@ -299,15 +299,21 @@ int spread_slices(int dk)
     return dk / kSpreadSliceDims;
 }
 
-template <int DK>
-static hipError_t launch_dk(const Params &p, hipStream_t stream)
+template <int DK, bool CAP>
+static hipError_t launch_cap(const Params &p, hipStream_t stream)
 {
     const dim3 grid(DK / kSpreadSliceDims, p.nch, p.nkv * p.units);
     if (p.dim == DK)
-        spread_kv_kernel<DK, true><<<grid, 64 * kSpreadWaves, 0, stream>>>(p);
+        spread_kv_kernel<DK, true, CAP><<<grid, 64 * kSpreadWaves, 0, stream>>>(p);
     else
-        spread_kv_kernel<DK, false><<<grid, 64 * kSpreadWaves, 0, stream>>>(p);
+        spread_kv_kernel<DK, false, CAP><<<grid, 64 * kSpreadWaves, 0, stream>>>(p);
     return hipGetLastError();
+}
+
+template <int DK>
+static hipError_t launch_dk(const Params &p, hipStream_t stream)
+{
+    return p.softcap > 0.0f ? launch_cap<DK, true>(p, stream) : launch_cap<DK, false>(p, stream);
 }
 
 hipError_t launch_spread_kv(const Params &p, hipStream_t stream)

@@ -70,7 +70,7 @@ __device__ __forceinline__ bool tile_whole(const Params &p, int row_lo, int row_
 // One workgroup per CU (its K/V stages fill the LDS), so at most two waves
 // per SIMD: each wave may hold 256 VGPRs, which the operand double-buffering
 // below uses. W waves per workgroup, one 16-row unit each.
-template <int DK, int W>
+template <int DK, int W, bool CAP>
 __global__ __launch_bounds__(64 * W, 2) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void tiled_kernel(Params p, int split, int z0)
 {
@@ -331,7 +331,7 @@ void tiled_kernel(Params p, int split, int z0)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     s[b][r] = acc[b][r];
-            cap_scores(p, s);
+            cap_scores<CAP>(p, s);
             bad |= bad_scores(s, ok);
             const float mn = fmaxf(m, tile_max(s, ok));
             const float ms = safe_max(mn);
@@ -425,7 +425,7 @@ static int device_cus()
 
 // Dynamic LDS above 64 KiB must be allowed once per kernel and device; a
 // repeated call from a racing thread is harmless.
-template <int DK, int W> static hipError_t configure_tiled()
+template <int DK, int W, bool CAP> static hipError_t configure_tiled()
 {
     static std::atomic<bool> configured[kMaxDevices];
     int dev = 0;
@@ -435,7 +435,7 @@ template <int DK, int W> static hipError_t configure_tiled()
     if (dev < 0 || dev >= kMaxDevices)
         return hipErrorInvalidDevice;
     if (!configured[dev].load(std::memory_order_acquire)) {
-        e = hipFuncSetAttribute((const void *)tiled_kernel<DK, W>,
+        e = hipFuncSetAttribute((const void *)tiled_kernel<DK, W, CAP>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)TiledLds<DK>::bytes);
         if (e != hipSuccess)
@@ -460,18 +460,25 @@ static int tail_chunks(const Params &p, int nqb, int cus)
     return 1;
 }
 
+template <int DK, bool CAP>
+static hipError_t launch_tiled_grid(const Params &p, int split, dim3 grid, hipStream_t stream)
+{
+    const hipError_t e = configure_tiled<DK, kTiledWaves, CAP>();
+    if (e != hipSuccess)
+        return e;
+    tiled_kernel<DK, kTiledWaves, CAP>
+        <<<grid, 64 * kTiledWaves, TiledLds<DK>::bytes, stream>>>(p, split, 0);
+    return hipGetLastError();
+}
+
 template <int DK>
 static hipError_t launch_tiled_dk(const Params &p, int split, hipStream_t stream, bool *merged)
 {
-    hipError_t e = configure_tiled<DK, kTiledWaves>();
-    if (e != hipSuccess)
-        return e;
     const int nqb = (p.nrows + kTiledRows - 1) / kTiledRows;
     const int tail = split ? tail_chunks(p, nqb, device_cus()) : 0;
     const dim3 grid(nqb * p.nkv, 1, split ? p.nch - tail : 1);
-    tiled_kernel<DK, kTiledWaves>
-        <<<grid, 64 * kTiledWaves, TiledLds<DK>::bytes, stream>>>(p, split, 0);
-    e = hipGetLastError();
+    hipError_t e = p.softcap > 0.0f ? launch_tiled_grid<DK, true>(p, split, grid, stream)
+                                    : launch_tiled_grid<DK, false>(p, split, grid, stream);
     if (e != hipSuccess || !tail)
         return e;
     // the tail runs after every other chunk's partial is written: with all

@@ -64,6 +64,7 @@ __device__ __forceinline__ bool wide_tile_whole(const Params &p, int row_lo, int
     return kmax <= qlo && (p.window == 0 || qhi - kmin < p.window);
 }
 
+template <bool CAP>
 __global__ __launch_bounds__(64 * kWideWaves, 2) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void tiled_wide_kernel(Params p, int split, int z0)
 {
@@ -335,7 +336,7 @@ void tiled_wide_kernel(Params p, int split, int z0)
                 s[0][r] = s0[r];
                 s[1][r] = s1[r];
             }
-            cap_scores(p, s);
+            cap_scores<CAP>(p, s);
             if (half == 0)
                 bad |= bad_scores(s, ok);
             const float mn = fmaxf(m, tile_max(s, ok));
@@ -422,7 +423,8 @@ void tiled_wide_kernel(Params p, int split, int z0)
 constexpr int kWideMaxDevices = 64;
 
 
-hipError_t launch_tiled_wide(const Params &p, int split, hipStream_t stream)
+template <bool CAP>
+static hipError_t launch_wide(const Params &p, int split, hipStream_t stream)
 {
     static std::atomic<bool> configured[kWideMaxDevices];
     int dev = 0;
@@ -432,7 +434,7 @@ hipError_t launch_tiled_wide(const Params &p, int split, hipStream_t stream)
     if (dev < 0 || dev >= kWideMaxDevices)
         return hipErrorInvalidDevice;
     if (!configured[dev].load(std::memory_order_acquire)) {
-        e = hipFuncSetAttribute((const void *)tiled_wide_kernel,
+        e = hipFuncSetAttribute((const void *)tiled_wide_kernel<CAP>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideLdsBytes);
         if (e != hipSuccess)
             return e;
@@ -440,8 +442,14 @@ hipError_t launch_tiled_wide(const Params &p, int split, hipStream_t stream)
     }
     const int nqb = (p.nrows + kWideRows - 1) / kWideRows;
     const dim3 grid(nqb * p.nkv, 1, split ? p.nch : 1);
-    tiled_wide_kernel<<<grid, 64 * kWideWaves, kWideLdsBytes, stream>>>(p, split, 0);
+    tiled_wide_kernel<CAP><<<grid, 64 * kWideWaves, kWideLdsBytes, stream>>>(p, split, 0);
     return hipGetLastError();
+}
+
+hipError_t launch_tiled_wide(const Params &p, int split, hipStream_t stream)
+{
+    return p.softcap > 0.0f ? launch_wide<true>(p, split, stream)
+                            : launch_wide<false>(p, split, stream);
 }
 
 int tiled_wide_rows()
