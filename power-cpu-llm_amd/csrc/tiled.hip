@@ -408,7 +408,7 @@ constexpr int kMaxDevices = 64;
 
 // Compute units of the current device (cached per device; callers on other
 // threads with their own contexts may race here, so the cache is atomic).
-static int device_cus()
+int device_cus()
 {
     static std::atomic<int> cached[kMaxDevices];
     int dev = 0;
@@ -446,9 +446,10 @@ template <int DK, int W, bool CAP> static hipError_t configure_tiled()
 }
 
 // Chunks of a split launch to run as (16-row unit, chunk) items of the
-// pipelined kernel: the last chunk when the 8-wave items leave a last round
-// of at most one chunk's items and the tail's items fit one round. 0: none.
-static int tail_chunks(const Params &p, int nqb, int cus)
+// pipelined kernel: the last chunk when the tiled items (nqb row blocks per
+// KV head, one workgroup per CU) leave a last round of at most one chunk's
+// items and the tail's items fit one round. 0: none.
+int tiled_tail_chunks(const Params &p, int nqb, int cus)
 {
     const int64_t per_chunk = (int64_t)nqb * p.nkv;
     const int64_t items = per_chunk * p.nch;
@@ -475,7 +476,7 @@ template <int DK>
 static hipError_t launch_tiled_dk(const Params &p, int split, hipStream_t stream, bool *merged)
 {
     const int nqb = (p.nrows + kTiledRows - 1) / kTiledRows;
-    const int tail = split ? tail_chunks(p, nqb, device_cus()) : 0;
+    const int tail = split ? tiled_tail_chunks(p, nqb, device_cus()) : 0;
     const dim3 grid(nqb * p.nkv, 1, split ? p.nch - tail : 1);
     hipError_t e = p.softcap > 0.0f ? launch_tiled_grid<DK, true>(p, split, grid, stream)
                                     : launch_tiled_grid<DK, false>(p, split, grid, stream);
@@ -490,7 +491,7 @@ static hipError_t launch_tiled_dk(const Params &p, int split, hipStream_t stream
     return e;
 }
 
-hipError_t launch_tiled_wide(const Params &p, int split, hipStream_t stream);
+hipError_t launch_tiled_wide(const Params &p, int split, hipStream_t stream, bool *merged);
 int tiled_wide_rows();
 
 // Rows of one workgroup: 128 up to head dim 256; 64 at 512 (tiled_wide.hip).
@@ -508,7 +509,7 @@ hipError_t launch_tiled(const Params &p, int split, hipStream_t stream, bool *me
     case 64: return launch_tiled_dk<64>(p, split, stream, merged);
     case 128: return launch_tiled_dk<128>(p, split, stream, merged);
     case 256: return launch_tiled_dk<256>(p, split, stream, merged);
-    case 512: return launch_tiled_wide(p, split, stream);
+    case 512: return launch_tiled_wide(p, split, stream, merged);
     default: return hipErrorInvalidValue;
     }
 }

@@ -424,7 +424,7 @@ constexpr int kWideMaxDevices = 64;
 
 
 template <bool CAP>
-static hipError_t launch_wide(const Params &p, int split, hipStream_t stream)
+static hipError_t launch_wide(const Params &p, int split, dim3 grid, hipStream_t stream)
 {
     static std::atomic<bool> configured[kWideMaxDevices];
     int dev = 0;
@@ -440,16 +440,33 @@ static hipError_t launch_wide(const Params &p, int split, hipStream_t stream)
             return e;
         configured[dev].store(true, std::memory_order_release);
     }
-    const int nqb = (p.nrows + kWideRows - 1) / kWideRows;
-    const dim3 grid(nqb * p.nkv, 1, split ? p.nch : 1);
     tiled_wide_kernel<CAP><<<grid, 64 * kWideWaves, kWideLdsBytes, stream>>>(p, split, 0);
     return hipGetLastError();
 }
 
-hipError_t launch_tiled_wide(const Params &p, int split, hipStream_t stream)
+int device_cus();
+int tiled_tail_chunks(const Params &p, int nqb, int cus);
+hipError_t launch_pipe_kv_chunks(const Params &p, int c0, int n, bool merge_out,
+                                 hipStream_t stream);
+
+// A split launch whose chunk items leave a small last round runs that
+// round's chunk through the pipelined decode kernel, as the other tiled
+// kernel does; with all chunks in one span that tail also merges every
+// chunk partial into the output (*merged: no combine needed).
+hipError_t launch_tiled_wide(const Params &p, int split, hipStream_t stream, bool *merged)
 {
-    return p.softcap > 0.0f ? launch_wide<true>(p, split, stream)
-                            : launch_wide<false>(p, split, stream);
+    const int nqb = (p.nrows + kWideRows - 1) / kWideRows;
+    const int tail = split ? tiled_tail_chunks(p, nqb, device_cus()) : 0;
+    const dim3 grid(nqb * p.nkv, 1, split ? p.nch - tail : 1);
+    hipError_t e = p.softcap > 0.0f ? launch_wide<true>(p, split, grid, stream)
+                                    : launch_wide<false>(p, split, grid, stream);
+    if (e != hipSuccess || !tail)
+        return e;
+    const bool merge_out = p.nspan == 1;
+    e = launch_pipe_kv_chunks(p, p.nch - tail, tail, merge_out, stream);
+    if (e == hipSuccess && merge_out)
+        *merged = true;
+    return e;
 }
 
 int tiled_wide_rows()
