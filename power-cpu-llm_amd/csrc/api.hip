@@ -53,11 +53,14 @@ constexpr int64_t kPipeMinItemsWide = 512;
 // (requested beyond them, the pipelined kernel runs).
 constexpr int64_t kSpreadMaxWorkgroups = 768;
 // Every non-empty workspace begins with the spread decode's region of
-// published score words, room for kSpreadMaxItems (chunk, unit, KV head)
-// items; no other data ever lands there, so a stale word carries an earlier
+// published words: the score words of up to kSpreadMaxItems (chunk, unit,
+// KV head) items, then their chunk partials (16 rows x (256 + 2) words an
+// item). No other data ever lands there, so a stale word carries an earlier
 // launch's epoch and never the current one.
 constexpr int64_t kSpreadMaxItems = 128;
-constexpr size_t kTagFloats = (size_t)kSpreadMaxItems * pcl::kSpreadWordsPerItem * 2;
+constexpr size_t kSpreadScoreWords = (size_t)kSpreadMaxItems * pcl::kSpreadWordsPerItem;
+constexpr size_t kSpreadPartWords = (size_t)kSpreadMaxItems * pcl::kRows * (256 + 2);
+constexpr size_t kTagFloats = 2 * (kSpreadScoreWords + kSpreadPartWords);
 
 // Epochs of spread launches, per device: every launch on a device takes a
 // new one (shared by all contexts and the allocation-free scratch).
@@ -261,8 +264,7 @@ int make_plan(const pcl_attention_desc &d, int64_t h_lo, int64_t h_hi, int64_t h
     const bool partials = plan->kernel == PCL_KERNEL_TILED_SPLIT ||
                           ((plan->kernel == PCL_KERNEL_SPLIT_KV ||
                             plan->kernel == PCL_KERNEL_PIPE_KV ||
-                            plan->kernel == PCL_KERNEL_TWO_PASS ||
-                            plan->kernel == PCL_KERNEL_SPREAD_KV) && nch > 1);
+                            plan->kernel == PCL_KERNEL_TWO_PASS) && nch > 1);
     plan->part_floats = 0;
     if (partials) {
         plan->part_floats = (size_t)nkv * p.nrows_pad * nch * (dk + 2);
@@ -380,14 +382,15 @@ int run_plan_ws(pcl_context *ctx, Plan &plan, float *ws)
             p.ws_rec = body + plan.part_floats;
         if (plan.kernel == PCL_KERNEL_SPREAD_KV) {
             p.ws_tag = reinterpret_cast<uint64_t *>(ws);
+            if (p.nch > 1) // the launch merges its own chunk partials
+                p.ws_ptag = p.ws_tag + kSpreadScoreWords;
             p.epoch = next_epoch(ctx->device);
         }
     }
     hipError_t e = hipSuccess;
     bool combine = plan.kernel == PCL_KERNEL_TILED_SPLIT ||
                          ((plan.kernel == PCL_KERNEL_SPLIT_KV || plan.kernel == PCL_KERNEL_PIPE_KV ||
-                           plan.kernel == PCL_KERNEL_TWO_PASS ||
-                           plan.kernel == PCL_KERNEL_SPREAD_KV) &&
+                           plan.kernel == PCL_KERNEL_TWO_PASS) &&
                           p.ws_o);
     int span = open_span(ctx, 0);
     switch (plan.kernel) {

@@ -109,6 +109,10 @@ struct Params {
     // words of (epoch, score bits), and the launch's epoch
     uint64_t *ws_tag;
     uint32_t epoch;
+    // the spread decode's chunk partials as (epoch, bits) words,
+    // [kv][row (nrows_pad)][chunk][dk + 2] (O, then m and l), which the
+    // launch's own merge workgroups combine
+    uint64_t *ws_ptag;
     int *err;
 };
 

@@ -28,11 +28,15 @@
 // only for launches whose workgroups all fit on the chip at once, and a wave
 // waits only for the workgroups of its own item, adjacent in dispatch order.
 //
-// Output: for a launch of a single chunk, the output itself; otherwise the
-// chunk partial (m, l, O) for the combine kernel (split_kv.hip). (Merging
-// the partials in the kernel instead, by the last workgroup of each slice to
-// finish, was measured slower on MI355X: its chain of dependent memory round
-// trips outlasts the separate combine launch.)
+// Output: for a launch of a single chunk, the output itself. Otherwise each
+// workgroup publishes its chunk partial (m, l, O) as (epoch, bits) words,
+// and merge workgroups appended to the grid (dispatched after every item's
+// workgroups, so they wait only for workgroups already running) take them
+// and run the ordered chunk and span merges of the combine kernels
+// (split_kv.hip) for four dims of one row per thread, writing the output:
+// no combine launch. (Merging by the last workgroup of each slice to finish
+// instead was measured slower: its chain of dependent round trips outlasted
+// the separate combine launch.)
 #include "attention_device.hpp"
 
 namespace pcl {
@@ -58,9 +62,124 @@ __device__ __forceinline__ uint64_t take(const uint64_t *p)
 }
 
 
-template <int DK, bool FULL, bool CAP>
-__global__ __launch_bounds__(64 * kSpreadWaves, 2) void spread_kv_kernel(Params p)
+// Threads of a spread workgroup, and the chunks a merge thread requests per
+// batch of loads.
+constexpr int kSpreadThreads = 64 * kSpreadWaves;
+constexpr int kMergeBatch = 8;
+
+// Merge role: thread e of the merge workgroups owns four dims of one row of
+// one KV head; it takes every chunk partial of that row as published words
+// and merges them exactly as the combine kernels do (per span the span's
+// kSpanChunks slots in ascending order from (-inf, 0, 0), absent chunks as
+// empty parts; then the spans in ascending order), then writes the output.
+__device__ __forceinline__ void spread_merge(const Params &p, int64_t e)
 {
+    const int q4 = p.dim / 4;
+    const int64_t per_kv = (int64_t)p.nrows * q4;
+    if (e >= p.nkv * per_kv)
+        return;
+    const int kvl = (int)(e / per_kv);
+    const int row = (int)(e % per_kv) / q4;
+    const int d = 4 * (int)(e % per_kv % q4);
+    const int64_t slot0 = ((int64_t)kvl * p.nrows_pad + row) * p.nch;
+    const int stride = p.dk + 2;
+    Merged4 tot = {kNegInf, 0.f, f4{0.f, 0.f, 0.f, 0.f}};
+    bool gave_up = false;
+    // Wait cheaply while the items run: the row's threads poll one word of
+    // each chunk partial (its m), a word a thread per chunk, sleeping between
+    // polls (polling every word of every partial slowed the items' own loads
+    // by half). The full loads below re-check every word.
+    for (int polls = 0;; ++polls) {
+        bool fresh = true;
+        for (int cc = d / 4; cc < p.nch; cc += q4)
+            fresh &= (uint32_t)(take(p.ws_ptag + (slot0 + cc) * stride + p.dk) >> 32) == p.epoch;
+        if (__all(fresh))
+            break;
+        if (polls >= kMaxPolls) {
+            atomicOr(p.err, kErrWait);
+            return;
+        }
+        __builtin_amdgcn_s_sleep(8);
+    }
+    for (int sl = 0; sl < p.nspan; ++sl) {
+        const int span = p.s_lo + sl;
+        const int c0 = max(span * kSpanChunks, p.c_lo) - p.c_lo;
+        const int c1 = min((span + 1) * kSpanChunks, p.c_lo + p.nch) - p.c_lo;
+        Merged4 s = {kNegInf, 0.f, f4{0.f, 0.f, 0.f, 0.f}};
+        for (int b0 = 0; b0 < kSpanChunks; b0 += kMergeBatch) {
+            float mv[kMergeBatch], lv[kMergeBatch];
+            f4 ov[kMergeBatch];
+            for (int polls = 0; c0 + b0 < c1; ++polls) { // no loads for absent chunks
+                bool fresh = true;
+#pragma unroll
+                for (int i = 0; i < kMergeBatch; ++i) {
+                    const int cc = c0 + b0 + i;
+                    const uint64_t *w = p.ws_ptag + (slot0 + (cc < c1 ? cc : c0)) * stride;
+                    const uint64_t wm = take(w + p.dk), wl = take(w + p.dk + 1);
+                    uint64_t wo[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        wo[j] = take(w + d + j);
+                    bool ok = (uint32_t)(wm >> 32) == p.epoch && (uint32_t)(wl >> 32) == p.epoch;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        ok &= (uint32_t)(wo[j] >> 32) == p.epoch;
+                        ov[i][j] = __uint_as_float((uint32_t)wo[j]);
+                    }
+                    mv[i] = __uint_as_float((uint32_t)wm);
+                    lv[i] = __uint_as_float((uint32_t)wl);
+                    fresh &= ok || cc >= c1;
+                }
+                if (__all(fresh))
+                    break;
+                if (polls >= kMaxPolls) {
+                    gave_up = true;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+#pragma unroll
+            for (int i = 0; i < kMergeBatch; ++i) {
+                // chunks past the span merge as empty parts (no-ops)
+                const bool in = c0 + b0 + i < c1;
+                merge_into4(s, in ? mv[i] : kNegInf, in ? lv[i] : 0.f,
+                            in ? ov[i] : f4{0.f, 0.f, 0.f, 0.f});
+            }
+        }
+        merge_into4(tot, s.M, s.L, s.acc);
+    }
+    if (gave_up) {
+        atomicOr(p.err, kErrWait);
+        return;
+    }
+    const int kh = p.kh_first + kvl;
+    const int query = row / p.group;
+    const int h = kh * p.group + row % p.group;
+    if (h < p.h_lo || h >= p.h_hi)
+        return;
+    float *o = p.out + (int64_t)query * p.o_stride + (int64_t)(h - p.h_base) * p.dim;
+    f4 v;
+    bool nonfinite = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        v[j] = tot.acc[j] / tot.L;
+        nonfinite |= !is_finite(v[j]);
+    }
+    stg4(o + d, v);
+    if (nonfinite)
+        atomicOr(p.err, kErrOutput);
+}
+
+template <int DK, bool FULL, bool CAP>
+__global__ __launch_bounds__(kSpreadThreads, 2) void spread_kv_kernel(Params p)
+{
+    if ((int)blockIdx.z >= p.nkv * p.units) { // an appended merge workgroup
+        const int64_t mw = blockIdx.x + (int64_t)gridDim.x *
+                                            (blockIdx.y + (int64_t)gridDim.y *
+                                                              (blockIdx.z - p.nkv * p.units));
+        spread_merge(p, mw * kSpreadThreads + threadIdx.x);
+        return;
+    }
     constexpr int S = DK / kSpreadSliceDims;                  // workgroups per item
     constexpr int BPW = kBlocksPerChunk / (S * kSpreadWaves); // score blocks per wave
     constexpr int NU = DK / 32;                               // score chain steps
@@ -264,7 +383,7 @@ __global__ __launch_bounds__(64 * kSpreadWaves, 2) void spread_kv_kernel(Params 
     // O[i] is dim d0 + 4g + i of row `row`.
     const int d = d0 + 4 * g;
     const bool dout = rin && (FULL || d < p.dim);
-    if (p.ws_o == nullptr) { // the launch's only chunk: final output
+    if (p.ws_ptag == nullptr) { // the launch's only chunk: final output
         if (!rin)
             return;
         const int query = row / p.group;
@@ -285,12 +404,17 @@ __global__ __launch_bounds__(64 * kSpreadWaves, 2) void spread_kv_kernel(Params 
         return;
     }
 
+    // the chunk partial for the merge workgroups
     const int64_t slot = ((int64_t)kvl * p.nrows_pad + row) * p.nch + ci;
-    if (dout)
-        stg4(p.ws_o + slot * p.dk + d, O);
+    uint64_t *pw = p.ws_ptag + slot * (p.dk + 2);
+    if (dout) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            publish(pw + d + i, p.epoch, O[i]);
+    }
     if (rin && slice == 0 && w == 0 && g == 0) {
-        stg(p.ws_ml + 2 * slot, m);
-        stg(p.ws_ml + 2 * slot + 1, l);
+        publish(pw + p.dk, p.epoch, m);
+        publish(pw + p.dk + 1, p.epoch, l);
     }
 }
 
@@ -302,11 +426,19 @@ int spread_slices(int dk)
 template <int DK, bool CAP>
 static hipError_t launch_cap(const Params &p, hipStream_t stream)
 {
-    const dim3 grid(DK / kSpreadSliceDims, p.nch, p.nkv * p.units);
+    // merge workgroups (one thread per four dims of a row) as whole planes
+    // after the items' planes
+    int merge_planes = 0;
+    if (p.ws_ptag) {
+        const int64_t threads = (int64_t)p.nkv * p.nrows * (p.dim / 4);
+        const int64_t per_plane = (int64_t)(DK / kSpreadSliceDims) * p.nch * kSpreadThreads;
+        merge_planes = (int)((threads + per_plane - 1) / per_plane);
+    }
+    const dim3 grid(DK / kSpreadSliceDims, p.nch, p.nkv * p.units + merge_planes);
     if (p.dim == DK)
-        spread_kv_kernel<DK, true, CAP><<<grid, 64 * kSpreadWaves, 0, stream>>>(p);
+        spread_kv_kernel<DK, true, CAP><<<grid, kSpreadThreads, 0, stream>>>(p);
     else
-        spread_kv_kernel<DK, false, CAP><<<grid, 64 * kSpreadWaves, 0, stream>>>(p);
+        spread_kv_kernel<DK, false, CAP><<<grid, kSpreadThreads, 0, stream>>>(p);
     return hipGetLastError();
 }
 
