@@ -109,9 +109,8 @@ struct Params {
     // words of (epoch, score bits), and the launch's epoch
     uint64_t *ws_tag;
     uint32_t epoch;
-    // the spread decode's chunk partials as (epoch, bits) words,
-    // [kv][row (nrows_pad)][chunk][dk + 2] (O, then m and l), which the
-    // launch's own merge workgroups combine
+    // the spread decode's chunk partials as published words (partial_words
+    // below), which the launch's own merge workgroups combine
     uint64_t *ws_ptag;
     int *err;
 };
@@ -419,6 +418,113 @@ __device__ __forceinline__ Merged4 merge_chunks4(const Params &p, int64_t slot0,
                     in ? ov[i] : f4{0.f, 0.f, 0.f, 0.f});
     }
     return s;
+}
+
+// ---- Published words -------------------------------------------------
+// Data exchanged between workgroups of one launch without flags or fences:
+// each value is one 64-bit word (the launch's epoch, the value's bits),
+// written with a device-coherent 64-bit store, which lands whole; a reader
+// accepts a word only when it carries the current epoch. The words live in
+// a workspace region that holds nothing else (zero when allocated; epochs
+// are never zero), so a stale word carries an earlier epoch. Every wait is
+// bounded by kMaxPolls polls.
+
+constexpr int kMaxPolls = 1 << 16;
+// Chunks whose partial words a merging thread requests per batch of loads.
+constexpr int kMergeBatch = 8;
+
+typedef __attribute__((address_space(1))) uint64_t *gu64_ptr;
+
+__device__ __forceinline__ void publish(uint64_t *p, uint32_t epoch, float v)
+{
+    const uint64_t word = ((uint64_t)epoch << 32) | (uint64_t)__float_as_uint(v);
+    __hip_atomic_store((gu64_ptr)p, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t take(const uint64_t *p)
+{
+    return __hip_atomic_load((gu64_ptr)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Published chunk partials of the spread decode: row `row` (a real row) of
+// launch KV head kvl, launch chunk ci, at
+// ws_ptag + (((kvl * nrows + row) * nch + ci) * (dk + 2)): O[dk], then m, l.
+__device__ __forceinline__ uint64_t *partial_words(const Params &p, int kvl, int row, int ci)
+{
+    return p.ws_ptag + (((int64_t)kvl * p.nrows + row) * p.nch + ci) * (p.dk + 2);
+}
+
+// Waits, cheaply, until the m words of chunks ci = first, first + step, ...
+// below last of row slot0 (the row's first chunk slot) carry the epoch (the
+// wave's lanes together cover their rows' chunks). Polling every word of
+// every partial instead slowed the producing workgroups' own loads. False
+// when the wait gave up.
+__device__ __forceinline__ bool wait_partials(const Params &p, int64_t slot0, int first,
+                                              int step, int last)
+{
+    const int stride = p.dk + 2;
+    for (int polls = 0;; ++polls) {
+        bool fresh = true;
+        for (int ci = first; ci < last; ci += step)
+            fresh &= (uint32_t)(take(p.ws_ptag + (slot0 + ci) * stride + p.dk) >> 32) == p.epoch;
+        if (__all(fresh))
+            return true;
+        if (polls >= kMaxPolls)
+            return false;
+        __builtin_amdgcn_s_sleep(8);
+    }
+}
+
+// One batch of a span's ordered chunk merge from published words: chunks
+// c0 + b0 + i (i < B; those at or past c1 merge as empty parts,
+// with no loads) of row slot0, four dims from d, merged into s in ascending
+// order. Every word is re-checked (and the batch reloaded until all carry
+// the epoch). False when the wait gave up.
+template <int B = kMergeBatch>
+__device__ __forceinline__ bool merge_words_batch(const Params &p, int64_t slot0, int c0,
+                                                  int b0, int c1, int d, Merged4 &s)
+{
+    const int stride = p.dk + 2;
+    float mv[B], lv[B];
+    f4 ov[B];
+    bool ok = true;
+    for (int polls = 0; c0 + b0 < c1; ++polls) {
+        bool fresh = true;
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            const int cc = c0 + b0 + i;
+            const uint64_t *w = p.ws_ptag + (slot0 + (cc < c1 ? cc : c0)) * stride;
+            const uint64_t wm = take(w + p.dk), wl = take(w + p.dk + 1);
+            uint64_t wo[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                wo[j] = take(w + d + j);
+            bool got = (uint32_t)(wm >> 32) == p.epoch && (uint32_t)(wl >> 32) == p.epoch;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                got &= (uint32_t)(wo[j] >> 32) == p.epoch;
+                ov[i][j] = __uint_as_float((uint32_t)wo[j]);
+            }
+            mv[i] = __uint_as_float((uint32_t)wm);
+            lv[i] = __uint_as_float((uint32_t)wl);
+            fresh &= got || cc >= c1;
+        }
+        if (__all(fresh))
+            break;
+        if (polls >= kMaxPolls) {
+            ok = false;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+        // chunks past the span merge as empty parts (no-ops)
+        const bool in = c0 + b0 + i < c1;
+        merge_into4(s, in ? mv[i] : kNegInf, in ? lv[i] : 0.f,
+                    in ? ov[i] : f4{0.f, 0.f, 0.f, 0.f});
+    }
+    return ok;
 }
 
 // Logit soft-cap: cap * tanh(s / cap) in f32, one definition for every

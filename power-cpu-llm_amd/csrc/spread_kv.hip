@@ -44,28 +44,12 @@ namespace pcl {
 constexpr int kSpreadWaves = 2;
 constexpr int kSpreadSliceDims = 32;
 constexpr int kBlocksPerChunk = 2 * kTilesPerChunk; // 16-key blocks
-constexpr int kMaxPolls = 1 << 16;                  // about 0.1 s of polling
 
-typedef __attribute__((address_space(1))) uint64_t *gu64_ptr;
 typedef __attribute__((address_space(3))) void *spread_lptr_t;
 typedef const __attribute__((address_space(1))) void *spread_gptr_t;
 
-__device__ __forceinline__ void publish(uint64_t *p, uint32_t epoch, float v)
-{
-    const uint64_t word = ((uint64_t)epoch << 32) | (uint64_t)__float_as_uint(v);
-    __hip_atomic_store((gu64_ptr)p, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ uint64_t take(const uint64_t *p)
-{
-    return __hip_atomic_load((gu64_ptr)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-
-// Threads of a spread workgroup, and the chunks a merge thread requests per
-// batch of loads.
+// Threads of a spread workgroup.
 constexpr int kSpreadThreads = 64 * kSpreadWaves;
-constexpr int kMergeBatch = 8;
 
 // Merge role: thread e of the merge workgroups owns four dims of one row of
 // one KV head; it takes every chunk partial of that row as published words
@@ -81,74 +65,24 @@ __device__ __forceinline__ void spread_merge(const Params &p, int64_t e)
     const int kvl = (int)(e / per_kv);
     const int row = (int)(e % per_kv) / q4;
     const int d = 4 * (int)(e % per_kv % q4);
-    const int64_t slot0 = ((int64_t)kvl * p.nrows_pad + row) * p.nch;
-    const int stride = p.dk + 2;
-    Merged4 tot = {kNegInf, 0.f, f4{0.f, 0.f, 0.f, 0.f}};
-    bool gave_up = false;
-    // Wait cheaply while the items run: the row's threads poll one word of
-    // each chunk partial (its m), a word a thread per chunk, sleeping between
-    // polls (polling every word of every partial slowed the items' own loads
-    // by half). The full loads below re-check every word.
-    for (int polls = 0;; ++polls) {
-        bool fresh = true;
-        for (int cc = d / 4; cc < p.nch; cc += q4)
-            fresh &= (uint32_t)(take(p.ws_ptag + (slot0 + cc) * stride + p.dk) >> 32) == p.epoch;
-        if (__all(fresh))
-            break;
-        if (polls >= kMaxPolls) {
-            atomicOr(p.err, kErrWait);
-            return;
-        }
-        __builtin_amdgcn_s_sleep(8);
+    const int64_t slot0 = ((int64_t)kvl * p.nrows + row) * p.nch;
+    // the row's threads poll one word of each chunk partial between them
+    if (!wait_partials(p, slot0, d / 4, q4, p.nch)) {
+        atomicOr(p.err, kErrWait);
+        return;
     }
+    Merged4 tot = {kNegInf, 0.f, f4{0.f, 0.f, 0.f, 0.f}};
+    bool ok = true;
     for (int sl = 0; sl < p.nspan; ++sl) {
         const int span = p.s_lo + sl;
         const int c0 = max(span * kSpanChunks, p.c_lo) - p.c_lo;
         const int c1 = min((span + 1) * kSpanChunks, p.c_lo + p.nch) - p.c_lo;
-        Merged4 s = {kNegInf, 0.f, f4{0.f, 0.f, 0.f, 0.f}};
-        for (int b0 = 0; b0 < kSpanChunks; b0 += kMergeBatch) {
-            float mv[kMergeBatch], lv[kMergeBatch];
-            f4 ov[kMergeBatch];
-            for (int polls = 0; c0 + b0 < c1; ++polls) { // no loads for absent chunks
-                bool fresh = true;
-#pragma unroll
-                for (int i = 0; i < kMergeBatch; ++i) {
-                    const int cc = c0 + b0 + i;
-                    const uint64_t *w = p.ws_ptag + (slot0 + (cc < c1 ? cc : c0)) * stride;
-                    const uint64_t wm = take(w + p.dk), wl = take(w + p.dk + 1);
-                    uint64_t wo[4];
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        wo[j] = take(w + d + j);
-                    bool ok = (uint32_t)(wm >> 32) == p.epoch && (uint32_t)(wl >> 32) == p.epoch;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        ok &= (uint32_t)(wo[j] >> 32) == p.epoch;
-                        ov[i][j] = __uint_as_float((uint32_t)wo[j]);
-                    }
-                    mv[i] = __uint_as_float((uint32_t)wm);
-                    lv[i] = __uint_as_float((uint32_t)wl);
-                    fresh &= ok || cc >= c1;
-                }
-                if (__all(fresh))
-                    break;
-                if (polls >= kMaxPolls) {
-                    gave_up = true;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(2);
-            }
-#pragma unroll
-            for (int i = 0; i < kMergeBatch; ++i) {
-                // chunks past the span merge as empty parts (no-ops)
-                const bool in = c0 + b0 + i < c1;
-                merge_into4(s, in ? mv[i] : kNegInf, in ? lv[i] : 0.f,
-                            in ? ov[i] : f4{0.f, 0.f, 0.f, 0.f});
-            }
-        }
-        merge_into4(tot, s.M, s.L, s.acc);
+        Merged4 sm = {kNegInf, 0.f, f4{0.f, 0.f, 0.f, 0.f}};
+        for (int b0 = 0; b0 < kSpanChunks; b0 += kMergeBatch)
+            ok &= merge_words_batch(p, slot0, c0, b0, c1, d, sm);
+        merge_into4(tot, sm.M, sm.L, sm.acc);
     }
-    if (gave_up) {
+    if (!ok) {
         atomicOr(p.err, kErrWait);
         return;
     }
@@ -405,14 +339,15 @@ __global__ __launch_bounds__(kSpreadThreads, 2) void spread_kv_kernel(Params p)
     }
 
     // the chunk partial for the merge workgroups
-    const int64_t slot = ((int64_t)kvl * p.nrows_pad + row) * p.nch + ci;
-    uint64_t *pw = p.ws_ptag + slot * (p.dk + 2);
+    if (!rin)
+        return;
+    uint64_t *pw = partial_words(p, kvl, row, ci);
     if (dout) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             publish(pw + d + i, p.epoch, O[i]);
     }
-    if (rin && slice == 0 && w == 0 && g == 0) {
+    if (slice == 0 && w == 0 && g == 0) {
         publish(pw + p.dk, p.epoch, m);
         publish(pw + p.dk + 1, p.epoch, l);
     }
