@@ -208,11 +208,23 @@ int pcl_attention_launch_noalloc(pcl_context *ctx, const pcl_attention_desc *des
 int pcl_context_reserve(pcl_context *ctx, size_t bytes);
 /* Wait for the stream; *device_error receives the error flag (bit 0: a
  * non-finite allowed score, bit 1: a non-finite output, bit 2: a non-finite
- * head-transform value, bit 3: a non-finite output-block value) and is
+ * head-transform value, bit 3: a non-finite output-block value, bit 4: a
+ * wait between workgroups ran out, pcl_context_set_wait_limit) and is
  * cleared. */
 int pcl_context_sync(pcl_context *ctx, int *device_error);
 /* Kernel the descriptor resolves to under PCL_KERNEL_AUTO. */
 int pcl_attention_resolve_kernel(const pcl_attention_desc *desc);
+
+/* Bound of the waits between workgroups of one launch (the spread decode's
+ * score exchange and its merge of chunk partials), in polls of a few hundred
+ * cycles each; 0 restores the default (65536, some tens of milliseconds).
+ * A wait that runs out sets bit 4 (16) of the device error flag and its
+ * workgroup finishes without its result: the launch's output is then not
+ * valid. Callers whose GPU is shared with other work may lower or raise it;
+ * tests use a tiny limit to exercise the failure path. No counterpart in
+ * the reference (its CPU threads do not wait on each other inside an
+ * attention call). PCL_INVALID_PARAMETER for a negative limit. */
+int pcl_context_set_wait_limit(pcl_context *ctx, int polls);
 
 /* Per-kernel timing, the device-side counterpart of the engine's stage
  * timers (stats::Span, src/engine/stats.rs:9-64). While enabled, every launch

@@ -56,6 +56,7 @@ EXPORTS = (
     "pcl_context_reserve",
     "pcl_context_sync",
     "pcl_attention_resolve_kernel",
+    "pcl_context_set_wait_limit",
     "pcl_context_set_timing",
     "pcl_context_timing",
     "pcl_kv_cache_create",
@@ -171,6 +172,8 @@ def load():
     lib.pcl_context_sync.argtypes = [vp, ctypes.POINTER(ctypes.c_int)]
     lib.pcl_attention_resolve_kernel.restype = ctypes.c_int
     lib.pcl_attention_resolve_kernel.argtypes = [ctypes.POINTER(PclDesc)]
+    lib.pcl_context_set_wait_limit.restype = ctypes.c_int
+    lib.pcl_context_set_wait_limit.argtypes = [vp, ctypes.c_int]
     lib.pcl_context_set_timing.restype = ctypes.c_int
     lib.pcl_context_set_timing.argtypes = [vp, ctypes.c_int]
     lib.pcl_context_timing.restype = ctypes.c_int
@@ -395,6 +398,13 @@ class Context:
 
     def resolve_kernel(self, desc):
         return self.lib.pcl_attention_resolve_kernel(ctypes.byref(desc))
+
+    def set_wait_limit(self, polls):
+        """pcl_context_set_wait_limit: bound of the spread decode's waits
+        between workgroups (0 = the default)."""
+        rc = self.lib.pcl_context_set_wait_limit(self.handle, int(polls))
+        if rc != OK:
+            raise AttentionError(rc)
 
     def set_timing(self, enable):
         rc = self.lib.pcl_context_set_timing(self.handle, int(bool(enable)))

@@ -385,6 +385,7 @@ int run_plan_ws(pcl_context *ctx, Plan &plan, float *ws)
             if (p.nch > 1) // the launch merges its own chunk partials
                 p.ws_ptag = p.ws_tag + kSpreadScoreWords;
             p.epoch = next_epoch(ctx->device);
+            p.max_polls = ctx->wait_polls;
         }
     }
     hipError_t e = hipSuccess;
@@ -808,6 +809,14 @@ int pcl_attention_launch_noalloc(pcl_context *ctx, const pcl_attention_desc *des
     const int out = run_plan_ws(ctx, plan, static_cast<float *>(ctx->noalloc_scratch));
     ctx->timing = timing;
     return out;
+}
+
+int pcl_context_set_wait_limit(pcl_context *ctx, int polls)
+{
+    if (!ctx || polls < 0)
+        return PCL_INVALID_PARAMETER;
+    ctx->wait_polls = polls == 0 ? 1 << 16 : polls;
+    return PCL_OK;
 }
 
 int pcl_context_set_timing(pcl_context *ctx, int enable)

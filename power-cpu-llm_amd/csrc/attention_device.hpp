@@ -109,6 +109,7 @@ struct Params {
     // words of (epoch, score bits), and the launch's epoch
     uint64_t *ws_tag;
     uint32_t epoch;
+    int max_polls; // bound of every wait for another workgroup's words
     // the spread decode's chunk partials as published words (partial_words
     // below), which the launch's own merge workgroups combine
     uint64_t *ws_ptag;
@@ -427,7 +428,8 @@ __device__ __forceinline__ Merged4 merge_chunks4(const Params &p, int64_t slot0,
 // accepts a word only when it carries the current epoch. The words live in
 // a workspace region that holds nothing else (zero when allocated; epochs
 // are never zero), so a stale word carries an earlier epoch. Every wait is
-// bounded by kMaxPolls polls.
+// bounded by the launch's max_polls polls (kMaxPolls unless the context set
+// another limit).
 
 constexpr int kMaxPolls = 1 << 16;
 // Chunks whose partial words a merging thread requests per batch of loads.
@@ -469,7 +471,7 @@ __device__ __forceinline__ bool wait_partials(const Params &p, int64_t slot0, in
             fresh &= (uint32_t)(take(p.ws_ptag + (slot0 + ci) * stride + p.dk) >> 32) == p.epoch;
         if (__all(fresh))
             return true;
-        if (polls >= kMaxPolls)
+        if (polls >= p.max_polls)
             return false;
         __builtin_amdgcn_s_sleep(8);
     }
@@ -511,7 +513,7 @@ __device__ __forceinline__ bool merge_words_batch(const Params &p, int64_t slot0
         }
         if (__all(fresh))
             break;
-        if (polls >= kMaxPolls) {
+        if (polls >= p.max_polls) {
             ok = false;
             break;
         }

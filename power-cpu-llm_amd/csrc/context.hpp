@@ -28,6 +28,8 @@ struct pcl_context {
     // K and V upload, the mask, the output, a private K and V.
     void *stage[kStageSlots] = {};
     size_t stage_bytes[kStageSlots] = {};
+    // bound of the spread decode's waits for other workgroups (polls)
+    int wait_polls = 1 << 16;
     // per-kernel timing: recorded spans and a pool of free events
     bool timing = false;
     std::vector<TimedSpan> spans;

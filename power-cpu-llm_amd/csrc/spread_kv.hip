@@ -22,7 +22,7 @@
 // workspace that holds nothing else (zero when allocated; epochs are never
 // zero), so a stale word carries an earlier epoch.
 //
-// The wait is bounded: after kMaxPolls reads a wave gives up, sets kErrWait
+// The wait is bounded: after max_polls reads a wave gives up, sets kErrWait
 // in the error flag and finishes (its results are then not valid and the
 // host reports the failure), so every wave exits. The host picks this kernel
 // only for launches whose workgroups all fit on the chip at once, and a wave
@@ -237,7 +237,7 @@ __global__ __launch_bounds__(kSpreadThreads, 2) void spread_kv_kernel(Params p)
                 }
             if (__all(fresh))
                 break;
-            if (++polls >= kMaxPolls) {
+            if (++polls >= p.max_polls) {
                 if (lane == 0)
                     atomicOr(p.err, kErrWait);
                 break;

@@ -486,6 +486,38 @@ def test_softcap_off_is_bitwise_inert(torch, ctx):
             assert err == 0 and np.max(np.abs(huge - base)) < 1e-6, kernel
 
 
+def test_spread_waits_give_up_at_the_host_limit_then_recover(pcl, torch, ctx):
+    # a limit of one poll on the waits between workgroups of the spread decode
+    # (its score exchange and the merge of its chunk partials): the waits run
+    # out while the items still run, which sets bit 4 of the error flag and
+    # every workgroup finishes (no hang); back at the default limit the same
+    # context reproduces the bits of another context
+    qheads, kvh, dim, nkeys = 16, 8, 256, 2048
+    g = np.random.default_rng(77)
+    q = prescale(g.standard_normal((1, qheads * dim), dtype=np.float32), dim)
+    k = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+    v = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+    want, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, pcl.KERNEL_SPREAD_KV, 1, 0, 0,
+                         nkeys - 1)
+    assert err == 0
+    other = pcl.Context(0, torch.cuda.current_stream().cuda_stream)
+    try:
+        with pytest.raises(pcl.AttentionError) as e:
+            other.set_wait_limit(-1)
+        assert e.value.kind == "InvalidParameter"
+        other.set_wait_limit(1)
+        _, err = run_desc(torch, other, q, k, v, qheads, kvh, dim, pcl.KERNEL_SPREAD_KV, 1, 0, 0,
+                          nkeys - 1)
+        assert err & 16, err
+        other.set_wait_limit(0)
+        got, err = run_desc(torch, other, q, k, v, qheads, kvh, dim, pcl.KERNEL_SPREAD_KV, 1, 0,
+                            0, nkeys - 1)
+        assert err == 0
+        assert np.array_equal(bits(got), bits(want))
+    finally:
+        other.close()
+
+
 def test_split_launch_tail_with_masks_segments_and_kv_ranges(torch, ctx, oracle):
     # the canvas shape (4 row blocks x 8 KV heads x 9 chunks = 288 items on
     # 256 CUs) leaves one chunk's items for a last round, which runs as
