@@ -221,9 +221,12 @@ int pcl_attention_resolve_kernel(const pcl_attention_desc *desc);
  * A wait that runs out sets bit 4 (16) of the device error flag and its
  * workgroup finishes without its result: the launch's output is then not
  * valid. Callers whose GPU is shared with other work may lower or raise it;
- * tests use a tiny limit to exercise the failure path. No counterpart in
- * the reference (its CPU threads do not wait on each other inside an
- * attention call). PCL_INVALID_PARAMETER for a negative limit. */
+ * tests use a tiny limit to exercise the failure path. ctx NULL sets the
+ * limit of the context the host-pointer entries (section 1) use; those
+ * entries rerun a launch whose waits ran out with the pipelined kernel,
+ * which never waits, so their result is unaffected. No counterpart in the
+ * reference (its CPU threads do not wait on each other inside an attention
+ * call). PCL_INVALID_PARAMETER for a negative limit. */
 int pcl_context_set_wait_limit(pcl_context *ctx, int polls);
 
 /* Per-kernel timing, the device-side counterpart of the engine's stage

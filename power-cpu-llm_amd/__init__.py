@@ -331,6 +331,15 @@ def raw_multi_kv(query, nq, q_stride, keys, values, qheads, kvheads, dim, nkeys,
     return bool(ok), out[:nq * o_stride]
 
 
+def set_host_wait_limit(polls):
+    """pcl_context_set_wait_limit(NULL, polls): the wait bound of the context
+    the host-pointer entries use (0 = the default); those entries rerun a
+    launch whose waits ran out with the pipelined kernel."""
+    rc = load().pcl_context_set_wait_limit(None, int(polls))
+    if rc != OK:
+        raise AttentionError(rc)
+
+
 class Context:
     """The device-resident entry (pcl_context). Pointers are device addresses
     (ints); torch tensors work through data_ptr(). stream None: the context

@@ -486,6 +486,10 @@ void *noalloc_scratch(int device)
 std::mutex g_abi_mutex;
 pcl_context *g_abi_ctx = nullptr;
 
+// Wait limit of the host-pointer entries' context (0: the default), set
+// with pcl_context_set_wait_limit(NULL, polls).
+std::atomic<int> g_abi_wait_polls{0};
+
 pcl_context *abi_context()
 {
     if (!g_abi_ctx) {
@@ -568,6 +572,8 @@ bool run_host(const float *query, size_t q_floats, const float *keys, const floa
             if (!ctx)
                 return false;
             (void)hipSetDevice(ctx->device);
+            const int polls = g_abi_wait_polls.load(std::memory_order_relaxed);
+            ctx->wait_polls = polls ? polls : 1 << 16;
             const size_t kv_bytes = kv_floats * sizeof(float);
             float *dq = static_cast<float *>(stage_buffer(ctx, kStageQ, q_floats * sizeof(float)));
             uint8_t *dm =
@@ -617,17 +623,32 @@ bool run_host(const float *query, size_t q_floats, const float *keys, const floa
                 return false;
             if (run_plan(ctx, plan) != PCL_OK)
                 return false;
+            int derr = 0;
+            if (pcl_context_sync(ctx, &derr) != PCL_OK)
+                return false;
+            if (derr & pcl::kErrWait) {
+                // the spread decode's workgroups gave up waiting for each
+                // other (a GPU shared with other work can keep some of them
+                // from running): once more with the pipelined kernel, which
+                // never waits, for the same bits
+                d.kernel = PCL_KERNEL_PIPE_KV;
+                if (make_plan(d, h_lo, h_hi, h_base, &plan) != PCL_OK ||
+                    run_plan(ctx, plan) != PCL_OK ||
+                    pcl_context_sync(ctx, &derr) != PCL_OK)
+                    return false;
+            }
+            if (derr != 0)
+                return false;
             e = hipMemcpy2DAsync(out, out_pitch_floats * sizeof(float), dout,
                                  out_pitch_floats * sizeof(float), out_row_floats * sizeof(float),
                                  out_rows, hipMemcpyDeviceToHost, ctx->stream);
+            if (e == hipSuccess)
+                e = hipStreamSynchronize(ctx->stream);
             if (e != hipSuccess) {
                 report("device to host copy", e);
                 return false;
             }
-            int derr = 0;
-            if (pcl_context_sync(ctx, &derr) != PCL_OK)
-                return false;
-            return derr == 0;
+            return true;
         }();
     }
     if (shared) {
@@ -813,8 +834,12 @@ int pcl_attention_launch_noalloc(pcl_context *ctx, const pcl_attention_desc *des
 
 int pcl_context_set_wait_limit(pcl_context *ctx, int polls)
 {
-    if (!ctx || polls < 0)
+    if (polls < 0)
         return PCL_INVALID_PARAMETER;
+    if (!ctx) { // the host-pointer entries' own context
+        g_abi_wait_polls.store(polls, std::memory_order_relaxed);
+        return PCL_OK;
+    }
     ctx->wait_polls = polls == 0 ? 1 << 16 : polls;
     return PCL_OK;
 }

@@ -155,6 +155,25 @@ def test_concurrent_head_range_calls_share_one_upload_and_see_rewrites(kernels, 
     pool.shutdown()
 
 
+def test_host_entry_reruns_a_spread_launch_whose_waits_ran_out(pcl, kernels):
+    # the engine-facing entry's context with a one-poll wait bound: its 2K
+    # decode (the spread kernel) gives up waiting, and the entry reruns it
+    # with the pipelined kernel, which never waits: the same bits as at the
+    # default bound
+    qheads, kvh, dim, nkeys = 16, 8, 256, 2048
+    g = np.random.default_rng(0x3A17)
+    q = prescale(g.standard_normal(qheads * dim, dtype=np.float32), dim)
+    k = g.standard_normal(nkeys * kvh * dim, dtype=np.float32)
+    v = g.standard_normal(nkeys * kvh * dim, dtype=np.float32)
+    want = kernels.attention(q, k, v, kvh, dim, None)
+    pcl.set_host_wait_limit(1)
+    try:
+        got = kernels.attention(q, k, v, kvh, dim, None)
+    finally:
+        pcl.set_host_wait_limit(0)
+    assert np.array_equal(bits(got), bits(want))
+
+
 def test_attention_multi_matches_single_queries(kernels):
     # int8/tests.rs:661-706
     rng = Rng(0x51ed270b)
