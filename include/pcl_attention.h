@@ -115,7 +115,8 @@ enum pcl_kernel {
     PCL_KERNEL_SPREAD_KV = 6,   /* split-KV decode with each key chunk spread
                                    over head_dim/32 workgroups that exchange
                                    raw scores (head dim <= 256, short
-                                   launches) + ordered combine */
+                                   launches); the launch's own merge
+                                   workgroups run the ordered combine */
 };
 
 /* Attention of nq query positions over keys [0, n0+n1): keys 0..n0-1 come
@@ -232,7 +233,8 @@ int pcl_context_set_wait_limit(pcl_context *ctx, int polls);
 /* Per-kernel timing, the device-side counterpart of the engine's stage
  * timers (stats::Span, src/engine/stats.rs:9-64). While enabled, every launch
  * records HIP events on the context's stream around the kernels that stream
- * K/V (role 0: split-KV, pipelined, two-pass or tiled kernels) and around the
+ * K/V (role 0: split-KV, pipelined, two-pass, spread or tiled kernels; the
+ * spread kernel includes its own merge) and around the
  * ordered combine (role 1). pcl_context_timing waits for the stream, adds the
  * elapsed times of the recorded launches to ms[role] and their number to
  * launches[role], and forgets them. Enabling costs two event records per role
