@@ -137,7 +137,8 @@ enum pcl_kernel {
  * 226-235; the engine itself caps only its final logits, src/engine/text.rs:
  * 963,979, so it leaves this off). An infinite score then becomes
  * +-softcap; a NaN one is still an error. Negative, subnormal or non-finite
- * values are PCL_INVALID_PARAMETER.
+ * values, and values above 2^126 (whose f32 reciprocal is subnormal), are
+ * PCL_INVALID_PARAMETER.
  * Output: query i, head h (kh_first*group <= h < kh_end*group) at
  * out + i*o_stride + (h - kh_first*group)*dim. */
 typedef struct pcl_attention_desc {

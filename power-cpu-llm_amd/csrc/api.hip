@@ -175,9 +175,11 @@ int make_plan(const pcl_attention_desc &d, int64_t h_lo, int64_t h_hi, int64_t h
         return PCL_INVALID_SHAPE;
     if (d.kernel < PCL_KERNEL_AUTO || d.kernel > PCL_KERNEL_SPREAD_KV)
         return PCL_INVALID_PARAMETER;
+    // negative, NaN, infinite or subnormal caps, and caps whose f32
+    // reciprocal (what the kernels multiply by) would be subnormal
     if (!(d.softcap >= 0.0f) || !std::isfinite(d.softcap) ||
-        (d.softcap > 0.0f && !std::isnormal(d.softcap)))
-        return PCL_INVALID_PARAMETER; // negative, NaN, infinite or subnormal cap
+        (d.softcap > 0.0f && (!std::isnormal(d.softcap) || !std::isnormal(1.0f / d.softcap))))
+        return PCL_INVALID_PARAMETER;
     const int64_t group = d.qheads / d.kvheads;
     const int64_t nkeys = d.n0 + d.n1;
     const int64_t nkv = d.kh_end - d.kh_first;

@@ -121,7 +121,8 @@ def test_descriptor_validation_on_the_host(pcl):
     # the optional logit soft-cap: 0 (either sign) is off, a normal positive
     # value is on; negative, subnormal and non-finite caps are rejected
     for cap, valid in ((0.0, True), (-0.0, True), (30.0, True), (1e30, True), (-1.0, False),
-                       (1e-40, False), (float("inf"), False), (float("nan"), False)):
+                       (1e-40, False), (3e38, False), (float("inf"), False),
+                       (float("nan"), False)):
         d.softcap = cap
         assert (lib.pcl_attention_resolve_kernel(ctypes.byref(d)) != -1) == valid, cap
     d.softcap = 0.0
