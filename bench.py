@@ -66,6 +66,9 @@ WORKLOADS = {
     # projections: transform fused with the cache append, then attention
     "transform_4k": (16, 8, 256, 4096, 0, True, 0, 0, "transform", False),
     "decode_32k_step": (16, 8, 256, 1, 32768, True, 0, 32767, "step", False),
+    # the whole attention layer of one decode token on the device: the step
+    # above, then the output block on its attended row (LAYER_HIDDEN wide)
+    "decode_32k_layer": (16, 8, 256, 1, 32768, True, 0, 32767, "layer", False),
     # the attention output block (projection of the 16 x 256 attended heads
     # to a 2816-wide hidden row, post-norm, residual) for one decode token and
     # for a 4K-token prompt; here `nkeys` is the hidden width
@@ -81,6 +84,8 @@ WORKLOADS = {
     "decode_32k_host_fanout": (16, 8, 256, 1, 32768, True, 0, 32767, "host", False),
 }
 HEADLINE = "decode_32k"
+# hidden width of the layer workload's output block (that of output_decode)
+LAYER_HIDDEN = 2816
 # the metric's second half: f32 prefill attention at 4K tokens (the global
 # layer; the sliding-window layer is reported beside it)
 PREFILL = ("prefill_4k", "prefill_4k_window1024")
@@ -129,6 +134,16 @@ def work(name):
         # weights and attended rows read, residual read, result written
         width, hidden = qh * dim, nkeys
         return 2 * nq * width * hidden, 4 * (width * hidden + nq * width + 2 * nq * hidden), 0
+    if kind == "layer":
+        # the attention step, then the output block on its attended rows
+        flops, bytes_, pairs = work_attention(qh, kvh, dim, nq, nkeys, causal, window, fq)
+        width = qh * dim
+        return (flops + 2 * nq * width * LAYER_HIDDEN,
+                bytes_ + 4 * (width * LAYER_HIDDEN + nq * width + 2 * nq * LAYER_HIDDEN), pairs)
+    return work_attention(qh, kvh, dim, nq, nkeys, causal, window, fq)
+
+
+def work_attention(qh, kvh, dim, nq, nkeys, causal, window, fq):
     pairs = allowed_pairs(nq, nkeys, causal, window, fq)
     flops = 4 * dim * pairs * qh
     # decode bytes: attended K and V rows of every KV head, plus Q and O
@@ -186,9 +201,9 @@ def time_workload(torch, pcl, ctx, name, steps, warmup, seed=0, kernel=0):
     nsets = max(2, min(MAX_SETS, -(-CYCLE_BYTES // set_bytes)))
     if kind == "cache":
         return time_cache_workload(torch, pcl, ctx, name, steps, warmup, nsets, seed)
-    if kind == "step":
+    if kind in ("step", "layer"):
         return time_cache_workload(torch, pcl, ctx, name, steps, warmup, nsets, seed,
-                                   transform=True)
+                                   transform=True, output=(kind == "layer"))
     if kind == "transform":
         return time_transform_workload(torch, pcl, ctx, name, steps, warmup, seed)
     if kind == "output":
@@ -381,14 +396,19 @@ def time_output_workload(torch, pcl, ctx, name, steps, warmup, seed):
     return ev, wall, kernel, None, {"stream_ms": ev, "combine_ms": 0.0}, nsets
 
 
-def time_cache_workload(torch, pcl, ctx, name, steps, warmup, nsets, seed, transform=False):
+def time_cache_workload(torch, pcl, ctx, name, steps, warmup, nsets, seed, transform=False,
+                        output=False):
     """Decode steps through pcl.LayerCache: per step, append one token's K/V
     after nkeys-1 cached rows (as device rows, or with transform=True from the
     token's raw Q/K/V projections through the head transform, fused with the
     append), attend over the cache's rows in place (its encoder descriptor),
-    roll the step back. Each input set is its own cache."""
+    with output=True run the output block (LAYER_HIDDEN-wide projection,
+    post-norm, residual) on the attended row, and roll the step back. Each
+    input set is its own cache and output weights."""
     qh, kvh, dim, nq, nkeys, causal, window, fq, kind, _ = WORKLOADS[name]
     t = make_transform(torch, pcl, ctx, qh, kvh, dim) if transform else None
+    width = qh * dim
+    dev = torch.device("cuda:0")
     sets = []
     for i in range(nsets):
         q, k, v = make_inputs(torch, name, seed + 1000 * i)
@@ -401,6 +421,15 @@ def time_cache_workload(torch, pcl, ctx, name, steps, warmup, nsets, seed, trans
         if transform:
             host["raw_q"] = q.clone()
             host["q_prepared"] = torch.empty_like(q)
+        if output:
+            gen = torch.Generator(device=dev)
+            gen.manual_seed(0x5EED0900 + seed + i)
+            host["w"] = torch.randn((LAYER_HIDDEN, width), generator=gen,
+                                    device=dev) * (1.0 / math.sqrt(width))
+            host["res"] = torch.randn((nq, LAYER_HIDDEN), generator=gen, device=dev)
+            host["post"] = 1 + 0.1 * torch.randn(LAYER_HIDDEN, generator=gen, device=dev)
+            host["proj"] = torch.empty((nq, LAYER_HIDDEN), device=dev)
+            host["result"] = torch.empty((nq, LAYER_HIDDEN), device=dev)
         sets.append((host, cache))
     torch.cuda.synchronize()
 
@@ -418,6 +447,11 @@ def time_cache_workload(torch, pcl, ctx, name, steps, warmup, nsets, seed, trans
                                qheads=qh, kh_first=0, kh_end=kvh, out=host["out"].data_ptr(),
                                o_stride=qh * dim)
         ctx.launch(d)
+        if output:
+            ctx.attention_output(host["out"].data_ptr(), nq, width, host["w"].data_ptr(),
+                                 LAYER_HIDDEN, host["post"].data_ptr(), 1e-6,
+                                 host["res"].data_ptr(), host["proj"].data_ptr(),
+                                 host["result"].data_ptr())
         cache.rollback(pending)
         return d
 
@@ -568,12 +602,16 @@ def roofline(name, r):
     spans over the timed steps."""
     kind = WORKLOADS[name][8]
     stream_s = r["stream_kernel_ms"] * 1e-3
+    if kind == "layer":
+        # the layer's bytes span several kernels (the output block has no
+        # timing span): the whole step is the timed unit
+        stream_s = r["ms"] * 1e-3
     if kind == "output" and nq_of(name) > 32:
         ach = r["algorithmic_flops"] / stream_s / 1e12
         roof = {"bound": "mfma", "achieved": ach, "peak": FP64_MFMA_PEAK_TFS,
                 "unit": "TFLOP/s", "frac": ach / FP64_MFMA_PEAK_TFS,
                 "traffic": traffic_bytes(name)}
-    elif kind in ("decode", "cache", "step", "transform", "output"):
+    elif kind in ("decode", "cache", "step", "layer", "transform", "output"):
         ach = r["algorithmic_bytes"] / stream_s / 1e9
         roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": ach / HBM_PEAK_GBS, "traffic": traffic_bytes(name)}
@@ -657,7 +695,7 @@ def main():
             r["frac_mfma_fp64"] = r["TFLOP/s"] / FP64_MFMA_PEAK_TFS
         elif kind == "host":
             r["pcie_inclusive_GB/s"] = r["GB/s"]
-        elif kind in ("decode", "cache", "step", "transform", "output"):
+        elif kind in ("decode", "cache", "step", "layer", "transform", "output"):
             r["frac_hbm"] = r["GB/s"] / HBM_PEAK_GBS
         else:
             r["frac_mfma"] = r["TFLOP/s"] / FP32_MFMA_PEAK_TFS
@@ -705,7 +743,7 @@ def main():
         roof = {"bound": "pcie", "achieved": value, "peak": None, "unit": "GB/s",
                 "frac": None, "traffic": None}
         roof["kernel"] = hr["kernel"]
-    elif kind in ("decode", "cache", "step", "transform") or (kind == "output" and nq <= 32):
+    elif kind in ("decode", "cache", "step", "layer", "transform") or (kind == "output" and nq <= 32):
         value, unit, metric = hr["GB/s"], "GB/s", "decode-attn HBM GB/s at 32K KV"
         roof = roofline(head, hr)
     else:

@@ -30,6 +30,11 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     # the same prefill and canvas at the global-layer geometry (16/2, d 512)
     ("prefill_4k_d512", 274_945_015_808, None, 8_390_656),
     ("canvas_256x2304_d512", 19_327_352_832, None, None),
+    # the output block of one token: W (2816 x 4096) + attended row + residual
+    # + result, 2 x 4096 x 2816 flops
+    ("output_decode", 23_068_672, 46_176_256, None),
+    # the whole decode layer: the 32K attention plus that output block
+    ("decode_32k_layer", 536_870_912 + 23_068_672, 536_903_680 + 46_176_256, None),
 ])
 def test_algorithmic_work_matches_the_configs(name, flops, bytes_, pairs):
     f, b, p = bench.work(name)
