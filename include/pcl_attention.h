@@ -282,9 +282,10 @@ int pcl_kv_cache_read(const pcl_kv_cache *cache, int64_t first, int64_t rows, fl
                       float *values);
 /* One uncommitted step of n tokens (encode_in_place's append,
  * attention.rs:949-1080): checks total + n <= context and the byte limit
- * (check_stage, attention.rs:545-558), copies the device rows keys/values
- * ([n][kvheads][dim]) after the retained rows, advances the total and fills
- * *pending. On an error the cache is unchanged. */
+ * (check_stage, attention.rs:545-558), copies the rows keys/values
+ * ([n][kvheads][dim]; device memory of the cache's device in one launch, host
+ * memory by runtime copies) after the retained rows, advances the total and
+ * fills *pending. On an error the cache is unchanged. */
 int pcl_kv_cache_append(pcl_kv_cache *cache, const float *keys, const float *values, int64_t n,
                         pcl_kv_pending *pending);
 /* LayerCache::rollback / keep / commit (attention.rs:280-310): undo the step;

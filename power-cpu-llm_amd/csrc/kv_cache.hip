@@ -12,6 +12,7 @@
 #include "pcl_attention.h"
 
 #include <algorithm>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 
@@ -42,6 +43,56 @@ hipError_t copy_rows(pcl_kv_cache *c, float *dk, float *dv, const float *sk, con
     if (e == hipSuccess)
         e = hipMemcpyAsync(dv, sv, bytes, kind, c->ctx->stream);
     return e;
+}
+
+// Caller rows of K and V that are device memory of the cache's device are
+// copied by one launch of this kernel (blockIdx.y picks K or V) rather than
+// two runtime copies: a decode step's one-row append is then one dispatch.
+// n4 16-byte pieces per array when `wide`, else n4 floats.
+__global__ __launch_bounds__(256) void append_rows_kernel(const float *sk, const float *sv,
+                                                         float *dk, float *dv, int64_t n,
+                                                         int wide)
+{
+    const float *src = blockIdx.y ? sv : sk;
+    float *dst = blockIdx.y ? dv : dk;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
+        if (wide)
+            reinterpret_cast<float4 *>(dst)[i] = reinterpret_cast<const float4 *>(src)[i];
+        else
+            dst[i] = src[i];
+    }
+}
+
+// True when p is device memory of `device`. An unregistered host pointer
+// makes the query fail; that failure is cleared here so that it is not
+// reported by a later launch check.
+bool device_memory(const void *p, int device)
+{
+    hipPointerAttribute_t a;
+    if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return a.type == hipMemoryTypeDevice && a.device == device;
+}
+
+// Appended caller rows: one kernel launch for device rows on the cache's
+// device, runtime copies otherwise (host or peer memory).
+hipError_t append_rows(pcl_kv_cache *c, float *dk, float *dv, const float *sk, const float *sv,
+                       int64_t rows)
+{
+    const int dev = c->ctx->device;
+    if (!device_memory(sk, dev) || !device_memory(sv, dev))
+        return copy_rows(c, dk, dv, sk, sv, rows, hipMemcpyDefault);
+    const int64_t floats = rows * c->width;
+    const bool wide = floats % 4 == 0 && ((uintptr_t)sk | (uintptr_t)sv | (uintptr_t)dk |
+                                          (uintptr_t)dv) % 16 == 0;
+    const int64_t n = wide ? floats / 4 : floats;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 2048);
+    append_rows_kernel<<<dim3((unsigned)blocks, 2), 256, 0, c->ctx->stream>>>(sk, sv, dk, dv, n,
+                                                                             wide ? 1 : 0);
+    return hipGetLastError();
 }
 
 // A pending record of the current step: its rows start within the retained
@@ -209,8 +260,8 @@ int pcl_kv_cache_append(pcl_kv_cache *c, const float *keys, const float *values,
     const int rc = pcl::kv_cache_reserve(c, n);
     if (rc != PCL_OK)
         return rc;
-    const hipError_t e = copy_rows(c, c->k + c->len * c->width, c->v + c->len * c->width, keys,
-                                   values, n, hipMemcpyDefault);
+    const hipError_t e =
+        append_rows(c, c->k + c->len * c->width, c->v + c->len * c->width, keys, values, n);
     if (e != hipSuccess) {
         report("appending rows", e);
         return PCL_NON_FINITE_VALUE;

@@ -199,6 +199,40 @@ def test_device_cache_follows_the_oracle_through_random_steps(pcl, torch, ctx, o
 
 
 @pytest.mark.gpu
+def test_device_cache_appends_device_unaligned_and_host_rows(pcl, torch, ctx, oracle):
+    # device rows on the cache's device take the one-launch copy (16-byte
+    # pieces when aligned, floats when not); host rows take runtime copies:
+    # every source lands the same rows
+    kvh, dim = 2, 16
+    width = kvh * dim
+    cache = pcl.LayerCache(ctx, kvh, dim, 4000, None, 1 << 24)
+    ref = oracle.OracleCache(kvh, dim, 4000, None, 1 << 24)
+    for i, n in enumerate([1, 3, 64, 1, 517]):
+        k = rows_of(3000 + i, n, width)
+        v = rows_of(4000 + i, n, width)
+        kind = i % 3
+        if kind == 0:  # aligned device rows
+            tk, tv = to_dev(torch, k), to_dev(torch, v)
+            pk, pv = tk.data_ptr(), tv.data_ptr()
+        elif kind == 1:  # device rows one float past an aligned start
+            tk = to_dev(torch, np.concatenate([[np.nan], k.reshape(-1)]))
+            tv = to_dev(torch, np.concatenate([[np.nan], v.reshape(-1)]))
+            pk, pv = tk.data_ptr() + 4, tv.data_ptr() + 4
+        else:  # pageable host rows
+            hk = np.ascontiguousarray(k, dtype=np.float32)
+            hv = np.ascontiguousarray(v, dtype=np.float32)
+            pk, pv = hk.ctypes.data, hv.ctypes.data
+        cache.append(pk, pv, n)
+        ref.append(k, v, n)
+        cache.commit()
+        ref.commit()
+        torch.cuda.synchronize()
+        assert_same_cache(cache, ref, width)
+    assert ctx.sync() == 0
+    cache.close()
+
+
+@pytest.mark.gpu
 def test_device_cache_limits_match_check_stage(pcl, torch, ctx):
     # attention/tests.rs:40-47 and 270-276 on the device cache: max_bytes
     # bounds the retained plus appended K+V of a step
