@@ -16,6 +16,29 @@
 #include <cstdio>
 #include <cstring>
 
+namespace pcl {
+
+// Caller rows of K and V that are device memory of the cache's device are
+// copied by one launch of this kernel (blockIdx.y picks K or V) rather than
+// two runtime copies: a decode step's one-row append is then one dispatch.
+// n 16-byte pieces per array when `wide`, else n floats.
+__global__ __launch_bounds__(256) void append_rows_kernel(const float *sk, const float *sv,
+                                                         float *dk, float *dv, int64_t n,
+                                                         int wide)
+{
+    const float *src = blockIdx.y ? sv : sk;
+    float *dst = blockIdx.y ? dv : dk;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
+        if (wide)
+            reinterpret_cast<float4 *>(dst)[i] = reinterpret_cast<const float4 *>(src)[i];
+        else
+            dst[i] = src[i];
+    }
+}
+
+} // namespace pcl
+
 namespace {
 
 void report(const char *what, hipError_t e)
@@ -45,25 +68,6 @@ hipError_t copy_rows(pcl_kv_cache *c, float *dk, float *dv, const float *sk, con
     return e;
 }
 
-// Caller rows of K and V that are device memory of the cache's device are
-// copied by one launch of this kernel (blockIdx.y picks K or V) rather than
-// two runtime copies: a decode step's one-row append is then one dispatch.
-// n4 16-byte pieces per array when `wide`, else n4 floats.
-__global__ __launch_bounds__(256) void append_rows_kernel(const float *sk, const float *sv,
-                                                         float *dk, float *dv, int64_t n,
-                                                         int wide)
-{
-    const float *src = blockIdx.y ? sv : sk;
-    float *dst = blockIdx.y ? dv : dk;
-    const int64_t step = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
-        if (wide)
-            reinterpret_cast<float4 *>(dst)[i] = reinterpret_cast<const float4 *>(src)[i];
-        else
-            dst[i] = src[i];
-    }
-}
-
 // True when p is device memory of `device`. An unregistered host pointer
 // makes the query fail; that failure is cleared here so that it is not
 // reported by a later launch check.
@@ -90,8 +94,8 @@ hipError_t append_rows(pcl_kv_cache *c, float *dk, float *dv, const float *sk, c
                                           (uintptr_t)dv) % 16 == 0;
     const int64_t n = wide ? floats / 4 : floats;
     const int64_t blocks = std::min<int64_t>((n + 255) / 256, 2048);
-    append_rows_kernel<<<dim3((unsigned)blocks, 2), 256, 0, c->ctx->stream>>>(sk, sv, dk, dv, n,
-                                                                             wide ? 1 : 0);
+    pcl::append_rows_kernel<<<dim3((unsigned)blocks, 2), 256, 0, c->ctx->stream>>>(
+        sk, sv, dk, dv, n, wide ? 1 : 0);
     return hipGetLastError();
 }
 
