@@ -179,9 +179,15 @@ void *pcl_context_stream(pcl_context *ctx);
  * or PCL_NON_FINITE_VALUE for a launch failure. Data errors (non-finite
  * allowed score or output) are recorded in the context's device error flag.
  * Grows the context's workspace when needed (a device allocation);
- * pcl_context_reserve avoids that inside timed regions. */
+ * pcl_context_reserve avoids that inside timed regions and before a graph
+ * capture. On a stream that is capturing a graph, AUTO does not take the
+ * spread decode (its workgroups accept a published word by the launch's
+ * epoch, which every replay would repeat) but the pipelined kernel, with the
+ * same bits; an explicit PCL_KERNEL_SPREAD_KV is refused there with
+ * PCL_INVALID_PARAMETER. No counterpart in the reference (host calls only). */
 int pcl_attention_launch(pcl_context *ctx, const pcl_attention_desc *desc);
-/* Workspace bytes a descriptor needs with the kernel it would run. */
+/* Workspace bytes a descriptor needs with the kernel it would run (under
+ * AUTO, also enough for the kernel a graph capture of it takes). */
 size_t pcl_attention_workspace_bytes(const pcl_attention_desc *desc);
 
 /* Bytes of the per-GPU scratch array of pcl_attention_launch_noalloc. */

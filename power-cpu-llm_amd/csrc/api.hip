@@ -770,13 +770,20 @@ size_t pcl_attention_workspace_bytes(const pcl_attention_desc *desc)
 {
     if (!desc)
         return 0;
+    const int64_t group = desc->kvheads ? desc->qheads / desc->kvheads : 0;
+    const int64_t h_lo = desc->kh_first * group, h_hi = desc->kh_end * group;
     Plan plan;
-    if (make_plan(*desc, desc->kh_first * (desc->kvheads ? desc->qheads / desc->kvheads : 0),
-                  desc->kh_end * (desc->kvheads ? desc->qheads / desc->kvheads : 0),
-                  desc->kh_first * (desc->kvheads ? desc->qheads / desc->kvheads : 0),
-                  &plan) != PCL_OK)
+    if (make_plan(*desc, h_lo, h_hi, h_lo, &plan) != PCL_OK)
         return 0;
-    return plan.ws_floats * sizeof(float);
+    size_t floats = plan.ws_floats;
+    if (plan.kernel == PCL_KERNEL_SPREAD_KV && desc->kernel == PCL_KERNEL_AUTO) {
+        // the same launch captured into a graph takes the pipelined kernel
+        pcl_attention_desc d = *desc;
+        d.kernel = PCL_KERNEL_PIPE_KV;
+        if (make_plan(d, h_lo, h_hi, h_lo, &plan) == PCL_OK)
+            floats = std::max(floats, plan.ws_floats);
+    }
+    return floats * sizeof(float);
 }
 
 int pcl_attention_resolve_kernel(const pcl_attention_desc *desc)
@@ -791,16 +798,57 @@ int pcl_attention_resolve_kernel(const pcl_attention_desc *desc)
     return plan.kernel;
 }
 
+} // extern "C"
+
+namespace {
+
+// True while `stream` is being captured into a graph (an error of the query
+// itself counts as not capturing and is cleared).
+bool capturing(hipStream_t stream)
+{
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &st) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return st != hipStreamCaptureStatusNone;
+}
+
+// The plan of a device-resident launch on ctx's stream. A launch being
+// captured into a graph never takes the spread decode: its workgroups accept
+// a published word by the launch's epoch, a kernel argument that every
+// replay of the graph repeats, so one replay could take the previous
+// replay's words. AUTO then takes the pipelined kernel (the same bits); an
+// explicit request for the spread decode is refused.
+int launch_plan(pcl_context *ctx, const pcl_attention_desc &desc, Plan *plan)
+{
+    if (desc.kvheads <= 0 || desc.qheads % desc.kvheads != 0)
+        return PCL_INVALID_SHAPE;
+    const int64_t group = desc.qheads / desc.kvheads;
+    const int64_t h_lo = desc.kh_first * group, h_hi = desc.kh_end * group;
+    int rc = make_plan(desc, h_lo, h_hi, h_lo, plan);
+    if (rc != PCL_OK || plan->empty || plan->kernel != PCL_KERNEL_SPREAD_KV)
+        return rc;
+    (void)hipSetDevice(ctx->device);
+    if (!capturing(ctx->stream))
+        return PCL_OK;
+    if (desc.kernel != PCL_KERNEL_AUTO)
+        return PCL_INVALID_PARAMETER;
+    pcl_attention_desc d = desc;
+    d.kernel = PCL_KERNEL_PIPE_KV;
+    return make_plan(d, h_lo, h_hi, h_lo, plan);
+}
+
+} // namespace
+
+extern "C" {
+
 int pcl_attention_launch(pcl_context *ctx, const pcl_attention_desc *desc)
 {
     if (!ctx || !desc)
         return PCL_INVALID_SHAPE;
-    if (desc->kvheads <= 0 || desc->qheads % desc->kvheads != 0)
-        return PCL_INVALID_SHAPE;
-    const int64_t group = desc->qheads / desc->kvheads;
     Plan plan;
-    const int rc = make_plan(*desc, desc->kh_first * group, desc->kh_end * group,
-                             desc->kh_first * group, &plan);
+    const int rc = launch_plan(ctx, *desc, &plan);
     if (rc != PCL_OK)
         return rc;
     (void)hipSetDevice(ctx->device);
@@ -811,12 +859,8 @@ int pcl_attention_launch_noalloc(pcl_context *ctx, const pcl_attention_desc *des
 {
     if (!ctx || !desc)
         return PCL_INVALID_SHAPE;
-    if (desc->kvheads <= 0 || desc->qheads % desc->kvheads != 0)
-        return PCL_INVALID_SHAPE;
-    const int64_t group = desc->qheads / desc->kvheads;
     Plan plan;
-    const int rc = make_plan(*desc, desc->kh_first * group, desc->kh_end * group,
-                             desc->kh_first * group, &plan);
+    const int rc = launch_plan(ctx, *desc, &plan);
     if (rc != PCL_OK)
         return rc;
     if (plan.empty)
