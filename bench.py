@@ -418,6 +418,7 @@ def time_cache_workload(torch, pcl, ctx, name, steps, warmup, nsets, seed, trans
     for i in range(nsets):
         q, k, v = make_inputs(torch, name, seed + 1000 * i)
         cache = pcl.LayerCache(ctx, kvh, dim, nkeys + 1, window, 1 << 40)
+        cache.reserve_rows(nkeys + 1)  # no growth (and no free) on the appends
         cache.append(k.data_ptr(), v.data_ptr(), nkeys - 1)
         cache.commit()
         out = torch.empty((nq, qh, dim), device="cuda:0", dtype=torch.float32)

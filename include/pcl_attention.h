@@ -273,6 +273,14 @@ int pcl_kv_cache_create(pcl_context *ctx, int64_t kvheads, int64_t dim, int64_t 
                         int64_t window, size_t max_bytes, pcl_kv_cache **out);
 /* Destroy caches (and head transforms) before the context they were made on. */
 void pcl_kv_cache_destroy(pcl_kv_cache *cache);
+/* Room for `rows` rows in the cache's buffers now (at most what max_bytes
+ * allows), so that appends up to that many retained plus appended rows do not
+ * reallocate (growth frees the old buffers, and on MI355X a process that
+ * frees device memory streams more slowly afterwards). Grow-only; call it
+ * between steps (moving the rows invalidates a pending record).
+ * PCL_RESOURCE_LIMIT if the buffers cannot be allocated. No counterpart in
+ * the reference (its caches are host vectors). */
+int pcl_kv_cache_reserve_rows(pcl_kv_cache *cache, int64_t rows);
 /* LayerCache::total_tokens / retained_tokens (attention.rs:268-273). */
 int64_t pcl_kv_cache_total_tokens(const pcl_kv_cache *cache);
 int64_t pcl_kv_cache_retained_tokens(const pcl_kv_cache *cache);

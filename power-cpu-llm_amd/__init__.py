@@ -61,6 +61,7 @@ EXPORTS = (
     "pcl_context_timing",
     "pcl_kv_cache_create",
     "pcl_kv_cache_destroy",
+    "pcl_kv_cache_reserve_rows",
     "pcl_kv_cache_total_tokens",
     "pcl_kv_cache_retained_tokens",
     "pcl_kv_cache_view",
@@ -186,6 +187,7 @@ def load():
             ("pcl_kv_cache_create", ctypes.c_int, [vp, i64, i64, i64, i64, sz,
                                                    ctypes.POINTER(vp)]),
             ("pcl_kv_cache_destroy", None, [vp]),
+            ("pcl_kv_cache_reserve_rows", ctypes.c_int, [vp, i64]),
             ("pcl_kv_cache_total_tokens", i64, [vp]),
             ("pcl_kv_cache_retained_tokens", i64, [vp]),
             ("pcl_kv_cache_view", ctypes.c_int, [vp, ctypes.POINTER(vp), ctypes.POINTER(vp),
@@ -472,6 +474,11 @@ class LayerCache:
         if rc != OK:
             raise AttentionError(rc)
         ctx._children.add(self)
+
+    def reserve_rows(self, rows):
+        """Room for `rows` rows in the device buffers now (grow-only; between
+        steps), so that appends up to that many rows do not reallocate."""
+        self._check(self.lib.pcl_kv_cache_reserve_rows(self.handle, int(rows)))
 
     def close(self):
         if self.handle:

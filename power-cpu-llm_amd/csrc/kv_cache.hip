@@ -112,24 +112,17 @@ bool valid_pending(const pcl_kv_cache *c, const pcl_kv_pending *p)
 
 namespace pcl {
 
-int kv_cache_reserve(pcl_kv_cache *c, int64_t n)
+// Rows the cache's byte limit allows in its buffers.
+int64_t row_limit(const pcl_kv_cache *c)
 {
-    // check_stage (attention.rs:543-558): the next position within the
-    // context, the retained plus appended K+V within the byte limit
-    if (n > c->context - c->total)
-        return PCL_RESOURCE_LIMIT;
+    return (int64_t)(c->max_bytes / ((size_t)c->width * 2 * sizeof(float)));
+}
+
+// New buffers of `cap` rows (at least the retained rows), the retained rows
+// moved to their start and the old buffers freed.
+int move_to_buffers(pcl_kv_cache *c, int64_t cap)
+{
     const int64_t retained = c->len - c->start;
-    const double bytes = (double)(retained + n) * (double)c->width * 2.0 * sizeof(float);
-    if (bytes > (double)c->max_bytes)
-        return PCL_RESOURCE_LIMIT;
-    (void)hipSetDevice(c->ctx->device);
-    if (c->len + n <= c->cap)
-        return PCL_OK;
-    // new buffers for at least twice the step's rows (a Vec's growth),
-    // holding at most what the byte limit allows, retained rows first
-    const int64_t limit = (int64_t)(c->max_bytes / ((size_t)c->width * 2 * sizeof(float)));
-    const int64_t need = retained + n;
-    const int64_t cap = std::max(need, std::min(2 * need, limit));
     float *nk = nullptr, *nv = nullptr;
     hipError_t e = hipMalloc(&nk, (size_t)cap * c->width * sizeof(float));
     if (e == hipSuccess)
@@ -157,6 +150,26 @@ int kv_cache_reserve(pcl_kv_cache *c, int64_t n)
     c->len = retained;
     c->start = 0;
     return PCL_OK;
+}
+
+int kv_cache_reserve(pcl_kv_cache *c, int64_t n)
+{
+    // check_stage (attention.rs:543-558): the next position within the
+    // context, the retained plus appended K+V within the byte limit
+    if (n > c->context - c->total)
+        return PCL_RESOURCE_LIMIT;
+    const int64_t retained = c->len - c->start;
+    const double bytes = (double)(retained + n) * (double)c->width * 2.0 * sizeof(float);
+    if (bytes > (double)c->max_bytes)
+        return PCL_RESOURCE_LIMIT;
+    (void)hipSetDevice(c->ctx->device);
+    if (c->len + n <= c->cap)
+        return PCL_OK;
+    // new buffers for at least twice the step's rows (a Vec's growth),
+    // holding at most what the byte limit allows, retained rows first
+    const int64_t limit = row_limit(c);
+    const int64_t need = retained + n;
+    return move_to_buffers(c, std::max(need, std::min(2 * need, limit)));
 }
 
 void kv_cache_advance_rows(pcl_kv_cache *c, int64_t n, pcl_kv_pending *pending)
@@ -193,6 +206,17 @@ int pcl_kv_cache_create(pcl_context *ctx, int64_t kvheads, int64_t dim, int64_t 
     c->max_bytes = max_bytes;
     *out = c;
     return PCL_OK;
+}
+
+int pcl_kv_cache_reserve_rows(pcl_kv_cache *c, int64_t rows)
+{
+    if (!c || rows < 0)
+        return PCL_INVALID_SHAPE;
+    const int64_t cap = std::min(rows, pcl::row_limit(c));
+    if (cap <= c->cap)
+        return PCL_OK;
+    (void)hipSetDevice(c->ctx->device);
+    return pcl::move_to_buffers(c, cap);
 }
 
 void pcl_kv_cache_destroy(pcl_kv_cache *c)

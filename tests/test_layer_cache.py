@@ -233,6 +233,47 @@ def test_device_cache_appends_device_unaligned_and_host_rows(pcl, torch, ctx, or
 
 
 @pytest.mark.gpu
+def test_reserved_rows_keep_the_buffers_until_exceeded(pcl, torch, ctx, oracle):
+    # room reserved up front: appends within it keep the buffers in place;
+    # past it the cache grows as before; the rows follow the oracle's cache
+    # throughout, and a reservation past the byte limit is held to it
+    kvh, dim = 2, 16
+    width = kvh * dim
+    token = width * 2 * 4
+    cache = pcl.LayerCache(ctx, kvh, dim, 4000, None, 150 * token)
+    ref = oracle.OracleCache(kvh, dim, 4000, None, 150 * token)
+    with pytest.raises(pcl.AttentionError):
+        cache.reserve_rows(-1)
+    keep = []  # the appended device rows stay alive until the copies ran
+
+    def append(k, v, n):
+        tk, tv = to_dev(torch, k), to_dev(torch, v)
+        keep.append((tk, tv))
+        cache.append(tk.data_ptr(), tv.data_ptr(), n)
+        ref.append(k, v, n)
+        cache.commit()
+        ref.commit()
+
+    cache.reserve_rows(100)
+    k0, v0, _, _ = cache.view()
+    for i, n in enumerate([1, 40, 59]):  # 100 rows in all
+        append(rows_of(5000 + i, n, width), rows_of(6000 + i, n, width), n)
+        assert cache.view()[:2] == (k0, v0)
+        assert_same_cache(cache, ref, width)
+    cache.reserve_rows(80)  # grow-only: nothing moves
+    assert cache.view()[:2] == (k0, v0)
+    append(rows_of(7000, 3, width), rows_of(7001, 3, width), 3)
+    assert cache.view()[:2] != (k0, v0)
+    assert_same_cache(cache, ref, width)
+    cache.reserve_rows(10 ** 9)  # held to the 150-row byte limit
+    k1, v1, _, _ = cache.view()
+    append(rows_of(7002, 47, width), rows_of(7003, 47, width), 47)
+    assert cache.view()[:2] == (k1, v1)
+    assert_same_cache(cache, ref, width)
+    cache.close()
+
+
+@pytest.mark.gpu
 def test_device_cache_limits_match_check_stage(pcl, torch, ctx):
     # attention/tests.rs:40-47 and 270-276 on the device cache: max_bytes
     # bounds the retained plus appended K+V of a step
