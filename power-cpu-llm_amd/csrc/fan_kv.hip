@@ -1,0 +1,500 @@
+// Fanned chunk kernel for gfx950: one (16-row unit, 256-key chunk, KV head)
+// item over the eight waves of one workgroup.
+//
+// A chunk-split prefill or canvas whose chunk items leave a last round of
+// one chunk per row block (the canvas: 288 items of 128 rows on 256 CUs)
+// runs that chunk here, one workgroup per 16-row unit: 256 items for the
+// canvas, one per CU. A unit-chunk is 4.2 MFLOP at head dim 256 (6.8 us of
+// one CU's matrix peak), so the item is spread over all four SIMDs:
+//
+//   wave w forms the raw scores of tile w (its two 16-key blocks): the
+//   canonical score chain of attention_device.hpp, K read straight into MFMA
+//   A operands, Q^T (shared by the waves) read from LDS;
+//   the chunk's raw scores are exchanged through LDS; every wave then runs
+//   the same tile-by-tile online softmax (so all derive the same m, l and
+//   probabilities, bit for bit) and the P.V chain of its own DK/8 output
+//   dims, V of the first LT tiles from LDS (copied HBM -> LDS while the
+//   scores are formed) and of the rest from registers (requested once the
+//   score chain has consumed K).
+//
+// Each wave's K loads and V copies are issued at once, so the item takes
+// about two memory round trips instead of the pipelined kernel's chain of
+// sixteen (eight in its wide layout).
+//
+// Output: with merge_out (the launch's last chunk, one span, the earlier
+// chunks' partials already written by the chunk items) every thread merges
+// the earlier partials of its rows and dims in ascending order and then its
+// own chunk state, which is the combine's ordered merge bit for bit (empty
+// slots merge as no-ops), and writes the output; otherwise it writes the
+// chunk partial for the combine kernels.
+#include "attention_device.hpp"
+
+#include <atomic>
+
+namespace pcl {
+
+constexpr int kFanWaves = 8;
+constexpr int kFanThreads = 64 * kFanWaves;
+
+// LDS of a fanned item: region A holds Q (row-major, swizzled) during the
+// score chains and the chunk's raw scores after them; region B
+// holds V of the first LT tiles, key-major.
+template <int DK> struct FanLds {
+    // tiles of V in LDS: 128 KiB of them (all eight at head dim 128)
+    static constexpr int LT = DK >= 256 ? 4 : kTilesPerChunk;
+    static constexpr int qFloats = kRows * DK;
+    static constexpr int sFloats = 2 * kTilesPerChunk * 4 * 64; // [block][r][lane]
+    static constexpr int aFloats = qFloats > sFloats ? qFloats : sFloats;
+    static constexpr int vFloats = LT * kTile * DK;
+    static constexpr size_t bytes = (size_t)(aFloats + vFloats) * sizeof(float);
+};
+
+typedef __attribute__((address_space(3))) void *fan_lptr_t;
+typedef const __attribute__((address_space(1))) void *fan_gptr_t;
+
+// s_waitcnt immediate for vmcnt(n) alone (gfx9 encoding: vmcnt in bits 3:0
+// and 15:14; expcnt 7 and lgkmcnt 15 wait for nothing). The compiler's own
+// waits know this form (an inline-asm wait they would not).
+constexpr int waitcnt_vm(int n)
+{
+    return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8);
+}
+
+// The same with lgkmcnt(0): every LDS access of the wave complete too.
+constexpr int waitcnt_vm_lgkm0(int n)
+{
+    return (n & 15) | ((n >> 4) << 14) | (7 << 4);
+}
+
+// A workgroup barrier that leaves vector-memory loads in flight (the caller
+// has waited for whatever the other waves must see; __syncthreads would
+// also wait for every LDS copy still in flight). The empty statements keep
+// the compiler from moving memory accesses across it.
+__device__ __forceinline__ void fan_barrier()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Earlier chunk partials a merging thread requests before the tiles run
+// (the rest, in a span of more chunks, after them).
+constexpr int kMergeHead = 8;
+
+// FULL: the head dim equals the padded head dim (no dim clamping).
+template <int DK, bool FULL, bool CAP, bool MERGE>
+__global__ __launch_bounds__(kFanThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void fan_kv_kernel(Params p, int ci)
+{
+    using LD = FanLds<DK>;
+    constexpr int NU = DK / 32;          // score chain steps
+    constexpr int VD = DK / kFanWaves;   // output dims of a wave
+    constexpr int VW = VD / 16;          // dims of a lane per key (output blocks of a wave)
+    constexpr int LT = LD::LT;
+    constexpr int RT = kTilesPerChunk - LT; // tiles of V in registers
+    static_assert(VW >= 1 && VW * 16 * kFanWaves == DK, "whole 16-dim output blocks");
+    constexpr int NV = LT * kTile * DK / 256 / kFanWaves; // V copies (1 KiB each) per wave
+    static_assert(NV * 256 * kFanWaves == LT * kTile * DK, "whole 1 KiB copies per wave");
+    extern __shared__ float lds[];
+    float *qs = lds;                   // region A: Q^T, then the raw scores
+    float *vls = lds + LD::aFloats;    // region B: V of tiles 0 .. LT-1
+
+    const int c = p.c_lo + ci;
+    // consecutive workgroups cycle over the KV heads (each XCD's L2 then
+    // serves one head's K and V when there are eight)
+    const int kvl = (int)blockIdx.x % p.nkv;
+    const int unit = (int)blockIdx.x / p.nkv;
+    const int tid = threadIdx.x;
+    const int w = tid >> 6;
+    const int lane = tid & 63;
+    const int col = lane & 15;
+    const int g = lane >> 4;
+    const int kh = p.kh_first + kvl;
+    const int row = unit * kRows + col;
+    const bool rin = row < p.nrows;
+    const int64_t cbase = (int64_t)c * kChunk;
+    const int64_t klast = p.nkeys - 1;
+    const int64_t hoff = (int64_t)kh * p.dim;
+    const int d0 = VD * w; // the wave's output dims
+
+    // Q of the unit's 16 rows, HBM -> LDS (region A, unscaled): copy j moves
+    // 1 KiB (256 floats) of the row-major [16][DK] block, each row's 16-byte
+    // pieces XOR-swizzled by (row & 7) so that the eight rows an MFMA operand
+    // read touches hit distinct banks. Padding rows copy the last real row
+    // and dims past the head's last its first dims: both read as zero below.
+    constexpr int NQC = kRows * DK / 256 / kFanWaves; // Q copies per wave
+    static_assert(NQC * 256 * kFanWaves == kRows * DK, "whole 1 KiB copies per wave");
+#pragma unroll
+    for (int i = 0; i < NQC; ++i) {
+        const int j = w * NQC + i;
+        const int f = 256 * j + 4 * lane;
+        const int r = f / DK;
+        const int qd = 4 * (((f % DK) / 4) ^ (r & 7));
+        const int qrow = min(unit * kRows + r, p.nrows - 1);
+        const int query = qrow / p.group;
+        const int h = kh * p.group + qrow % p.group;
+        const float *qp = p.q + (int64_t)query * p.q_stride + (int64_t)h * p.dim +
+                          (FULL || qd < p.dim ? qd : 0);
+        __builtin_amdgcn_global_load_lds((fan_gptr_t)qp, (fan_lptr_t)(qs + 256 * j), 16, 0, 0);
+    }
+    // K of tile w (blocks 2w, 2w + 1) straight into MFMA A operands:
+    // kb[b][u][hh] = K[key 32w + 16b + col][32u + 8g + 4hh ..]
+    f4 kb[2][NU][2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        const int64_t key = cbase + kTile * w + 16 * b + col;
+        const float *kp = key_row(p, key < klast ? key : klast) + hoff;
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int d = 32 * u + 8 * g + 4 * hh;
+                const bool din = FULL || d < p.dim;
+                const f4 x = ldg4(kp + (din ? d : 0));
+                kb[b][u][hh] = din ? x : f4{0.f, 0.f, 0.f, 0.f};
+            }
+    }
+    // (the V copies below must not be scheduled ahead of the K loads: the
+    // score chains wait for K by count)
+    __builtin_amdgcn_sched_barrier(0);
+    // V of tiles 0 .. LT-1, HBM -> LDS: copy j moves 1 KiB of the key-major
+    // region. A dim past the head's last copies the head's first dims
+    // instead (that output is dropped); keys past the last copy the last key
+    // (masked).
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int j = w * NV + i;
+        const int f = 256 * j + 4 * lane;
+        const int key = f / DK;
+        const int vd = f % DK;
+        const int64_t kt = cbase + key;
+        const float *vp = value_row(p, kt < klast ? kt : klast) + hoff +
+                          (FULL || vd < p.dim ? vd : 0);
+        __builtin_amdgcn_global_load_lds((fan_gptr_t)vp, (fan_lptr_t)(vls + 256 * j), 16, 0, 0);
+    }
+    // Q and K have landed (the V copies may stay in flight): every wave's Q
+    // copies are in LDS after the barrier.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(NV));
+    fan_barrier();
+
+    // the score chains of blocks 2w and 2w + 1, B operands
+    // Q[row][32u + 8g + jj] * q_scale (zero for padding rows and dims)
+    f4 acc[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+        float q[8];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const int c4 = 8 * u + 2 * g + hh;
+            const bool qin = rin && (FULL || 4 * c4 < p.dim);
+            const f4 x = *(const f4 *)(qs + col * DK + 4 * (c4 ^ (col & 7))) * p.q_scale;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                q[4 * hh + j] = qin ? x[j] : 0.f;
+        }
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+                acc[b] = mfma(kb[b][u][jj >> 2][jj & 3], q[jj], acc[b]);
+    }
+
+    // V of tiles LT .. 7 for the wave's dims, into registers now that K is
+    // consumed: vr[t - LT][b][r][x] = V[key 32t + 16b + 4g + r][d0 + VW col + x]
+    float vr[RT > 0 ? RT : 1][2][4][VW];
+#pragma unroll
+    for (int t = LT; t < kTilesPerChunk; ++t)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t kt = cbase + kTile * t + 16 * b + 4 * g + r;
+                const int vd = d0 + VW * col;
+                const float *vp = value_row(p, kt < klast ? kt : klast) + hoff +
+                                  (FULL || vd < p.dim ? vd : 0);
+                if constexpr (VW == 2) {
+                    const f2 x = ldg2(vp);
+                    vr[t - LT][b][r][0] = x.x;
+                    vr[t - LT][b][r][1] = x.y;
+                } else {
+#pragma unroll
+                    for (int x = 0; x < VW; ++x)
+                        vr[t - LT][b][r][x] = ldg(vp + x);
+                }
+            }
+
+    // the raw scores into region A once every wave has read Q^T; then the
+    // V copies have landed (each wave waits for its own, the barrier for
+    // all: only the register loads above may still be in flight)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            qs[((2 * w + b) * 4 + r) * 64 + lane] = acc[b][r];
+    constexpr int NVR = RT * 8 * (VW == 2 ? 1 : VW); // V register loads in flight
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(NVR));
+    fan_barrier();
+
+    // The merge's own layout (after the tiles): thread tid owns row
+    // mrow = tid / 32 of the unit and the f4 columns mq(k) = tid % 32 + 32k
+    // (k < NK), so a wave's loads of a chunk partial are two rows' contiguous
+    // bytes. With MERGE, the earlier chunks' partials of the first kMergeHead
+    // chunks are requested now: they land while the tiles run.
+    constexpr int NK = DK / 4 / 32;
+    const int mrow = unit * kRows + tid / 32;
+    const bool mrin = mrow < p.nrows;
+    const int64_t mslot0 = ((int64_t)kvl * p.nrows_pad + (mrin ? mrow : 0)) * p.nch;
+    f2 eml[MERGE ? kMergeHead : 1];
+    f4 eo[MERGE ? kMergeHead : 1][NK];
+    if constexpr (MERGE) {
+#pragma unroll
+        for (int c0 = 0; c0 < kMergeHead; ++c0) {
+            // slots past ci re-read the last earlier chunk (not merged)
+            const int64_t cc = mslot0 + (c0 < ci ? c0 : ci - 1);
+            eml[c0] = ldg2(p.ws_ml + 2 * cc);
+#pragma unroll
+            for (int k = 0; k < NK; ++k)
+                eo[c0][k] = ldg4(p.ws_o + cc * p.dk + 4 * (tid % 32 + 32 * k));
+        }
+    }
+
+    // Online softmax (the same on every wave) and the P.V chains of the
+    // wave's VW output blocks, tile by tile. Output block x: A operand
+    // V[key][d0 + VW col + x], so O[x][i] is dim d0 + VW (4g + i) + x.
+    float m = kNegInf, l = 0.f;
+    f4 O[VW];
+#pragma unroll
+    for (int x = 0; x < VW; ++x)
+        O[x] = f4{0.f, 0.f, 0.f, 0.f};
+    bool bad = false;
+    const ChunkKeys ck = chunk_keys(p, row, cbase);
+    auto tile_step = [&](int t, const bool ok[2][4]) {
+        float sv[2][4], pr[2][4];
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                sv[b][r] = qs[((2 * t + b) * 4 + r) * 64 + lane];
+        cap_scores<CAP>(p, sv);
+        bad |= bad_scores(sv, ok);
+        const float mn = fmaxf(m, tile_max(sv, ok));
+        const float ms = safe_max(mn);
+        const float alpha = fexp(m - ms);
+        const float rs = tile_probs(sv, ok, ms, pr);
+        l = __builtin_fmaf(l, alpha, rs);
+        m = mn;
+#pragma unroll
+        for (int x = 0; x < VW; ++x)
+            O[x] = O[x] * alpha;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float va[VW];
+                if (t < LT) {
+                    const float *vp = vls + (kTile * t + 16 * b + 4 * g + r) * DK + d0 + VW * col;
+                    if constexpr (VW == 2) {
+                        const f2 y = *(const f2 *)vp;
+                        va[0] = y.x;
+                        va[1] = y.y;
+                    } else {
+#pragma unroll
+                        for (int x = 0; x < VW; ++x)
+                            va[x] = vp[x];
+                    }
+                } else {
+#pragma unroll
+                    for (int x = 0; x < VW; ++x)
+                        va[x] = vr[t >= LT ? t - LT : 0][b][r][x];
+                }
+#pragma unroll
+                for (int x = 0; x < VW; ++x)
+                    O[x] = mfma(va[x], pr[b][r], O[x]);
+            }
+    };
+    // A chunk that every real row of the unit sees whole needs no per-key
+    // test (padding rows then count as allowed: their columns never reach a
+    // real row's state). Otherwise a tile with no allowed key for any row of
+    // the unit is skipped, which leaves the state bit-unchanged.
+    if (!p.mask && __all(!rin || (ck.lo <= 0 && ck.hi >= kChunk - 1))) {
+        const bool ok[2][4] = {{true, true, true, true}, {true, true, true, true}};
+#pragma unroll
+        for (int t = 0; t < kTilesPerChunk; ++t)
+            tile_step(t, ok);
+    } else {
+#pragma unroll
+        for (int t = 0; t < kTilesPerChunk; ++t) {
+            bool ok[2][4];
+            const bool any = tile_keys(ck, t, g, ok);
+            if (__any(any))
+                tile_step(t, ok);
+        }
+    }
+    if (bad && w == 0)
+        atomicOr(p.err, kErrScore);
+
+    // The chunk state into region B (free once every wave is past its
+    // tiles), row-major [16][DK] with each row's f4 columns XOR-swizzled by
+    // (row & 7), then (m, l) per row: lane (col, g) holds the 4 VW
+    // consecutive dims d0 + 4 VW g .. of row col (dim d0 + VW (4g + i) + x
+    // is O[x][i]).
+    float *ost = vls;
+    float *mlst = vls + kRows * DK;
+    fan_barrier();
+#pragma unroll
+    for (int k = 0; k < VW; ++k) {
+        f4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int n = 4 * k + e;
+            v[e] = O[n % VW][n / VW];
+        }
+        const int c4 = (d0 + 4 * VW * g + 4 * k) / 4;
+        *(f4 *)(ost + col * DK + 4 * (c4 ^ (col & 7))) = v;
+    }
+    if (w == 0 && g == 0) {
+        mlst[2 * col] = m;
+        mlst[2 * col + 1] = l;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (!mrin)
+        return;
+    const int mr = tid / 32; // the merge row within the unit
+    const float mm = mlst[2 * mr], ml = mlst[2 * mr + 1];
+    f4 ov[NK];
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+        const int c4 = tid % 32 + 32 * k;
+        ov[k] = *(const f4 *)(ost + mr * DK + 4 * (c4 ^ (mr & 7)));
+    }
+    if constexpr (!MERGE) { // chunk partial for the combine kernels
+        const int64_t slot = mslot0 + ci;
+        float *wo = p.ws_o + slot * p.dk;
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+            const int d = 4 * (tid % 32 + 32 * k);
+            if (FULL || d < p.dim)
+                stg4(wo + d, ov[k]);
+        }
+        if (tid % 32 == 0) {
+            stg(p.ws_ml + 2 * slot, mm);
+            stg(p.ws_ml + 2 * slot + 1, ml);
+        }
+        return;
+    } else {
+        const int query = mrow / p.group;
+        const int h = kh * p.group + mrow % p.group;
+        if (h < p.h_lo || h >= p.h_hi)
+            return;
+        float *o = p.out + (int64_t)query * p.o_stride + (int64_t)(h - p.h_base) * p.dim;
+        bool nonfinite = false;
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+            const int d = 4 * (tid % 32 + 32 * k);
+            if (!FULL && d >= p.dim)
+                continue;
+            // the span's earlier chunks in ascending order (the combine's
+            // order, without its empty slots, which merge as no-ops), then
+            // this chunk, the span's last; then the span into the empty total
+            Merged4 sv = {kNegInf, 0.f, f4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+            for (int c0 = 0; c0 < kMergeHead; ++c0)
+                if (c0 < ci)
+                    merge_into4(sv, eml[c0].x, eml[c0].y, eo[c0][k]);
+            for (int c0 = kMergeHead; c0 < ci; ++c0) {
+                const int64_t cc = mslot0 + c0;
+                const f2 x = ldg2(p.ws_ml + 2 * cc);
+                merge_into4(sv, x.x, x.y, ldg4(p.ws_o + cc * p.dk + d));
+            }
+            merge_into4(sv, mm, ml, ov[k]);
+            const MergeFactors f = merge_factors(kNegInf, sv.M);
+            const float L = merge_value(0.f, sv.L, f);
+            f4 v;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[j] = merge_value(0.f, sv.acc[j], f) / L;
+                nonfinite |= !is_finite(v[j]);
+            }
+            stg4(o + d, v);
+        }
+        if (nonfinite)
+            atomicOr(p.err, kErrOutput);
+    }
+}
+
+constexpr int kFanMaxDevices = 64;
+
+// Dynamic LDS above 64 KiB must be allowed once per kernel and device; a
+// repeated call from a racing thread is harmless.
+template <int DK, bool FULL, bool CAP, bool MERGE> static hipError_t configure_fan()
+{
+    static std::atomic<bool> configured[kFanMaxDevices];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return e;
+    if (dev < 0 || dev >= kFanMaxDevices)
+        return hipErrorInvalidDevice;
+    if (!configured[dev].load(std::memory_order_acquire)) {
+        e = hipFuncSetAttribute((const void *)fan_kv_kernel<DK, FULL, CAP, MERGE>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)FanLds<DK>::bytes);
+        if (e != hipSuccess)
+            return e;
+        configured[dev].store(true, std::memory_order_release);
+    }
+    return hipSuccess;
+}
+
+template <int DK, bool FULL, bool CAP, bool MERGE>
+static hipError_t launch_fan_dk(const Params &p, int ci, hipStream_t stream)
+{
+    const hipError_t e = configure_fan<DK, FULL, CAP, MERGE>();
+    if (e != hipSuccess)
+        return e;
+    fan_kv_kernel<DK, FULL, CAP, MERGE>
+        <<<dim3(p.units * p.nkv), kFanThreads, FanLds<DK>::bytes, stream>>>(p, ci);
+    return hipGetLastError();
+}
+
+template <int DK, bool MERGE>
+static hipError_t launch_fan_mode(const Params &p, int ci, hipStream_t stream)
+{
+    const bool full = p.dim == DK;
+    if (p.softcap > 0.0f)
+        return full ? launch_fan_dk<DK, true, true, MERGE>(p, ci, stream)
+                    : launch_fan_dk<DK, false, true, MERGE>(p, ci, stream);
+    return full ? launch_fan_dk<DK, true, false, MERGE>(p, ci, stream)
+                : launch_fan_dk<DK, false, false, MERGE>(p, ci, stream);
+}
+
+template <int DK>
+static hipError_t launch_fan_cap(const Params &p, int ci, bool merge_out, hipStream_t stream)
+{
+    return merge_out ? launch_fan_mode<DK, true>(p, ci, stream)
+                     : launch_fan_mode<DK, false>(p, ci, stream);
+}
+
+// Whether launch chunk items at padded head dim dk can run fanned.
+bool fan_supported(int dk)
+{
+    return dk == 128 || dk == 256;
+}
+
+// The launch's chunk ci (its last) as one fanned item per (16-row unit, KV
+// head). merge_out: the launch is one span and every other chunk's partial
+// is written; the output is then the merged result. Otherwise the chunk's
+// partial is written for the combine kernels.
+hipError_t launch_fan_chunk(const Params &p, int ci, bool merge_out, hipStream_t stream)
+{
+    if (merge_out && (p.nspan != 1 || ci < 1 || ci != p.nch - 1 || p.nch > kSpanChunks))
+        return hipErrorInvalidValue;
+    switch (p.dk) {
+    case 128: return launch_fan_cap<128>(p, ci, merge_out, stream);
+    case 256: return launch_fan_cap<256>(p, ci, merge_out, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+} // namespace pcl

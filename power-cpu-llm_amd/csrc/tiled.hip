@@ -30,6 +30,8 @@ namespace pcl {
 
 hipError_t launch_pipe_kv_chunks(const Params &p, int c0, int n, bool merge_out,
                                  hipStream_t stream);
+hipError_t launch_fan_chunk(const Params &p, int ci, bool merge_out, hipStream_t stream);
+bool fan_supported(int dk);
 
 constexpr int kTiledWaves = 8;
 constexpr int kTiledRows = kTiledWaves * kRows; // 128
@@ -485,7 +487,8 @@ static hipError_t launch_tiled_dk(const Params &p, int split, hipStream_t stream
     // the tail runs after every other chunk's partial is written: with all
     // chunks in one span it merges them into the output itself
     const bool merge_out = p.nspan == 1;
-    e = launch_pipe_kv_chunks(p, p.nch - tail, tail, merge_out, stream);
+    e = fan_supported(DK) ? launch_fan_chunk(p, p.nch - 1, merge_out, stream)
+                          : launch_pipe_kv_chunks(p, p.nch - tail, tail, merge_out, stream);
     if (e == hipSuccess && merge_out)
         *merged = true;
     return e;

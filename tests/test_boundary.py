@@ -187,6 +187,8 @@ def _resource_remarks(source):
     ("spread_kv.hip", "_ZN3pcl16spread_kv_kernelILi256ELb1ELb0EEEvNS_6ParamsE"),
     ("pipe_kv.hip", "_ZN3pcl14pipe_kv_kernelILi256ELi1ELb1ELb0EEEvNS_6ParamsEi"),
     ("pipe_kv.hip", "_ZN3pcl14pipe_kv_kernelILi512ELi1ELb1ELb1EEEvNS_6ParamsEi"),
+    ("fan_kv.hip", "_ZN3pcl13fan_kv_kernelILi256ELb1ELb0ELb1EEEvNS_6ParamsEi"),
+    ("fan_kv.hip", "_ZN3pcl13fan_kv_kernelILi256ELb0ELb1ELb0EEEvNS_6ParamsEi"),
 ])
 def test_hot_kernels_do_not_spill_registers(source, kernel):
     # a spill in these kernels costs every tile or block: the prefill once

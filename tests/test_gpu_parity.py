@@ -416,6 +416,11 @@ DESC_CASES = [
     # chunk-split kernel runs the last chunk as single-wave workgroups
     (16, 8, 64, 256, 2304, 0, 0, 0),
     (16, 8, 128, 256, 2304, 1, 700, 2048),
+    # the same last round fanned over a workgroup's eight waves: at a padded
+    # head dim (208 -> 256), and over two spans (17 chunks: the fanned chunk
+    # writes its partial for the combine instead of merging the output)
+    (16, 8, 208, 256, 2304, 1, 0, 2048),
+    (16, 8, 256, 256, 4352, 0, 0, 0),
     # head dim 512 (and 320, padded to 512) through the wave-pair tiled
     # kernel, one pass and one chunk per block
     (16, 2, 512, 100, 700, 1, 0, 600),
