@@ -2,31 +2,37 @@
 // item over the eight waves of one workgroup.
 //
 // A chunk-split prefill or canvas whose chunk items leave a last round of
-// one chunk per row block (the canvas: 288 items of 128 rows on 256 CUs)
-// runs that chunk here, one workgroup per 16-row unit: 256 items for the
-// canvas, one per CU. A unit-chunk is 4.2 MFLOP at head dim 256 (6.8 us of
-// one CU's matrix peak), so the item is spread over all four SIMDs:
+// one chunk per row block (the canvas: 288 items of 128 rows on 256 CUs; at
+// head dim 512, 576 items of 64 rows) runs that chunk here, one workgroup
+// per 16-row unit: 256 items for either canvas, one per CU. A unit-chunk is
+// 4.2 MFLOP at head dim 256 (6.8 us of one CU's matrix peak), so the item
+// is spread over all four SIMDs:
 //
 //   wave w forms the raw scores of tile w (its two 16-key blocks): the
 //   canonical score chain of attention_device.hpp, K read straight into MFMA
-//   A operands, Q^T (shared by the waves) read from LDS;
-//   the chunk's raw scores are exchanged through LDS; every wave then runs
-//   the same tile-by-tile online softmax (so all derive the same m, l and
-//   probabilities, bit for bit) and the P.V chain of its own DK/8 output
-//   dims, V of the first LT tiles from LDS (copied HBM -> LDS while the
-//   scores are formed) and of the rest from registers (requested once the
-//   score chain has consumed K).
+//   A operands (at head dim 512 in four pieces, two in flight), Q (shared
+//   by the waves) read from LDS;
+//   wave w takes its tile's maximum; after a barrier every wave runs the
+//   running-maximum chain over the tile maxima, and wave w forms its tile's
+//   probabilities and row sum against the running maximum at its tile;
+//   after a second barrier every wave runs the l chain and the P.V chain of
+//   its own DK/8 output dims over all eight tiles, probabilities from LDS,
+//   V of the first LT tiles from LDS (copied HBM -> LDS while the scores are
+//   formed) and of the rest from registers (requested once the score chain
+//   has consumed K, VB tiles in flight).
 //
-// Each wave's K loads and V copies are issued at once, so the item takes
-// about two memory round trips instead of the pipelined kernel's chain of
-// sixteen (eight in its wide layout).
+// Every value is the one the sequential per-tile online softmax forms (the
+// same operations on the same operands in the same order), so the results
+// are the other kernels' bits; each wave computes one tile's exponentials
+// instead of all eight.
 //
 // Output: with merge_out (the launch's last chunk, one span, the earlier
-// chunks' partials already written by the chunk items) every thread merges
-// the earlier partials of its rows and dims in ascending order and then its
-// own chunk state, which is the combine's ordered merge bit for bit (empty
-// slots merge as no-ops), and writes the output; otherwise it writes the
-// chunk partial for the combine kernels.
+// chunks' partials already written by the chunk items) the chunk state is
+// transposed through LDS to a row-contiguous layout, and every thread
+// merges the earlier partials of its row and dims in ascending order and
+// then its own chunk state, which is the combine's ordered merge bit for bit
+// (empty slots merge as no-ops), and writes the output; otherwise it writes
+// the chunk partial for the combine kernels.
 #include "attention_device.hpp"
 
 #include <atomic>
@@ -36,17 +42,38 @@ namespace pcl {
 constexpr int kFanWaves = 8;
 constexpr int kFanThreads = 64 * kFanWaves;
 
-// LDS of a fanned item: region A holds Q (row-major, swizzled) during the
-// score chains and the chunk's raw scores after them; region B
-// holds V of the first LT tiles, key-major.
-template <int DK> struct FanLds {
-    // tiles of V in LDS: 128 KiB of them (all eight at head dim 128)
-    static constexpr int LT = DK >= 256 ? 4 : kTilesPerChunk;
+template <int DK> struct FanCfg {
+    static constexpr int NU = DK / 32;        // score chain steps
+    static constexpr int VD = DK / kFanWaves; // output dims of a wave
+    static constexpr int VW = VD / 16;        // output blocks of a wave (dims of a lane per key)
+    // K of a wave's tile in pieces of KU score steps, KB pieces in flight
+    static constexpr int KU = DK > 256 ? 4 : NU;
+    static constexpr int KPN = NU / KU;
+    static constexpr int KB = KPN > 1 ? 2 : 1;
+    // V: tiles 0 .. LT-1 in LDS, the rest through registers, VB in flight
+    static constexpr int LT = DK <= 128 ? kTilesPerChunk : DK <= 256 ? 4 : 1;
+    static constexpr int RT = kTilesPerChunk - LT;
+    static constexpr int VB = RT < 4 ? RT : 4;
+    // merge: f4 columns of a thread's row; the earlier partials are
+    // requested before the tiles when they fit the registers
+    static constexpr int NK = DK / 128;
+    static constexpr bool PREFETCH = NK <= 2;
+    // LDS, in floats: region A holds Q (row-major, each row's f4 columns
+    // XOR-swizzled by (row & 7)) during the score chains and the
+    // probabilities ([tile][4b + r][lane]) after them; region B holds V of
+    // tiles 0 .. LT-1 (key-major) and after the tiles the chunk state
+    // ([row][DK], swizzled like Q, then (m, l) per row); region C holds
+    // each tile's row maxima and row sums and whether it has any allowed key
     static constexpr int qFloats = kRows * DK;
-    static constexpr int sFloats = 2 * kTilesPerChunk * 4 * 64; // [block][r][lane]
-    static constexpr int aFloats = qFloats > sFloats ? qFloats : sFloats;
-    static constexpr int vFloats = LT * kTile * DK;
-    static constexpr size_t bytes = (size_t)(aFloats + vFloats) * sizeof(float);
+    static constexpr int pFloats = kTilesPerChunk * 8 * 64;
+    static constexpr int aFloats = qFloats > pFloats ? qFloats : pFloats;
+    static constexpr int vtFloats = LT * kTile * DK;
+    static constexpr int oFloats = kRows * DK + 2 * kRows;
+    static constexpr int bFloats = vtFloats > oFloats ? vtFloats : oFloats;
+    static constexpr int cFloats = 2 * kTilesPerChunk * kRows + kTilesPerChunk;
+    static constexpr size_t bytes = (size_t)(aFloats + bFloats + cFloats) * sizeof(float);
+    static_assert(VW >= 1 && VW * 16 * kFanWaves == DK, "whole 16-dim output blocks");
+    static_assert(KU * KPN == NU, "whole K pieces");
 };
 
 typedef __attribute__((address_space(3))) void *fan_lptr_t;
@@ -77,27 +104,29 @@ __device__ __forceinline__ void fan_barrier()
     asm volatile("" ::: "memory");
 }
 
-// Earlier chunk partials a merging thread requests before the tiles run
-// (the rest, in a span of more chunks, after them).
+// Earlier chunk partials a merging thread requests in one batch (the rest,
+// in a span of more chunks, one at a time after them).
 constexpr int kMergeHead = 8;
 
-// FULL: the head dim equals the padded head dim (no dim clamping).
+// FULL: the head dim equals the padded head dim (no dim clamping). MERGE:
+// the launch's last chunk of one span, merged into the output.
 template <int DK, bool FULL, bool CAP, bool MERGE>
 __global__ __launch_bounds__(kFanThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fan_kv_kernel(Params p, int ci)
 {
-    using LD = FanLds<DK>;
-    constexpr int NU = DK / 32;          // score chain steps
-    constexpr int VD = DK / kFanWaves;   // output dims of a wave
-    constexpr int VW = VD / 16;          // dims of a lane per key (output blocks of a wave)
-    constexpr int LT = LD::LT;
-    constexpr int RT = kTilesPerChunk - LT; // tiles of V in registers
-    static_assert(VW >= 1 && VW * 16 * kFanWaves == DK, "whole 16-dim output blocks");
+    using C = FanCfg<DK>;
+    constexpr int NU = C::NU, VD = C::VD, VW = C::VW, KU = C::KU, KPN = C::KPN, KB = C::KB;
+    constexpr int LT = C::LT, VB = C::VB, NK = C::NK;
     constexpr int NV = LT * kTile * DK / 256 / kFanWaves; // V copies (1 KiB each) per wave
     static_assert(NV * 256 * kFanWaves == LT * kTile * DK, "whole 1 KiB copies per wave");
+    constexpr int NQC = kRows * DK / 256 / kFanWaves; // Q copies per wave
+    static_assert(NQC * 256 * kFanWaves == kRows * DK, "whole 1 KiB copies per wave");
     extern __shared__ float lds[];
-    float *qs = lds;                   // region A: Q^T, then the raw scores
-    float *vls = lds + LD::aFloats;    // region B: V of tiles 0 .. LT-1
+    float *qs = lds;                  // region A: Q, then the probabilities
+    float *vls = lds + C::aFloats;    // region B: V of tiles 0 .. LT-1, then the chunk state
+    float *tmx = vls + C::bFloats;    // region C: [tile][row] maxima,
+    float *trs = tmx + kTilesPerChunk * kRows; // [tile][row] row sums,
+    float *tany = trs + kTilesPerChunk * kRows; // [tile] any allowed key (0 / 1)
 
     const int c = p.c_lo + ci;
     // consecutive workgroups cycle over the KV heads (each XCD's L2 then
@@ -117,13 +146,31 @@ void fan_kv_kernel(Params p, int ci)
     const int64_t hoff = (int64_t)kh * p.dim;
     const int d0 = VD * w; // the wave's output dims
 
+    // Allowed flags of the lane's keys of tile w. A chunk that every real
+    // row of the unit sees whole needs no per-key test (padding rows then
+    // count as allowed: their columns never reach a real row's state); a
+    // tile with no allowed key for any row of the unit is skipped, which
+    // leaves the state bit-unchanged. (Mask bytes are read here, before the
+    // large loads.)
+    const ChunkKeys ck = chunk_keys(p, row, cbase);
+    bool ok[2][4];
+    bool any = true;
+    if (!p.mask && __all(!rin || (ck.lo <= 0 && ck.hi >= kChunk - 1))) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                ok[b][r] = true;
+    } else {
+        any = tile_keys(ck, w, g, ok);
+    }
+    const bool tile_any = __any(any);
+
     // Q of the unit's 16 rows, HBM -> LDS (region A, unscaled): copy j moves
     // 1 KiB (256 floats) of the row-major [16][DK] block, each row's 16-byte
     // pieces XOR-swizzled by (row & 7) so that the eight rows an MFMA operand
     // read touches hit distinct banks. Padding rows copy the last real row
     // and dims past the head's last its first dims: both read as zero below.
-    constexpr int NQC = kRows * DK / 256 / kFanWaves; // Q copies per wave
-    static_assert(NQC * 256 * kFanWaves == kRows * DK, "whole 1 KiB copies per wave");
 #pragma unroll
     for (int i = 0; i < NQC; ++i) {
         const int j = w * NQC + i;
@@ -137,23 +184,29 @@ void fan_kv_kernel(Params p, int ci)
                           (FULL || qd < p.dim ? qd : 0);
         __builtin_amdgcn_global_load_lds((fan_gptr_t)qp, (fan_lptr_t)(qs + 256 * j), 16, 0, 0);
     }
-    // K of tile w (blocks 2w, 2w + 1) straight into MFMA A operands:
-    // kb[b][u][hh] = K[key 32w + 16b + col][32u + 8g + 4hh ..]
-    f4 kb[2][NU][2];
+    // K of tile w (blocks 2w, 2w + 1) straight into MFMA A operands, piece
+    // pc covering score steps [KU pc, KU pc + KU):
+    // kb[buf][b][uu][hh] = K[key 32w + 16b + col][32u + 8g + 4hh ..], u = KU pc + uu
+    f4 kb[KB][2][KU][2];
+    auto load_k = [&](int pc, int buf) {
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-        const int64_t key = cbase + kTile * w + 16 * b + col;
-        const float *kp = key_row(p, key < klast ? key : klast) + hoff;
+        for (int b = 0; b < 2; ++b) {
+            const int64_t key = cbase + kTile * w + 16 * b + col;
+            const float *kp = key_row(p, key < klast ? key : klast) + hoff;
 #pragma unroll
-        for (int u = 0; u < NU; ++u)
+            for (int uu = 0; uu < KU; ++uu)
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const int d = 32 * u + 8 * g + 4 * hh;
-                const bool din = FULL || d < p.dim;
-                const f4 x = ldg4(kp + (din ? d : 0));
-                kb[b][u][hh] = din ? x : f4{0.f, 0.f, 0.f, 0.f};
-            }
-    }
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int d = 32 * (KU * pc + uu) + 8 * g + 4 * hh;
+                    const bool din = FULL || d < p.dim;
+                    const f4 x = ldg4(kp + (din ? d : 0));
+                    kb[buf][b][uu][hh] = din ? x : f4{0.f, 0.f, 0.f, 0.f};
+                }
+        }
+    };
+#pragma unroll
+    for (int pc = 0; pc < KB; ++pc)
+        load_k(pc, pc);
     // (the V copies below must not be scheduled ahead of the K loads: the
     // score chains wait for K by count)
     __builtin_amdgcn_sched_barrier(0);
@@ -181,29 +234,58 @@ void fan_kv_kernel(Params p, int ci)
     // Q[row][32u + 8g + jj] * q_scale (zero for padding rows and dims)
     f4 acc[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-    for (int u = 0; u < NU; ++u) {
-        float q[8];
+    for (int pc = 0; pc < KPN; ++pc) {
+        const int buf = pc % KB;
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-            const int c4 = 8 * u + 2 * g + hh;
-            const bool qin = rin && (FULL || 4 * c4 < p.dim);
-            const f4 x = *(const f4 *)(qs + col * DK + 4 * (c4 ^ (col & 7))) * p.q_scale;
+        for (int uu = 0; uu < KU; ++uu) {
+            const int u = KU * pc + uu;
+            float q[8];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                q[4 * hh + j] = qin ? x[j] : 0.f;
+            for (int hh = 0; hh < 2; ++hh) {
+                const int c4 = 8 * u + 2 * g + hh;
+                const bool qin = rin && (FULL || 4 * c4 < p.dim);
+                const f4 x = *(const f4 *)(qs + col * DK + 4 * (c4 ^ (col & 7))) * p.q_scale;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    q[4 * hh + j] = qin ? x[j] : 0.f;
+            }
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj)
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+                    acc[b] = mfma(kb[buf][b][uu][jj >> 2][jj & 3], q[jj], acc[b]);
         }
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj)
-#pragma unroll
-            for (int b = 0; b < 2; ++b)
-                acc[b] = mfma(kb[b][u][jj >> 2][jj & 3], q[jj], acc[b]);
+        if (pc + KB < KPN) { // this buffer's operands are consumed: the next piece
+            __builtin_amdgcn_sched_barrier(0);
+            load_k(pc + KB, buf);
+        }
     }
 
-    // V of tiles LT .. 7 for the wave's dims, into registers now that K is
-    // consumed: vr[t - LT][b][r][x] = V[key 32t + 16b + 4g + r][d0 + VW col + x]
-    float vr[RT > 0 ? RT : 1][2][4][VW];
+    // The tile's maximum (wave w), and whether it has a non-finite allowed
+    // score. The lanes of each row agree on the maximum.
+    float s[2][4];
 #pragma unroll
-    for (int t = LT; t < kTilesPerChunk; ++t)
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            s[b][r] = acc[b][r];
+    cap_scores<CAP>(p, s);
+    bool bad = false;
+    float tm = kNegInf;
+    if (tile_any) {
+        bad = bad_scores(s, ok);
+        tm = tile_max(s, ok);
+    }
+    if (g == 0)
+        tmx[w * kRows + col] = tm;
+    if (lane == 0)
+        tany[w] = tile_any ? 1.f : 0.f;
+
+    // V of tiles LT .. LT+VB-1 for the wave's dims, into registers now that
+    // K is consumed: vr[slot][b][r][x] = V[key 32t + 16b + 4g + r][d0 + VW col + x]
+    // for tile t in slot (t - LT) % VB
+    float vr[VB > 0 ? VB : 1][2][4][VW];
+    auto load_v = [&](int t) {
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -212,44 +294,78 @@ void fan_kv_kernel(Params p, int ci)
                 const int vd = d0 + VW * col;
                 const float *vp = value_row(p, kt < klast ? kt : klast) + hoff +
                                   (FULL || vd < p.dim ? vd : 0);
-                if constexpr (VW == 2) {
-                    const f2 x = ldg2(vp);
-                    vr[t - LT][b][r][0] = x.x;
-                    vr[t - LT][b][r][1] = x.y;
-                } else {
+                float *dst = vr[(t - LT) % (VB > 0 ? VB : 1)][b][r];
+                if constexpr (VW == 4) {
+                    const f4 x = ldg4(vp);
 #pragma unroll
-                    for (int x = 0; x < VW; ++x)
-                        vr[t - LT][b][r][x] = ldg(vp + x);
+                    for (int e = 0; e < 4; ++e)
+                        dst[e] = x[e];
+                } else if constexpr (VW == 2) {
+                    const f2 x = ldg2(vp);
+                    dst[0] = x.x;
+                    dst[1] = x.y;
+                } else {
+                    dst[0] = ldg(vp);
                 }
             }
+    };
+#pragma unroll
+    for (int t = LT; t < LT + VB; ++t)
+        load_v(t);
 
-    // the raw scores into region A once every wave has read Q^T; then the
-    // V copies have landed (each wave waits for its own, the barrier for
-    // all: only the register loads above may still be in flight)
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // Every tile maximum in LDS, and every wave past its score chain (region
+    // A is free). The running maximum after each tile (the same on every
+    // wave), then wave w's probabilities and row sum against it.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    fan_barrier();
+    float tmr[kTilesPerChunk];
+    bool tan[kTilesPerChunk];
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int t = 0; t < kTilesPerChunk; ++t) {
+        tmr[t] = tmx[t * kRows + col];
+        tan[t] = tany[t] != 0.f;
+    }
+    {
+        float mrun = kNegInf, msw = 0.f;
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            qs[((2 * w + b) * 4 + r) * 64 + lane] = acc[b][r];
-    constexpr int NVR = RT * 8 * (VW == 2 ? 1 : VW); // V register loads in flight
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(NVR));
+        for (int t = 0; t < kTilesPerChunk; ++t) {
+            if (tan[t])
+                mrun = fmaxf(mrun, tmr[t]);
+            if (t == w)
+                msw = safe_max(mrun);
+        }
+        if (tile_any) {
+            float pr[2][4];
+            const float rs = tile_probs(s, ok, msw, pr);
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    qs[(w * 8 + 4 * b + r) * 64 + lane] = pr[b][r];
+            if (g == 0)
+                trs[w * kRows + col] = rs;
+        }
+    }
+    if (bad)
+        atomicOr(p.err, kErrScore);
+    // the probabilities and row sums in LDS, and the V copies landed (each
+    // wave waits for its own, the barrier for all: only the V register
+    // loads may still be in flight)
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(VB * 8));
     fan_barrier();
 
     // The merge's own layout (after the tiles): thread tid owns row
-    // mrow = tid / 32 of the unit and the f4 columns mq(k) = tid % 32 + 32k
-    // (k < NK), so a wave's loads of a chunk partial are two rows' contiguous
-    // bytes. With MERGE, the earlier chunks' partials of the first kMergeHead
-    // chunks are requested now: they land while the tiles run.
-    constexpr int NK = DK / 4 / 32;
+    // mrow = tid / 32 of the unit and the f4 columns tid % 32 + 32k (k < NK),
+    // so a wave's loads of a chunk partial are two rows' contiguous bytes.
     const int mrow = unit * kRows + tid / 32;
     const bool mrin = mrow < p.nrows;
     const int64_t mslot0 = ((int64_t)kvl * p.nrows_pad + (mrin ? mrow : 0)) * p.nch;
-    f2 eml[MERGE ? kMergeHead : 1];
-    f4 eo[MERGE ? kMergeHead : 1][NK];
-    if constexpr (MERGE) {
+    constexpr int EH = MERGE ? kMergeHead : 1;
+    f2 eml[EH];
+    f4 eo[EH][NK];
+    auto load_earlier = [&]() {
 #pragma unroll
-        for (int c0 = 0; c0 < kMergeHead; ++c0) {
+        for (int c0 = 0; c0 < EH; ++c0) {
             // slots past ci re-read the last earlier chunk (not merged)
             const int64_t cc = mslot0 + (c0 < ci ? c0 : ci - 1);
             eml[c0] = ldg2(p.ws_ml + 2 * cc);
@@ -257,82 +373,70 @@ void fan_kv_kernel(Params p, int ci)
             for (int k = 0; k < NK; ++k)
                 eo[c0][k] = ldg4(p.ws_o + cc * p.dk + 4 * (tid % 32 + 32 * k));
         }
-    }
+    };
+    if constexpr (MERGE && C::PREFETCH)
+        load_earlier(); // they land while the tiles run
 
-    // Online softmax (the same on every wave) and the P.V chains of the
-    // wave's VW output blocks, tile by tile. Output block x: A operand
-    // V[key][d0 + VW col + x], so O[x][i] is dim d0 + VW (4g + i) + x.
+    // The l chain and the P.V chains of the wave's VW output blocks, tile
+    // by tile. Output block x: A operand V[key][d0 + VW col + x], so O[x][i]
+    // is dim d0 + VW (4g + i) + x.
     float m = kNegInf, l = 0.f;
     f4 O[VW];
 #pragma unroll
     for (int x = 0; x < VW; ++x)
         O[x] = f4{0.f, 0.f, 0.f, 0.f};
-    bool bad = false;
-    const ChunkKeys ck = chunk_keys(p, row, cbase);
-    auto tile_step = [&](int t, const bool ok[2][4]) {
-        float sv[2][4], pr[2][4];
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+    for (int t = 0; t < kTilesPerChunk; ++t) {
+        if (tan[t]) {
+            const float mn = fmaxf(m, tmr[t]);
+            const float ms = safe_max(mn);
+            const float alpha = fexp(m - ms);
+            l = __builtin_fmaf(l, alpha, trs[t * kRows + col]);
+            m = mn;
+            float pr[8];
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                sv[b][r] = qs[((2 * t + b) * 4 + r) * 64 + lane];
-        cap_scores<CAP>(p, sv);
-        bad |= bad_scores(sv, ok);
-        const float mn = fmaxf(m, tile_max(sv, ok));
-        const float ms = safe_max(mn);
-        const float alpha = fexp(m - ms);
-        const float rs = tile_probs(sv, ok, ms, pr);
-        l = __builtin_fmaf(l, alpha, rs);
-        m = mn;
+            for (int e = 0; e < 8; ++e)
+                pr[e] = qs[(t * 8 + e) * 64 + lane];
 #pragma unroll
-        for (int x = 0; x < VW; ++x)
-            O[x] = O[x] * alpha;
+            for (int x = 0; x < VW; ++x)
+                O[x] = O[x] * alpha;
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+            for (int b = 0; b < 2; ++b)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float va[VW];
-                if (t < LT) {
-                    const float *vp = vls + (kTile * t + 16 * b + 4 * g + r) * DK + d0 + VW * col;
-                    if constexpr (VW == 2) {
-                        const f2 y = *(const f2 *)vp;
-                        va[0] = y.x;
-                        va[1] = y.y;
+                for (int r = 0; r < 4; ++r) {
+                    float va[VW];
+                    if (t < LT) {
+                        const float *vp =
+                            vls + (kTile * t + 16 * b + 4 * g + r) * DK + d0 + VW * col;
+                        if constexpr (VW == 4) {
+                            const f4 y = *(const f4 *)vp;
+#pragma unroll
+                            for (int x = 0; x < 4; ++x)
+                                va[x] = y[x];
+                        } else if constexpr (VW == 2) {
+                            const f2 y = *(const f2 *)vp;
+                            va[0] = y.x;
+                            va[1] = y.y;
+                        } else {
+                            va[0] = vp[0];
+                        }
                     } else {
 #pragma unroll
                         for (int x = 0; x < VW; ++x)
-                            va[x] = vp[x];
+                            va[x] = vr[(t - LT) % (VB > 0 ? VB : 1)][b][r][x];
                     }
-                } else {
 #pragma unroll
                     for (int x = 0; x < VW; ++x)
-                        va[x] = vr[t >= LT ? t - LT : 0][b][r][x];
+                        O[x] = mfma(va[x], pr[4 * b + r], O[x]);
                 }
-#pragma unroll
-                for (int x = 0; x < VW; ++x)
-                    O[x] = mfma(va[x], pr[b][r], O[x]);
-            }
-    };
-    // A chunk that every real row of the unit sees whole needs no per-key
-    // test (padding rows then count as allowed: their columns never reach a
-    // real row's state). Otherwise a tile with no allowed key for any row of
-    // the unit is skipped, which leaves the state bit-unchanged.
-    if (!p.mask && __all(!rin || (ck.lo <= 0 && ck.hi >= kChunk - 1))) {
-        const bool ok[2][4] = {{true, true, true, true}, {true, true, true, true}};
-#pragma unroll
-        for (int t = 0; t < kTilesPerChunk; ++t)
-            tile_step(t, ok);
-    } else {
-#pragma unroll
-        for (int t = 0; t < kTilesPerChunk; ++t) {
-            bool ok[2][4];
-            const bool any = tile_keys(ck, t, g, ok);
-            if (__any(any))
-                tile_step(t, ok);
+        }
+        if (t >= LT && t + VB < kTilesPerChunk) { // this slot is consumed: a later tile
+            __builtin_amdgcn_sched_barrier(0);
+            load_v(t + VB);
         }
     }
-    if (bad && w == 0)
-        atomicOr(p.err, kErrScore);
+    if constexpr (MERGE && !C::PREFETCH)
+        load_earlier();
 
     // The chunk state into region B (free once every wave is past its
     // tiles), row-major [16][DK] with each row's f4 columns XOR-swizzled by
@@ -357,7 +461,8 @@ void fan_kv_kernel(Params p, int ci)
         mlst[2 * col] = m;
         mlst[2 * col + 1] = l;
     }
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    fan_barrier();
     if (!mrin)
         return;
     const int mr = tid / 32; // the merge row within the unit
@@ -439,7 +544,7 @@ template <int DK, bool FULL, bool CAP, bool MERGE> static hipError_t configure_f
     if (!configured[dev].load(std::memory_order_acquire)) {
         e = hipFuncSetAttribute((const void *)fan_kv_kernel<DK, FULL, CAP, MERGE>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)FanLds<DK>::bytes);
+                                (int)FanCfg<DK>::bytes);
         if (e != hipSuccess)
             return e;
         configured[dev].store(true, std::memory_order_release);
@@ -454,7 +559,7 @@ static hipError_t launch_fan_dk(const Params &p, int ci, hipStream_t stream)
     if (e != hipSuccess)
         return e;
     fan_kv_kernel<DK, FULL, CAP, MERGE>
-        <<<dim3(p.units * p.nkv), kFanThreads, FanLds<DK>::bytes, stream>>>(p, ci);
+        <<<dim3(p.units * p.nkv), kFanThreads, FanCfg<DK>::bytes, stream>>>(p, ci);
     return hipGetLastError();
 }
 
@@ -479,7 +584,7 @@ static hipError_t launch_fan_cap(const Params &p, int ci, bool merge_out, hipStr
 // Whether launch chunk items at padded head dim dk can run fanned.
 bool fan_supported(int dk)
 {
-    return dk == 128 || dk == 256;
+    return dk == 128 || dk == 256 || dk == 512;
 }
 
 // The launch's chunk ci (its last) as one fanned item per (16-row unit, KV
@@ -493,6 +598,7 @@ hipError_t launch_fan_chunk(const Params &p, int ci, bool merge_out, hipStream_t
     switch (p.dk) {
     case 128: return launch_fan_cap<128>(p, ci, merge_out, stream);
     case 256: return launch_fan_cap<256>(p, ci, merge_out, stream);
+    case 512: return launch_fan_cap<512>(p, ci, merge_out, stream);
     default: return hipErrorInvalidValue;
     }
 }

@@ -18,10 +18,10 @@
 //
 // split != 0: the workgroup computes the single chunk c_lo + z0 + blockIdx.z
 // and writes its chunk partial for the combine kernels. A split launch whose
-// chunk items leave a small last round runs that round's chunk through the
-// pipelined decode kernel instead (one (16-row unit, chunk) item per
-// workgroup, K/V streamed from L2 by four waves: more, shorter items fill
-// the CUs); each row's arithmetic is the same either way.
+// chunk items leave a small last round runs that round's chunk as fanned
+// items instead (fan_kv.hip: one (16-row unit, chunk) item per workgroup of
+// eight waves: more, shorter items fill the CUs; the pipelined decode kernel
+// at head dim 64); each row's arithmetic is the same either way.
 #include "attention_device.hpp"
 
 #include <atomic>

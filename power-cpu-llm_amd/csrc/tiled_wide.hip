@@ -446,13 +446,12 @@ static hipError_t launch_wide(const Params &p, int split, dim3 grid, hipStream_t
 
 int device_cus();
 int tiled_tail_chunks(const Params &p, int nqb, int cus);
-hipError_t launch_pipe_kv_chunks(const Params &p, int c0, int n, bool merge_out,
-                                 hipStream_t stream);
+hipError_t launch_fan_chunk(const Params &p, int ci, bool merge_out, hipStream_t stream);
 
 // A split launch whose chunk items leave a small last round runs that
-// round's chunk through the pipelined decode kernel, as the other tiled
-// kernel does; with all chunks in one span that tail also merges every
-// chunk partial into the output (*merged: no combine needed).
+// round's chunk as fanned (16-row unit, chunk) items (fan_kv.hip), as the
+// other tiled kernel does; with all chunks in one span that tail also
+// merges every chunk partial into the output (*merged: no combine needed).
 hipError_t launch_tiled_wide(const Params &p, int split, hipStream_t stream, bool *merged)
 {
     const int nqb = (p.nrows + kWideRows - 1) / kWideRows;
@@ -463,7 +462,7 @@ hipError_t launch_tiled_wide(const Params &p, int split, hipStream_t stream, boo
     if (e != hipSuccess || !tail)
         return e;
     const bool merge_out = p.nspan == 1;
-    e = launch_pipe_kv_chunks(p, p.nch - tail, tail, merge_out, stream);
+    e = launch_fan_chunk(p, p.nch - 1, merge_out, stream);
     if (e == hipSuccess && merge_out)
         *merged = true;
     return e;

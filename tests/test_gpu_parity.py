@@ -425,6 +425,11 @@ DESC_CASES = [
     # kernel, one pass and one chunk per block
     (16, 2, 512, 100, 700, 1, 0, 600),
     (16, 2, 512, 40, 5000, 1, 0, 4960),
+    # its chunk-split launches whose last round runs fanned: a padded head
+    # dim (320) with causal rows in the last chunk, and two spans (the
+    # fanned chunk writes its partial for the combine)
+    (16, 2, 320, 256, 2304, 1, 0, 2048),
+    (16, 2, 512, 256, 4352, 0, 0, 0),
     (8, 2, 320, 70, 400, 1, 130, 330),
 ]
 
