@@ -36,6 +36,7 @@
 #include "attention_device.hpp"
 
 #include <atomic>
+#include <type_traits>
 
 namespace pcl {
 
@@ -102,6 +103,26 @@ __device__ __forceinline__ void fan_barrier()
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+}
+
+// f(std::integral_constant<int, i>) for i = I .. N-1, in order (compile-time
+// indices where a builtin needs a constant).
+template <int I, int N, typename F> __device__ __forceinline__ void static_for(F &&f)
+{
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
+// Vector-memory operations a wave has issued after the K loads of score
+// step uu of piece pc (four loads per step), at the time that step's score
+// MFMAs run: the rest of the piece, the pieces in flight behind it, and the
+// V copies when they were issued after it (behind the first KB pieces).
+template <typename C> __device__ constexpr int k_loads_after(int pc, int uu, int nv)
+{
+    const int last = pc + C::KB - 1 < C::KPN - 1 ? pc + C::KB - 1 : C::KPN - 1;
+    return 4 * (C::KU - 1 - uu) + 4 * C::KU * (last - pc) + (pc < C::KB ? nv : 0);
 }
 
 // Earlier chunk partials a merging thread requests in one batch (the rest,
@@ -188,21 +209,25 @@ void fan_kv_kernel(Params p, int ci)
     // pc covering score steps [KU pc, KU pc + KU):
     // kb[buf][b][uu][hh] = K[key 32w + 16b + col][32u + 8g + 4hh ..], u = KU pc + uu
     f4 kb[KB][2][KU][2];
+    // (in score-step order: the chains start as their first operands land)
+    const float *kps[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        const int64_t key = cbase + kTile * w + 16 * b + col;
+        kps[b] = key_row(p, key < klast ? key : klast) + hoff;
+    }
     auto load_k = [&](int pc, int buf) {
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            const int64_t key = cbase + kTile * w + 16 * b + col;
-            const float *kp = key_row(p, key < klast ? key : klast) + hoff;
+        for (int uu = 0; uu < KU; ++uu)
 #pragma unroll
-            for (int uu = 0; uu < KU; ++uu)
+            for (int b = 0; b < 2; ++b)
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
                     const int d = 32 * (KU * pc + uu) + 8 * g + 4 * hh;
                     const bool din = FULL || d < p.dim;
-                    const f4 x = ldg4(kp + (din ? d : 0));
+                    const f4 x = ldg4(kps[b] + (din ? d : 0));
                     kb[buf][b][uu][hh] = din ? x : f4{0.f, 0.f, 0.f, 0.f};
                 }
-        }
     };
 #pragma unroll
     for (int pc = 0; pc < KB; ++pc)
@@ -225,20 +250,23 @@ void fan_kv_kernel(Params p, int ci)
                           (FULL || vd < p.dim ? vd : 0);
         __builtin_amdgcn_global_load_lds((fan_gptr_t)vp, (fan_lptr_t)(vls + 256 * j), 16, 0, 0);
     }
-    // Q and K have landed (the V copies may stay in flight): every wave's Q
+    // Q has landed (K and the V copies may stay in flight): every wave's Q
     // copies are in LDS after the barrier.
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(NV));
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(KB * KU * 4 + NV));
     fan_barrier();
 
     // the score chains of blocks 2w and 2w + 1, B operands
     // Q[row][32u + 8g + jj] * q_scale (zero for padding rows and dims)
     f4 acc[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-    for (int pc = 0; pc < KPN; ++pc) {
-        const int buf = pc % KB;
-#pragma unroll
-        for (int uu = 0; uu < KU; ++uu) {
+    static_for<0, KPN>([&](auto pcc) {
+        constexpr int pc = decltype(pcc)::value;
+        constexpr int buf = pc % KB;
+        static_for<0, KU>([&](auto uuc) {
+            constexpr int uu = decltype(uuc)::value;
             const int u = KU * pc + uu;
+            // this step's K operands have landed: wait for them by count
+            // (the compiler's own wait would also drain the V copies)
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(k_loads_after<C>(pc, uu, NV)));
             float q[8];
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
@@ -254,12 +282,12 @@ void fan_kv_kernel(Params p, int ci)
 #pragma unroll
                 for (int b = 0; b < 2; ++b)
                     acc[b] = mfma(kb[buf][b][uu][jj >> 2][jj & 3], q[jj], acc[b]);
-        }
-        if (pc + KB < KPN) { // this buffer's operands are consumed: the next piece
+        });
+        if constexpr (pc + KB < KPN) { // this buffer's operands are consumed: the next piece
             __builtin_amdgcn_sched_barrier(0);
             load_k(pc + KB, buf);
         }
-    }
+    });
 
     // The tile's maximum (wave w), and whether it has a non-finite allowed
     // score. The lanes of each row agree on the maximum.

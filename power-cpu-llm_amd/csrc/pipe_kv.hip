@@ -732,9 +732,10 @@ hipError_t launch_full(const Params &p, int c0, int n, bool merge_out, hipStream
 }
 
 // Chunks [c0, c0 + n) of the launch, their partials in the launch's chunk
-// slots (the chunk-split prefill runs its last round's chunk this way); with
-// merge_out (n = 1, the launch's last chunk, one span, the earlier chunks'
-// partials already written) the merged output instead.
+// slots (the chunk-split prefill runs its last round's chunk this way at
+// head dim 64; fan_kv.hip at the others); with merge_out (n = 1, the
+// launch's last chunk, one span, the earlier chunks' partials already
+// written) the merged output instead.
 hipError_t launch_pipe_kv_chunks(const Params &p, int c0, int n, bool merge_out,
                                  hipStream_t stream)
 {
