@@ -178,9 +178,19 @@ void tiled_wide_kernel(Params p, int split, int z0)
         }
     };
 
-    // Chunk merge into the span, at a span end the span merge into the
-    // total; `last` also normalises into the output (this wave's dims).
-    auto flush = [&](bool chunk, bool span_end, bool last) {
+    // Where the span accumulator (the row's output slot until the last
+    // merge) and the running total keep natural dims dh + 64a + 16g + 4i ..:
+    // in a whole 64-dim block the 16-byte slots are stored with g and i
+    // swapped, so the four lanes of a row in one load or store cover one
+    // contiguous 64-byte sector; a partial last block keeps the natural order.
+    auto acc_pos = [&](int a, int i) {
+        return dh + 64 * a + 64 <= p.dim ? dh + 64 * a + 16 * i + 4 * g
+                                         : dh + 64 * a + 16 * g + 4 * i;
+    };
+
+    // Chunk merge into the span, and at a span end the span merge into the
+    // total (this wave's dims; not the last merge: flush_last below).
+    auto flush = [&](bool chunk, bool span_end) {
         float *a1 = acc1, *a2 = acc2;
         asm volatile("" : "+v"(a1), "+v"(a2));
         const bool first1 = M1 == kNegInf;
@@ -190,7 +200,7 @@ void tiled_wide_kernel(Params p, int split, int z0)
             L1 = merge_value(L1, l, f1);
             M1 = f1.m;
         }
-        const bool add2 = (span_end || last) && M1 != kNegInf;
+        const bool add2 = span_end && M1 != kNegInf;
         const bool first2 = M2 == kNegInf;
         MergeFactors f2 = {M2, 1.f, 0.f};
         if (add2) {
@@ -198,49 +208,37 @@ void tiled_wide_kernel(Params p, int split, int z0)
             L2 = merge_value(L2, L1, f2);
             M2 = f2.m;
         }
-        bool nonfinite = false;
         if (rout) {
 #pragma unroll
             for (int a = 0; a < NQ; ++a)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int d = dh + 64 * a + 16 * g + 4 * i;
-                    if (d >= p.dim)
+                    if (dh + 64 * a + 16 * g + 4 * i >= p.dim)
                         continue;
+                    const int dm = acc_pos(a, i);
                     f4 s1 = f4{0.f, 0.f, 0.f, 0.f};
                     if (!first1)
-                        s1 = ldg4(a1 + d);
+                        s1 = ldg4(a1 + dm);
                     if (chunk) {
 #pragma unroll
                         for (int j = 0; j < 4; ++j)
                             s1[j] = merge_value(s1[j], O[a][j][i], f1);
                     }
-                    if (!(span_end || last)) {
-                        stg4(a1 + d, s1);
+                    if (!span_end) {
+                        stg4(a1 + dm, s1);
                         continue;
                     }
                     f4 s2 = f4{0.f, 0.f, 0.f, 0.f};
                     if (!first2)
-                        s2 = ldg4(a2 + d);
+                        s2 = ldg4(a2 + dm);
                     if (add2) {
 #pragma unroll
                         for (int j = 0; j < 4; ++j)
                             s2[j] = merge_value(s2[j], s1[j], f2);
                     }
-                    if (last) {
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            s2[j] = s2[j] / L2;
-                            nonfinite |= !is_finite(s2[j]);
-                        }
-                        stg4(a1 + d, s2);
-                    } else {
-                        stg4(a2 + d, s2);
-                    }
+                    stg4(a2 + dm, s2);
                 }
         }
-        if (nonfinite)
-            atomicOr(p.err, kErrOutput);
         if (chunk) {
             m = kNegInf;
             l = 0.f;
@@ -250,10 +248,76 @@ void tiled_wide_kernel(Params p, int split, int z0)
                 for (int j = 0; j < 4; ++j)
                     O[a][j] = f4{0.f, 0.f, 0.f, 0.f};
         }
-        if (span_end || last) {
+        if (span_end) {
             M1 = kNegInf;
             L1 = 0.f;
         }
+    };
+
+    // The last merge, normalised into the output (this wave's dims). The
+    // output's natural order overwrites the span accumulator's slots in
+    // another order, so every accumulator value is loaded first (after the
+    // tiles: Q^T's registers are free).
+    auto flush_last = [&](bool chunk) {
+        float *a1 = acc1, *a2 = acc2;
+        asm volatile("" : "+v"(a1), "+v"(a2));
+        const bool first1 = M1 == kNegInf;
+        MergeFactors f1 = {M1, 1.f, 0.f};
+        if (chunk) {
+            f1 = merge_factors(M1, m);
+            L1 = merge_value(L1, l, f1);
+            M1 = f1.m;
+        }
+        const bool add2 = M1 != kNegInf;
+        const bool first2 = M2 == kNegInf;
+        MergeFactors f2 = {M2, 1.f, 0.f};
+        if (add2) {
+            f2 = merge_factors(M2, M1);
+            L2 = merge_value(L2, L1, f2);
+            M2 = f2.m;
+        }
+        if (!rout)
+            return;
+        f4 s1v[NQ][4];
+#pragma unroll
+        for (int a = 0; a < NQ; ++a)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                s1v[a][i] = f4{0.f, 0.f, 0.f, 0.f};
+                if (!first1 && dh + 64 * a + 16 * g + 4 * i < p.dim)
+                    s1v[a][i] = ldg4(a1 + acc_pos(a, i));
+            }
+        bool nonfinite = false;
+#pragma unroll
+        for (int a = 0; a < NQ; ++a)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = dh + 64 * a + 16 * g + 4 * i;
+                if (d >= p.dim)
+                    continue;
+                f4 s1 = s1v[a][i];
+                if (chunk) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        s1[j] = merge_value(s1[j], O[a][j][i], f1);
+                }
+                f4 s2 = f4{0.f, 0.f, 0.f, 0.f};
+                if (!first2)
+                    s2 = ldg4(a2 + acc_pos(a, i));
+                if (add2) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        s2[j] = merge_value(s2[j], s1[j], f2);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    s2[j] = s2[j] / L2;
+                    nonfinite |= !is_finite(s2[j]);
+                }
+                stg4(a1 + d, s2);
+            }
+        if (nonfinite)
+            atomicOr(p.err, kErrOutput);
     };
 
     // This half's part of tile t's two score chains: half 0 runs u = 0..7
@@ -373,12 +437,11 @@ void tiled_wide_kernel(Params p, int split, int z0)
             processed = true;
         }
 
-        if (!split) {
-            const bool last = t + 1 == t_hi;
-            const bool chunk_end = ((t + 1) % kTilesPerChunk) == 0 || last;
+        if (!split && t + 1 < t_hi) { // (the last tile's merge follows the loop)
+            const bool chunk_end = ((t + 1) % kTilesPerChunk) == 0;
             const bool span_end = ((t + 1) % kSpanTiles) == 0;
-            if ((chunk_end && processed) || span_end || last)
-                flush(chunk_end && processed, span_end, last);
+            if ((chunk_end && processed) || span_end)
+                flush(chunk_end && processed, span_end);
             if (chunk_end)
                 processed = false;
         }
@@ -391,8 +454,8 @@ void tiled_wide_kernel(Params p, int split, int z0)
     if (bad)
         atomicOr(p.err, kErrScore);
     if (!split) {
-        if (t_lo >= t_hi) // no key at all: 0/0, flagged like any non-finite output
-            flush(false, false, true);
+        // with no key at all: 0/0, flagged like any non-finite output
+        flush_last(t_lo < t_hi && processed);
         return;
     }
 
