@@ -47,32 +47,35 @@ template <int DK> struct FanCfg {
     static constexpr int NU = DK / 32;        // score chain steps
     static constexpr int VD = DK / kFanWaves; // output dims of a wave
     static constexpr int VW = VD / 16;        // output blocks of a wave (dims of a lane per key)
-    // K of a wave's tile in pieces of KU score steps, KB pieces in flight
-    static constexpr int KU = DK > 256 ? 4 : NU;
+    // K of a wave's tile staged through LDS in pieces of KU score steps
+    // (32 keys x 32 KU dims, 4 KU one-KiB copies), KB pieces in flight
+    static constexpr int KU = DK <= 128 ? 4 : DK <= 256 ? 2 : 1;
     static constexpr int KPN = NU / KU;
     static constexpr int KB = KPN > 1 ? 2 : 1;
-    // V: tiles 0 .. LT-1 in LDS, the rest through registers, VB in flight
-    static constexpr int LT = DK <= 128 ? kTilesPerChunk : DK <= 256 ? 4 : 1;
-    static constexpr int RT = kTilesPerChunk - LT;
-    static constexpr int VB = RT < 4 ? RT : 4;
-    // merge: f4 columns of a thread's row; the earlier partials are
-    // requested before the tiles when they fit the registers
+    static constexpr int KCOPIES = 4 * KU;
+    static constexpr int kpFloats = kTile * 32 * KU;
+    // V through registers: the first VB0 tiles requested up front; then the
+    // rest once K is issued (VB = 8: every tile's V held at once), or VB
+    // tiles in flight, each slot refilled once its tile's P.V has run
+    static constexpr int VB = DK <= 256 ? kTilesPerChunk : 4;
+    static constexpr int VB0 = 4;
+    // merge: f4 columns of a thread's row; the earlier partials are copied
+    // into the freed K staging area while the tiles run when they fit it
     static constexpr int NK = DK / 128;
-    static constexpr bool PREFETCH = NK <= 2;
     // LDS, in floats: region A holds Q (row-major, each row's f4 columns
-    // XOR-swizzled by (row & 7)) during the score chains and the
-    // probabilities ([tile][4b + r][lane]) after them; region B holds V of
-    // tiles 0 .. LT-1 (key-major) and after the tiles the chunk state
-    // ([row][DK], swizzled like Q, then (m, l) per row); region C holds
-    // each tile's row maxima and row sums and whether it has any allowed key
+    // XOR-swizzled by (row & 7)) during the score chains, the
+    // probabilities ([tile][4b + r][lane]) after them and the chunk state
+    // ([row][DK], swizzled like Q) after the tiles; region K holds each
+    // wave's K pieces, then the earlier partials ([row][chunk][DK]);
+    // region C holds each tile's row maxima and row sums, whether it has any
+    // allowed key, and each row's (m, l)
     static constexpr int qFloats = kRows * DK;
     static constexpr int pFloats = kTilesPerChunk * 8 * 64;
     static constexpr int aFloats = qFloats > pFloats ? qFloats : pFloats;
-    static constexpr int vtFloats = LT * kTile * DK;
-    static constexpr int oFloats = kRows * DK + 2 * kRows;
-    static constexpr int bFloats = vtFloats > oFloats ? vtFloats : oFloats;
-    static constexpr int cFloats = 2 * kTilesPerChunk * kRows + kTilesPerChunk;
-    static constexpr size_t bytes = (size_t)(aFloats + bFloats + cFloats) * sizeof(float);
+    static constexpr int kFloats = kFanWaves * KB * kpFloats;
+    static constexpr bool PREFETCH = kRows * 8 * DK <= kFloats;
+    static constexpr int cFloats = 2 * kTilesPerChunk * kRows + kTilesPerChunk + 2 * kRows;
+    static constexpr size_t bytes = (size_t)(aFloats + kFloats + cFloats) * sizeof(float);
     static_assert(VW >= 1 && VW * 16 * kFanWaves == DK, "whole 16-dim output blocks");
     static_assert(KU * KPN == NU, "whole K pieces");
 };
@@ -115,14 +118,28 @@ template <int I, int N, typename F> __device__ __forceinline__ void static_for(F
     }
 }
 
-// Vector-memory operations a wave has issued after the K loads of score
-// step uu of piece pc (four loads per step), at the time that step's score
-// MFMAs run: the rest of the piece, the pieces in flight behind it, and the
-// V copies when they were issued after it (behind the first KB pieces).
-template <typename C> __device__ constexpr int k_loads_after(int pc, int uu, int nv)
+// Vector-memory operations a wave has issued after its copies of K piece pc
+// when that piece's score steps run. Issue order: Q, pieces 0 .. KB-1, V
+// tiles 0 .. VB0-1; after piece j's steps, piece j + KB (while there is
+// one), and after piece KPN - KB's steps V tiles VB0 .. 7 when every tile's
+// V is held at once.
+template <typename C> __device__ constexpr int ops_after_piece(int pc)
 {
-    const int last = pc + C::KB - 1 < C::KPN - 1 ? pc + C::KB - 1 : C::KPN - 1;
-    return 4 * (C::KU - 1 - uu) + 4 * C::KU * (last - pc) + (pc < C::KB ? nv : 0);
+    int n = 0;
+    // prologue entries after piece pc
+    for (int q = pc + 1; q < C::KB && q < C::KPN; ++q)
+        n += C::KCOPIES;
+    if (pc < C::KB)
+        n += 8 * C::VB0;
+    // entries issued after piece j's steps, j < pc (all after piece pc's
+    // copies when the entry is issued later than piece pc)
+    for (int j = 0; j < pc; ++j) {
+        if (j + C::KB < C::KPN && j + C::KB > pc)
+            n += C::KCOPIES;
+        if (C::VB == kTilesPerChunk && j == C::KPN - C::KB)
+            n += 8 * (kTilesPerChunk - C::VB0);
+    }
+    return n;
 }
 
 // Earlier chunk partials a merging thread requests in one batch (the rest,
@@ -137,17 +154,16 @@ void fan_kv_kernel(Params p, int ci)
 {
     using C = FanCfg<DK>;
     constexpr int NU = C::NU, VD = C::VD, VW = C::VW, KU = C::KU, KPN = C::KPN, KB = C::KB;
-    constexpr int LT = C::LT, VB = C::VB, NK = C::NK;
-    constexpr int NV = LT * kTile * DK / 256 / kFanWaves; // V copies (1 KiB each) per wave
-    static_assert(NV * 256 * kFanWaves == LT * kTile * DK, "whole 1 KiB copies per wave");
+    constexpr int VB = C::VB, VB0 = C::VB0, NK = C::NK;
     constexpr int NQC = kRows * DK / 256 / kFanWaves; // Q copies per wave
     static_assert(NQC * 256 * kFanWaves == kRows * DK, "whole 1 KiB copies per wave");
     extern __shared__ float lds[];
-    float *qs = lds;                  // region A: Q, then the probabilities
-    float *vls = lds + C::aFloats;    // region B: V of tiles 0 .. LT-1, then the chunk state
-    float *tmx = vls + C::bFloats;    // region C: [tile][row] maxima,
-    float *trs = tmx + kTilesPerChunk * kRows; // [tile][row] row sums,
-    float *tany = trs + kTilesPerChunk * kRows; // [tile] any allowed key (0 / 1)
+    float *qs = lds;                  // region A: Q, the probabilities, the chunk state
+    float *kst = lds + C::aFloats;    // region K: K pieces, then the earlier partials
+    float *tmx = kst + C::kFloats;    // region C: [tile][row] maxima,
+    float *trs = tmx + kTilesPerChunk * kRows;  // [tile][row] row sums,
+    float *tany = trs + kTilesPerChunk * kRows; // [tile] any allowed key (0 / 1),
+    float *mlst = tany + kTilesPerChunk;        // [row] (m, l)
 
     const int c = p.c_lo + ci;
     // consecutive workgroups cycle over the KV heads (each XCD's L2 then
@@ -187,6 +203,21 @@ void fan_kv_kernel(Params p, int ci)
     }
     const bool tile_any = __any(any);
 
+    // The merge's own layout (after the tiles): thread tid owns row
+    // mrow = tid / 32 of the unit and the f4 columns tid % 32 + 32k (k < NK),
+    // so a wave's accesses of a chunk partial are two rows' contiguous bytes.
+    // With MERGE the earlier chunks' (m, l) are requested first.
+    const int mrow = unit * kRows + tid / 32;
+    const bool mrin = mrow < p.nrows;
+    const int64_t mslot0 = ((int64_t)kvl * p.nrows_pad + (mrin ? mrow : 0)) * p.nch;
+    constexpr int EH = MERGE ? kMergeHead : 1;
+    f2 eml[EH];
+    if constexpr (MERGE) {
+#pragma unroll
+        for (int c0 = 0; c0 < EH; ++c0) // slots past ci re-read the last earlier chunk
+            eml[c0] = ldg2(p.ws_ml + 2 * (mslot0 + (c0 < ci ? c0 : ci - 1)));
+    }
+
     // Q of the unit's 16 rows, HBM -> LDS (region A, unscaled): copy j moves
     // 1 KiB (256 floats) of the row-major [16][DK] block, each row's 16-byte
     // pieces XOR-swizzled by (row & 7) so that the eight rows an MFMA operand
@@ -205,69 +236,83 @@ void fan_kv_kernel(Params p, int ci)
                           (FULL || qd < p.dim ? qd : 0);
         __builtin_amdgcn_global_load_lds((fan_gptr_t)qp, (fan_lptr_t)(qs + 256 * j), 16, 0, 0);
     }
-    // K of tile w (blocks 2w, 2w + 1) straight into MFMA A operands, piece
-    // pc covering score steps [KU pc, KU pc + KU):
-    // kb[buf][b][uu][hh] = K[key 32w + 16b + col][32u + 8g + 4hh ..], u = KU pc + uu
-    f4 kb[KB][2][KU][2];
-    // (in score-step order: the chains start as their first operands land)
-    const float *kps[2];
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-        const int64_t key = cbase + kTile * w + 16 * b + col;
-        kps[b] = key_row(p, key < klast ? key : klast) + hoff;
-    }
+    // K piece pc of tile w (keys 32w .. 32w+31, dims [32 KU pc, 32 KU (pc+1))),
+    // HBM -> this wave's buffer in region K as contiguous copies (four keys'
+    // 128 KU bytes each): [key][8 KU f4 slots], slot s of key k stored at
+    // s ^ (k & 7) (an MFMA operand read's eight keys then hit distinct
+    // banks). A dim past the head's last copies the head's first dims (Q is
+    // zero there); keys past the last copy the last key (masked).
     auto load_k = [&](int pc, int buf) {
+        float *dst = kst + (w * KB + buf) * C::kpFloats;
 #pragma unroll
-        for (int uu = 0; uu < KU; ++uu)
-#pragma unroll
-            for (int b = 0; b < 2; ++b)
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const int d = 32 * (KU * pc + uu) + 8 * g + 4 * hh;
-                    const bool din = FULL || d < p.dim;
-                    const f4 x = ldg4(kps[b] + (din ? d : 0));
-                    kb[buf][b][uu][hh] = din ? x : f4{0.f, 0.f, 0.f, 0.f};
-                }
+        for (int i = 0; i < C::KCOPIES; ++i) {
+            const int f = 256 * i + 4 * lane;
+            const int key = f / (32 * KU);
+            const int pos = (f % (32 * KU)) / 4;
+            const int kd = 32 * KU * pc + 4 * (pos ^ (key & 7));
+            const int64_t kt = cbase + kTile * w + key;
+            const float *kp = key_row(p, kt < klast ? kt : klast) + hoff +
+                              (FULL || kd < p.dim ? kd : 0);
+            __builtin_amdgcn_global_load_lds((fan_gptr_t)kp, (fan_lptr_t)(dst + 256 * i), 16, 0,
+                                             0);
+        }
     };
 #pragma unroll
     for (int pc = 0; pc < KB; ++pc)
         load_k(pc, pc);
-    // (the V copies below must not be scheduled ahead of the K loads: the
-    // score chains wait for K by count)
-    __builtin_amdgcn_sched_barrier(0);
-    // V of tiles 0 .. LT-1, HBM -> LDS: copy j moves 1 KiB of the key-major
-    // region. A dim past the head's last copies the head's first dims
-    // instead (that output is dropped); keys past the last copy the last key
-    // (masked).
+
+    // V for the wave's dims into registers: vr[slot][b][r][x] =
+    // V[key 32t + 16b + 4g + r][d0 + VW col + x] for tile t in slot t % VB
+    float vr[VB][2][4][VW];
+    auto load_v = [&](int t) {
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int j = w * NV + i;
-        const int f = 256 * j + 4 * lane;
-        const int key = f / DK;
-        const int vd = f % DK;
-        const int64_t kt = cbase + key;
-        const float *vp = value_row(p, kt < klast ? kt : klast) + hoff +
-                          (FULL || vd < p.dim ? vd : 0);
-        __builtin_amdgcn_global_load_lds((fan_gptr_t)vp, (fan_lptr_t)(vls + 256 * j), 16, 0, 0);
-    }
-    // Q has landed (K and the V copies may stay in flight): every wave's Q
-    // copies are in LDS after the barrier.
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(KB * KU * 4 + NV));
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t kt = cbase + kTile * t + 16 * b + 4 * g + r;
+                const int vd = d0 + VW * col;
+                const float *vp = value_row(p, kt < klast ? kt : klast) + hoff +
+                                  (FULL || vd < p.dim ? vd : 0);
+                float *dst = vr[t % VB][b][r];
+                if constexpr (VW == 4) {
+                    const f4 x = ldg4(vp);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        dst[e] = x[e];
+                } else if constexpr (VW == 2) {
+                    const f2 x = ldg2(vp);
+                    dst[0] = x.x;
+                    dst[1] = x.y;
+                } else {
+                    dst[0] = ldg(vp);
+                }
+            }
+    };
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < VB0; ++t)
+        load_v(t);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // Q has landed (each wave waits for its own copies, the barrier for
+    // all; K and V stay in flight).
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(KB * C::KCOPIES + 8 * VB0));
     fan_barrier();
 
-    // the score chains of blocks 2w and 2w + 1, B operands
+    // the score chains of blocks 2w and 2w + 1: A operands from this wave's
+    // K pieces (each piece waited for by count), B operands
     // Q[row][32u + 8g + jj] * q_scale (zero for padding rows and dims)
     f4 acc[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
     static_for<0, KPN>([&](auto pcc) {
         constexpr int pc = decltype(pcc)::value;
         constexpr int buf = pc % KB;
-        static_for<0, KU>([&](auto uuc) {
-            constexpr int uu = decltype(uuc)::value;
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(ops_after_piece<C>(pc)));
+        const float *kb = kst + (w * KB + buf) * C::kpFloats;
+#pragma unroll
+        for (int uu = 0; uu < KU; ++uu) {
             const int u = KU * pc + uu;
-            // this step's K operands have landed: wait for them by count
-            // (the compiler's own wait would also drain the V copies)
-            __builtin_amdgcn_s_waitcnt(waitcnt_vm(k_loads_after<C>(pc, uu, NV)));
             float q[8];
+            f4 ka[2][2];
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 const int c4 = 8 * u + 2 * g + hh;
@@ -276,17 +321,29 @@ void fan_kv_kernel(Params p, int ci)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     q[4 * hh + j] = qin ? x[j] : 0.f;
+                const int s4 = 8 * uu + 2 * g + hh; // the f4 slot within the piece
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+                    ka[b][hh] = *(const f4 *)(kb + (16 * b + col) * 32 * KU + 4 * (s4 ^ (col & 7)));
             }
 #pragma unroll
             for (int jj = 0; jj < 8; ++jj)
 #pragma unroll
                 for (int b = 0; b < 2; ++b)
-                    acc[b] = mfma(kb[buf][b][uu][jj >> 2][jj & 3], q[jj], acc[b]);
-        });
-        if constexpr (pc + KB < KPN) { // this buffer's operands are consumed: the next piece
-            __builtin_amdgcn_sched_barrier(0);
-            load_k(pc + KB, buf);
+                    acc[b] = mfma(ka[b][jj >> 2][jj & 3], q[jj], acc[b]);
         }
+        // this buffer's operands are read: the next piece (or, after the
+        // last piece is requested, the remaining V)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (pc + KB < KPN)
+            load_k(pc + KB, buf);
+        if constexpr (VB == kTilesPerChunk && pc == KPN - KB) {
+#pragma unroll
+            for (int t = VB0; t < kTilesPerChunk; ++t)
+                load_v(t);
+        }
+        __builtin_amdgcn_sched_barrier(0);
     });
 
     // The tile's maximum (wave w), and whether it has a non-finite allowed
@@ -309,43 +366,32 @@ void fan_kv_kernel(Params p, int ci)
     if (lane == 0)
         tany[w] = tile_any ? 1.f : 0.f;
 
-    // V of tiles LT .. LT+VB-1 for the wave's dims, into registers now that
-    // K is consumed: vr[slot][b][r][x] = V[key 32t + 16b + 4g + r][d0 + VW col + x]
-    // for tile t in slot (t - LT) % VB
-    float vr[VB > 0 ? VB : 1][2][4][VW];
-    auto load_v = [&](int t) {
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t kt = cbase + kTile * t + 16 * b + 4 * g + r;
-                const int vd = d0 + VW * col;
-                const float *vp = value_row(p, kt < klast ? kt : klast) + hoff +
-                                  (FULL || vd < p.dim ? vd : 0);
-                float *dst = vr[(t - LT) % (VB > 0 ? VB : 1)][b][r];
-                if constexpr (VW == 4) {
-                    const f4 x = ldg4(vp);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        dst[e] = x[e];
-                } else if constexpr (VW == 2) {
-                    const f2 x = ldg2(vp);
-                    dst[0] = x.x;
-                    dst[1] = x.y;
-                } else {
-                    dst[0] = ldg(vp);
-                }
-            }
-    };
-#pragma unroll
-    for (int t = LT; t < LT + VB; ++t)
-        load_v(t);
-
-    // Every tile maximum in LDS, and every wave past its score chain (region
-    // A is free). The running maximum after each tile (the same on every
-    // wave), then wave w's probabilities and row sum against it.
+    // Every tile maximum in LDS, and every wave past its score chain
+    // (regions A and K are free). The running maximum after each tile (the
+    // same on every wave), then wave w's probabilities and row sum against
+    // it.
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     fan_barrier();
+    if constexpr (MERGE && C::PREFETCH) {
+        // the earlier chunks' partials of the unit's rows, HBM -> region K
+        // ([row][kMergeHead][DK]; chunks past ci re-read the last earlier
+        // one, rows past the launch's the last real row), landing while the
+        // tiles run
+        constexpr int NPC = kRows * kMergeHead * DK / 256 / kFanWaves;
+        static_assert(NPC * 256 * kFanWaves == kRows * kMergeHead * DK, "whole copies");
+#pragma unroll
+        for (int i = 0; i < NPC; ++i) {
+            const int f = 256 * (w * NPC + i) + 4 * lane;
+            const int r = f / (kMergeHead * DK);
+            const int c0 = (f / DK) % kMergeHead;
+            const int d = f % DK;
+            const int prow = min(unit * kRows + r, p.nrows - 1);
+            const int64_t slot = ((int64_t)kvl * p.nrows_pad + prow) * p.nch +
+                                 (c0 < ci ? c0 : ci - 1);
+            __builtin_amdgcn_global_load_lds((fan_gptr_t)(p.ws_o + slot * p.dk + d),
+                                             (fan_lptr_t)(kst + 256 * (w * NPC + i)), 16, 0, 0);
+        }
+    }
     float tmr[kTilesPerChunk];
     bool tan[kTilesPerChunk];
 #pragma unroll
@@ -376,34 +422,9 @@ void fan_kv_kernel(Params p, int ci)
     }
     if (bad)
         atomicOr(p.err, kErrScore);
-    // the probabilities and row sums in LDS, and the V copies landed (each
-    // wave waits for its own, the barrier for all: only the V register
-    // loads may still be in flight)
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(VB * 8));
+    // the probabilities and row sums in LDS
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     fan_barrier();
-
-    // The merge's own layout (after the tiles): thread tid owns row
-    // mrow = tid / 32 of the unit and the f4 columns tid % 32 + 32k (k < NK),
-    // so a wave's loads of a chunk partial are two rows' contiguous bytes.
-    const int mrow = unit * kRows + tid / 32;
-    const bool mrin = mrow < p.nrows;
-    const int64_t mslot0 = ((int64_t)kvl * p.nrows_pad + (mrin ? mrow : 0)) * p.nch;
-    constexpr int EH = MERGE ? kMergeHead : 1;
-    f2 eml[EH];
-    f4 eo[EH][NK];
-    auto load_earlier = [&]() {
-#pragma unroll
-        for (int c0 = 0; c0 < EH; ++c0) {
-            // slots past ci re-read the last earlier chunk (not merged)
-            const int64_t cc = mslot0 + (c0 < ci ? c0 : ci - 1);
-            eml[c0] = ldg2(p.ws_ml + 2 * cc);
-#pragma unroll
-            for (int k = 0; k < NK; ++k)
-                eo[c0][k] = ldg4(p.ws_o + cc * p.dk + 4 * (tid % 32 + 32 * k));
-        }
-    };
-    if constexpr (MERGE && C::PREFETCH)
-        load_earlier(); // they land while the tiles run
 
     // The l chain and the P.V chains of the wave's VW output blocks, tile
     // by tile. Output block x: A operand V[key][d0 + VW col + x], so O[x][i]
@@ -431,48 +452,34 @@ void fan_kv_kernel(Params p, int ci)
 #pragma unroll
             for (int b = 0; b < 2; ++b)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float va[VW];
-                    if (t < LT) {
-                        const float *vp =
-                            vls + (kTile * t + 16 * b + 4 * g + r) * DK + d0 + VW * col;
-                        if constexpr (VW == 4) {
-                            const f4 y = *(const f4 *)vp;
-#pragma unroll
-                            for (int x = 0; x < 4; ++x)
-                                va[x] = y[x];
-                        } else if constexpr (VW == 2) {
-                            const f2 y = *(const f2 *)vp;
-                            va[0] = y.x;
-                            va[1] = y.y;
-                        } else {
-                            va[0] = vp[0];
-                        }
-                    } else {
-#pragma unroll
-                        for (int x = 0; x < VW; ++x)
-                            va[x] = vr[(t - LT) % (VB > 0 ? VB : 1)][b][r][x];
-                    }
+                for (int r = 0; r < 4; ++r)
 #pragma unroll
                     for (int x = 0; x < VW; ++x)
-                        O[x] = mfma(va[x], pr[4 * b + r], O[x]);
-                }
+                        O[x] = mfma(vr[t % VB][b][r][x], pr[4 * b + r], O[x]);
         }
-        if (t >= LT && t + VB < kTilesPerChunk) { // this slot is consumed: a later tile
+        if (VB < kTilesPerChunk && t + VB < kTilesPerChunk) { // this slot is free: a later tile
             __builtin_amdgcn_sched_barrier(0);
             load_v(t + VB);
         }
     }
-    if constexpr (MERGE && !C::PREFETCH)
-        load_earlier();
+    // without the copies of region K: the earlier partials into registers
+    f4 eo[MERGE && !C::PREFETCH ? kMergeHead : 1][NK];
+    if constexpr (MERGE && !C::PREFETCH) {
+#pragma unroll
+        for (int c0 = 0; c0 < kMergeHead; ++c0) {
+            const int64_t cc = mslot0 + (c0 < ci ? c0 : ci - 1);
+#pragma unroll
+            for (int k = 0; k < NK; ++k)
+                eo[c0][k] = ldg4(p.ws_o + cc * p.dk + 4 * (tid % 32 + 32 * k));
+        }
+    }
 
-    // The chunk state into region B (free once every wave is past its
+    // The chunk state into region A (free once every wave is past its
     // tiles), row-major [16][DK] with each row's f4 columns XOR-swizzled by
-    // (row & 7), then (m, l) per row: lane (col, g) holds the 4 VW
+    // (row & 7), and (m, l) per row: lane (col, g) holds the 4 VW
     // consecutive dims d0 + 4 VW g .. of row col (dim d0 + VW (4g + i) + x
     // is O[x][i]).
-    float *ost = vls;
-    float *mlst = vls + kRows * DK;
+    float *ost = qs;
     fan_barrier();
 #pragma unroll
     for (int k = 0; k < VW; ++k) {
@@ -489,7 +496,8 @@ void fan_kv_kernel(Params p, int ci)
         mlst[2 * col] = m;
         mlst[2 * col + 1] = l;
     }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    // (the earlier partials' copies have landed too)
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
     fan_barrier();
     if (!mrin)
         return;
@@ -533,8 +541,14 @@ void fan_kv_kernel(Params p, int ci)
             Merged4 sv = {kNegInf, 0.f, f4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
             for (int c0 = 0; c0 < kMergeHead; ++c0)
-                if (c0 < ci)
-                    merge_into4(sv, eml[c0].x, eml[c0].y, eo[c0][k]);
+                if (c0 < ci) {
+                    f4 x;
+                    if constexpr (C::PREFETCH)
+                        x = *(const f4 *)(kst + (mr * kMergeHead + c0) * DK + d);
+                    else
+                        x = eo[c0][k];
+                    merge_into4(sv, eml[c0].x, eml[c0].y, x);
+                }
             for (int c0 = kMergeHead; c0 < ci; ++c0) {
                 const int64_t cc = mslot0 + c0;
                 const f2 x = ldg2(p.ws_ml + 2 * cc);
