@@ -153,7 +153,7 @@ __global__ __launch_bounds__(kFanThreads, 2) __attribute__((amdgpu_waves_per_eu(
 void fan_kv_kernel(Params p, int ci)
 {
     using C = FanCfg<DK>;
-    constexpr int NU = C::NU, VD = C::VD, VW = C::VW, KU = C::KU, KPN = C::KPN, KB = C::KB;
+    constexpr int VD = C::VD, VW = C::VW, KU = C::KU, KPN = C::KPN, KB = C::KB;
     constexpr int VB = C::VB, VB0 = C::VB0, NK = C::NK;
     constexpr int NQC = kRows * DK / 256 / kFanWaves; // Q copies per wave
     static_assert(NQC * 256 * kFanWaves == kRows * DK, "whole 1 KiB copies per wave");
