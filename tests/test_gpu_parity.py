@@ -421,6 +421,9 @@ DESC_CASES = [
     # writes its partial for the combine instead of merging the output)
     (16, 8, 208, 256, 2304, 1, 0, 2048),
     (16, 8, 256, 256, 4352, 0, 0, 0),
+    # ... and with padding rows in the last 16-row unit (500 rows)
+    (16, 8, 256, 250, 2304, 0, 0, 0),
+    (16, 8, 256, 250, 2304, 1, 0, 2054),
     # head dim 512 (and 320, padded to 512) through the wave-pair tiled
     # kernel, one pass and one chunk per block
     (16, 2, 512, 100, 700, 1, 0, 600),
