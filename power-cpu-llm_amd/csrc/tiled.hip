@@ -10,11 +10,12 @@
 //
 // Per tile each wave runs the score chain, online softmax and P.V chain of
 // the canonical arithmetic (attention_device.hpp). The merges are rare (every
-// 8 and every 128 tiles), so their accumulators live in memory rather than
-// registers: the span accumulator in the row's own output slot, the running
-// total across spans in the workspace; the last merge writes the normalised
-// output. Tiles wholly masked for the workgroup are never loaded; tiles
-// wholly masked for a wave are skipped by that wave.
+// 8 and every 128 tiles), so their accumulators live outside the registers:
+// the span accumulator's leading 64-dim blocks in the LDS beside the stages,
+// the rest in the row's own output slot, the running total across spans in
+// the workspace; the last merge writes the normalised output. Tiles wholly
+// masked for the workgroup are never loaded; tiles wholly masked for a wave
+// are skipped by that wave.
 //
 // split != 0: the workgroup computes the single chunk c_lo + z0 + blockIdx.z
 // and writes its chunk partial for the combine kernels. A split launch whose
@@ -24,6 +25,7 @@
 // at head dim 64); each row's arithmetic is the same either way.
 #include "attention_device.hpp"
 
+#include <algorithm>
 #include <atomic>
 
 namespace pcl {
@@ -36,10 +38,16 @@ bool fan_supported(int dk);
 constexpr int kTiledWaves = 8;
 constexpr int kTiledRows = kTiledWaves * kRows; // 128
 
+// LDS of one workgroup: two K/V stages, then the leading 64-dim blocks of
+// the span accumulator (as many as the 160 KiB of a CU hold beside the
+// stages: one at head dim 256, all of them at 128 and 64).
 template <int DK> struct TiledLds {
     static constexpr int tileFloats = kTile * DK;
     static constexpr int stage = 2 * tileFloats; // K then V
-    static constexpr size_t bytes = 2 * stage * sizeof(float);
+    static constexpr int stageFloats = 2 * stage;
+    static constexpr int blockFloats = kTiledRows * 64; // one 64-dim block of every row
+    static constexpr int spanBlocks = std::min(DK / 64, (40960 - stageFloats) / blockFloats);
+    static constexpr size_t bytes = (size_t)(stageFloats + spanBlocks * blockFloats) * sizeof(float);
 };
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
@@ -81,7 +89,9 @@ void tiled_kernel(Params p, int split, int z0)
     constexpr int NQ = DK / 64;                // 64-dim output groups
     constexpr int NI = kTile * DK / 256 / W;   // DMA pieces per wave per array
     constexpr int ROWS = W * kRows;            // rows of the workgroup
+    constexpr int NL = LD::spanBlocks;         // span accumulator blocks kept in LDS
     static_assert(NI * W * 256 == kTile * DK, "whole 1 KiB pieces per wave");
+    static_assert(ROWS == kTiledRows, "LDS span blocks sized for the workgroup");
     extern __shared__ float lds[];
 
     const int tid = threadIdx.x;
@@ -192,6 +202,13 @@ void tiled_kernel(Params p, int split, int z0)
     auto acc_pos = [&](int a, int i) {
         return 64 * a + 64 <= p.dim ? 64 * a + 16 * i + 4 * g : 64 * a + 16 * g + 4 * i;
     };
+    // Blocks a < NL of the span accumulator stay in LDS instead, private to
+    // the wave: 256 bytes per row, the lane's 16-byte slot 4g + i XOR-ed
+    // with the row so that the 16 rows of one access hit distinct banks.
+    float *const lspan = lds + LD::stageFloats + w * NL * kRows * 64;
+    auto lacc = [&](int a, int i) -> f4 & {
+        return *(f4 *)(lspan + a * kRows * 64 + col * 64 + 4 * ((4 * g + i) ^ col));
+    };
 
     // Chunk merge into the span, and at a span end the span merge into the
     // total (not the last merge: flush_last below).
@@ -228,14 +245,17 @@ void tiled_kernel(Params p, int split, int z0)
                     const int dm = acc_pos(a, i);
                     f4 s1 = f4{0.f, 0.f, 0.f, 0.f};
                     if (!first1)
-                        s1 = ldg4(a1 + dm);
+                        s1 = a < NL ? lacc(a, i) : ldg4(a1 + dm);
                     if (chunk) {
 #pragma unroll
                         for (int j = 0; j < 4; ++j)
                             s1[j] = merge_value(s1[j], O[a][j][i], f1);
                     }
                     if (!span_end) {
-                        stg4(a1 + dm, s1);
+                        if (a < NL)
+                            lacc(a, i) = s1;
+                        else
+                            stg4(a1 + dm, s1);
                         continue;
                     }
                     f4 s2 = f4{0.f, 0.f, 0.f, 0.f};
@@ -295,7 +315,7 @@ void tiled_kernel(Params p, int split, int z0)
             for (int i = 0; i < 4; ++i) {
                 s1v[a][i] = f4{0.f, 0.f, 0.f, 0.f};
                 if (!first1 && 64 * a + 16 * g + 4 * i < p.dim)
-                    s1v[a][i] = ldg4(a1 + acc_pos(a, i));
+                    s1v[a][i] = a < NL ? lacc(a, i) : ldg4(a1 + acc_pos(a, i));
             }
         bool nonfinite = false;
 #pragma unroll
