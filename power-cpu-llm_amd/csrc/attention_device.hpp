@@ -133,6 +133,21 @@ __device__ __forceinline__ f4 ldg4(const float *p)
 
 // Streaming load for data read exactly once (decode K/V): the nontemporal
 // hint keeps it from displacing reused lines; the HBM stream runs faster.
+// s_waitcnt immediate for vmcnt(n) alone (gfx9 encoding: vmcnt in bits 3:0
+// and 15:14; expcnt 7 and lgkmcnt 15 wait for nothing), for
+// __builtin_amdgcn_s_waitcnt. The compiler's own waits know this form (an
+// inline-asm wait they would not).
+constexpr int waitcnt_vm(int n)
+{
+    return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8);
+}
+
+// The same with lgkmcnt(0): every LDS access of the wave complete too.
+constexpr int waitcnt_vm_lgkm0(int n)
+{
+    return (n & 15) | ((n >> 4) << 14) | (7 << 4);
+}
+
 __device__ __forceinline__ f4 ldg4_stream(const float *p)
 {
     return __builtin_nontemporal_load((gf4_cptr)p);

@@ -83,20 +83,6 @@ template <int DK> struct FanCfg {
 typedef __attribute__((address_space(3))) void *fan_lptr_t;
 typedef const __attribute__((address_space(1))) void *fan_gptr_t;
 
-// s_waitcnt immediate for vmcnt(n) alone (gfx9 encoding: vmcnt in bits 3:0
-// and 15:14; expcnt 7 and lgkmcnt 15 wait for nothing). The compiler's own
-// waits know this form (an inline-asm wait they would not).
-constexpr int waitcnt_vm(int n)
-{
-    return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8);
-}
-
-// The same with lgkmcnt(0): every LDS access of the wave complete too.
-constexpr int waitcnt_vm_lgkm0(int n)
-{
-    return (n & 15) | ((n >> 4) << 14) | (7 << 4);
-}
-
 // A workgroup barrier that leaves vector-memory loads in flight (the caller
 // has waited for whatever the other waves must see; __syncthreads would
 // also wait for every LDS copy still in flight). The empty statements keep

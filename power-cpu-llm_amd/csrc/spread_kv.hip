@@ -7,7 +7,8 @@
 //   wave at head dim 256): the canonical score chain of attention_device.hpp
 //   on K read straight into MFMA operands, published to the workspace;
 //   output dims [32j, 32j + 32) (16 per wave): V for those dims and all 256
-//   keys is copied into LDS, requested right behind the wave's K.
+//   keys, requested right behind the wave's K and Q (all before the first
+//   wait) and kept in LDS.
 // The two waves then read the chunk's raw scores back (half each, shared
 // through LDS) and each runs the
 // tile-by-tile online softmax and the P.V chain for its own dims exactly as
@@ -104,7 +105,7 @@ __device__ __forceinline__ void spread_merge(const Params &p, int64_t e)
         atomicOr(p.err, kErrOutput);
 }
 
-template <int DK, bool FULL, bool CAP>
+template <int DK, bool FULL, bool CAP, bool EARLY>
 __global__ __launch_bounds__(kSpreadThreads, 2) void spread_kv_kernel(Params p)
 {
     if ((int)blockIdx.z >= p.nkv * p.units) { // an appended merge workgroup
@@ -147,51 +148,107 @@ __global__ __launch_bounds__(kSpreadThreads, 2) void spread_kv_kernel(Params p)
     const int d0 = kSpreadSliceDims * slice + 16 * w; // the wave's output dims
 
     {
-        // Q^T B operands: Q[row][32u + 8g + jj] * q_scale (0 for padding rows).
+        // K of this wave's score blocks (MFMA A operands), Q^T (B operands:
+        // Q[row][32u + 8g + jj] * q_scale, 0 for padding rows) and V of the
+        // wave's 16 dims for the chunk's 256 keys: lane L of block i moves
+        // 16 bytes (dims d0 + 4(L % 4) ..) of key 16i + 4(s % 4) + s / 4
+        // into LDS slot s = L / 4. A dim past the head's last reads the
+        // head's first dims instead (that output is dropped).
+        const int blk0 = (slice * kSpreadWaves + w) * BPW;
+        f4 kb[BPW][NU][2];
         float q[NU][8];
+        f4 vr[EARLY ? kBlocksPerChunk : 1];
         const int query = rin ? row / p.group : 0;
         const int h = kh * p.group + (rin ? row % p.group : 0);
         const float *qp = p.q + (int64_t)query * p.q_stride + (int64_t)h * p.dim;
+        const int sl = lane >> 2;
+        const int kin = 4 * (sl & 3) + (sl >> 2);
+        const int vd = 4 * (lane & 3);
+        const int dv = FULL || d0 + vd < p.dim ? d0 + vd : 0;
+        if constexpr (EARLY) {
+            // At most one workgroup per CU: every request goes out before
+            // the first wait, K (from HBM) first, then Q (from L2), then V
+            // into registers (written to LDS once the scores are out;
+            // register loads, because with LDS copies also in flight the
+            // compiler would wait for all of them before the first score
+            // step).
 #pragma unroll
-        for (int u = 0; u < NU; ++u)
+            for (int i = 0; i < BPW; ++i) {
+                const int64_t key = cbase + 16 * (blk0 + i) + col;
+                const float *kp = key_row(p, key < klast ? key : klast) + hoff;
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const int d = 32 * u + 8 * g + 4 * hh;
-                const bool din = FULL || d < p.dim;
-                const f4 x = ldg4(qp + (din ? d : 0)) * p.q_scale;
-                const f4 v = (rin && din) ? x : f4{0.f, 0.f, 0.f, 0.f};
+                for (int u = 0; u < NU; ++u)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    q[u][4 * hh + j] = v[j];
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const int d = 32 * u + 8 * g + 4 * hh;
+                        kb[i][u][hh] = ldg4_stream(kp + (FULL || d < p.dim ? d : 0));
+                    }
             }
-        // K of this wave's score blocks, straight into MFMA A operands
-        const int blk0 = (slice * kSpreadWaves + w) * BPW;
-        f4 kb[BPW][NU][2];
+            f4 qr[NU][2];
 #pragma unroll
-        for (int i = 0; i < BPW; ++i) {
-            const int64_t key = cbase + 16 * (blk0 + i) + col;
-            const float *kp = key_row(p, key < klast ? key : klast) + hoff;
+            for (int u = 0; u < NU; ++u)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int d = 32 * u + 8 * g + 4 * hh;
+                    qr[u][hh] = ldg4(qp + (FULL || d < p.dim ? d : 0));
+                }
+#pragma unroll
+            for (int i = 0; i < kBlocksPerChunk; ++i) {
+                const int64_t key = cbase + 16 * i + kin;
+                vr[i] = ldg4_stream(value_row(p, key < klast ? key : klast) + hoff + dv);
+            }
+            // K and Q have landed; V may still be in flight
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(kBlocksPerChunk));
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int u = 0; u < NU; ++u)
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
                     const int d = 32 * u + 8 * g + 4 * hh;
                     const bool din = FULL || d < p.dim;
-                    const f4 x = ldg4_stream(kp + (din ? d : 0));
-                    kb[i][u][hh] = din ? x : f4{0.f, 0.f, 0.f, 0.f};
+                    const f4 x = qr[u][hh] * p.q_scale;
+                    const f4 v = (rin && din) ? x : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        q[u][4 * hh + j] = v[j];
+                    if (!din) {
+#pragma unroll
+                        for (int i = 0; i < BPW; ++i)
+                            kb[i][u][hh] = f4{0.f, 0.f, 0.f, 0.f};
+                    }
                 }
-        }
-        // V of the wave's 16 dims, HBM -> LDS with no register staging,
-        // requested behind K so that it streams while the scores are formed:
-        // lane L of block i's copy moves 16 bytes (dims d0 + 4(L % 4) ..)
-        // of key 16i + 4(s % 4) + s / 4 into slot s = L / 4. A dim past the
-        // head's last copies the head's first dims instead (that output is
-        // dropped).
-        {
-            const int sl = lane >> 2;
-            const int kin = 4 * (sl & 3) + (sl >> 2);
-            const int vd = 4 * (lane & 3);
-            const int dv = FULL || d0 + vd < p.dim ? d0 + vd : 0;
+        } else {
+            // Two workgroups per CU: Q, then K, then V copied HBM -> LDS
+            // with no register staging behind each wave's K (all requested
+            // up front measured slower here: the second workgroup's K then
+            // queues behind the first one's V).
+#pragma unroll
+            for (int u = 0; u < NU; ++u)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int d = 32 * u + 8 * g + 4 * hh;
+                    const bool din = FULL || d < p.dim;
+                    const f4 x = ldg4(qp + (din ? d : 0)) * p.q_scale;
+                    const f4 v = (rin && din) ? x : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        q[u][4 * hh + j] = v[j];
+                }
+#pragma unroll
+            for (int i = 0; i < BPW; ++i) {
+                const int64_t key = cbase + 16 * (blk0 + i) + col;
+                const float *kp = key_row(p, key < klast ? key : klast) + hoff;
+#pragma unroll
+                for (int u = 0; u < NU; ++u)
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const int d = 32 * u + 8 * g + 4 * hh;
+                        const bool din = FULL || d < p.dim;
+                        const f4 x = ldg4_stream(kp + (din ? d : 0));
+                        kb[i][u][hh] = din ? x : f4{0.f, 0.f, 0.f, 0.f};
+                    }
+            }
             float *vl = &vlds[w][0][0][0];
 #pragma unroll
             for (int i = 0; i < kBlocksPerChunk; ++i) {
@@ -213,6 +270,12 @@ __global__ __launch_bounds__(kSpreadThreads, 2) void spread_kv_kernel(Params p)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
                 publish(words + ((blk0 + i) * 4 + r) * 64 + lane, p.epoch, acc[r]);
+        }
+        if constexpr (EARLY) {
+            float *vl = &vlds[w][0][0][0];
+#pragma unroll
+            for (int i = 0; i < kBlocksPerChunk; ++i)
+                *(f4 *)(vl + i * 256 + 4 * lane) = vr[i];
         }
     }
 
@@ -250,7 +313,7 @@ __global__ __launch_bounds__(kSpreadThreads, 2) void spread_kv_kernel(Params p)
             for (int r = 0; r < 4; ++r)
                 slds[w * HB + b][r][lane] = __uint_as_float((uint32_t)x[b][r]);
     }
-    // the V copies have landed (s_waitcnt covers the LDS copies too) and both
+    // the V copies have landed (s_waitcnt covers LDS copies too) and both
     // halves of the scores are in LDS
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -353,6 +416,8 @@ __global__ __launch_bounds__(kSpreadThreads, 2) void spread_kv_kernel(Params p)
     }
 }
 
+int device_cus();
+
 int spread_slices(int dk)
 {
     return dk / kSpreadSliceDims;
@@ -370,10 +435,21 @@ static hipError_t launch_cap(const Params &p, hipStream_t stream)
         merge_planes = (int)((threads + per_plane - 1) / per_plane);
     }
     const dim3 grid(DK / kSpreadSliceDims, p.nch, p.nkv * p.units + merge_planes);
-    if (p.dim == DK)
-        spread_kv_kernel<DK, true, CAP><<<grid, kSpreadThreads, 0, stream>>>(p);
-    else
-        spread_kv_kernel<DK, false, CAP><<<grid, kSpreadThreads, 0, stream>>>(p);
+    // every request up front when the item workgroups take at most one per CU
+    const int64_t wgs = (int64_t)(DK / kSpreadSliceDims) * p.nch * p.nkv * p.units;
+    const int cus = device_cus();
+    const bool early = cus > 0 && wgs <= cus;
+    if (p.dim == DK) {
+        if (early)
+            spread_kv_kernel<DK, true, CAP, true><<<grid, kSpreadThreads, 0, stream>>>(p);
+        else
+            spread_kv_kernel<DK, true, CAP, false><<<grid, kSpreadThreads, 0, stream>>>(p);
+    } else {
+        if (early)
+            spread_kv_kernel<DK, false, CAP, true><<<grid, kSpreadThreads, 0, stream>>>(p);
+        else
+            spread_kv_kernel<DK, false, CAP, false><<<grid, kSpreadThreads, 0, stream>>>(p);
+    }
     return hipGetLastError();
 }
 
