@@ -1,20 +1,22 @@
 // Spread split-KV decode for gfx950: one 256-key chunk over S = DK/32
-// workgroups, for short decodes whose (chunk, 16-row unit, KV head) items
-// are too few to fill the chip (a 2K decode has 64 of them on 256 CUs).
+// slices of two waves, for short decodes whose (chunk, 16-row unit, KV head)
+// items are too few to fill the chip (a 2K decode has 64 of them on 256
+// CUs).
 //
-// Workgroup j of an item runs two waves and takes
+// Slice j of an item takes
 //   the scores of 16 / S of the chunk's 16 key blocks (one 16-key block per
 //   wave at head dim 256): the canonical score chain of attention_device.hpp
 //   on K read straight into MFMA operands, published to the workspace;
 //   output dims [32j, 32j + 32) (16 per wave): V for those dims and all 256
-//   keys, requested right behind the wave's K and Q (all before the first
-//   wait) and kept in LDS.
-// The two waves then read the chunk's raw scores back (half each, shared
-// through LDS) and each runs the
-// tile-by-tile online softmax and the P.V chain for its own dims exactly as
-// the other kernels do (every workgroup of the item derives the same m, l
-// and probabilities, bit for bit). So each workgroup reads 1/S of the
-// chunk's K and 1/S of its V, and a 2K decode runs 512 workgroups.
+//   keys, requested behind the wave's K and kept in LDS.
+// A workgroup runs one slice (two waves) or two (four waves, so that a
+// launch of up to two slices per CU still has one workgroup per CU). Its
+// waves then read the chunk's raw scores back (a share each, shared through
+// LDS) and each runs the tile-by-tile online softmax and the P.V chain for
+// its own dims exactly as the other kernels do (every workgroup of the item
+// derives the same m, l and probabilities, bit for bit). So each slice
+// reads 1/S of the chunk's K and 1/S of its V, and a 2K decode runs 512
+// slices.
 //
 // Publication needs no flag and no fence: every score is stored as one
 // 64-bit word (the launch's epoch, the score's bits) with a device-coherent
@@ -42,15 +44,13 @@
 
 namespace pcl {
 
-constexpr int kSpreadWaves = 2;
+constexpr int kSliceWaves = 2; // waves per 32-dim slice
 constexpr int kSpreadSliceDims = 32;
 constexpr int kBlocksPerChunk = 2 * kTilesPerChunk; // 16-key blocks
 
 typedef __attribute__((address_space(3))) void *spread_lptr_t;
 typedef const __attribute__((address_space(1))) void *spread_gptr_t;
 
-// Threads of a spread workgroup.
-constexpr int kSpreadThreads = 64 * kSpreadWaves;
 
 // Merge role: thread e of the merge workgroups owns four dims of one row of
 // one KV head; it takes every chunk partial of that row as published words
@@ -105,35 +105,38 @@ __device__ __forceinline__ void spread_merge(const Params &p, int64_t e)
         atomicOr(p.err, kErrOutput);
 }
 
-template <int DK, bool FULL, bool CAP, bool EARLY>
-__global__ __launch_bounds__(kSpreadThreads, 2) void spread_kv_kernel(Params p)
+template <int DK, bool FULL, bool CAP, bool EARLY, int WV>
+__global__ __launch_bounds__(64 * WV, 2) void spread_kv_kernel(Params p)
 {
     if ((int)blockIdx.z >= p.nkv * p.units) { // an appended merge workgroup
         const int64_t mw = blockIdx.x + (int64_t)gridDim.x *
                                             (blockIdx.y + (int64_t)gridDim.y *
                                                               (blockIdx.z - p.nkv * p.units));
-        spread_merge(p, mw * kSpreadThreads + threadIdx.x);
+        spread_merge(p, mw * (64 * WV) + threadIdx.x);
         return;
     }
-    constexpr int S = DK / kSpreadSliceDims;                  // workgroups per item
-    constexpr int BPW = kBlocksPerChunk / (S * kSpreadWaves); // score blocks per wave
-    constexpr int NU = DK / 32;                               // score chain steps
-    static_assert(BPW >= 1 && BPW * S * kSpreadWaves == kBlocksPerChunk, "whole blocks");
+    constexpr int S = DK / kSpreadSliceDims;                 // slices per item
+    constexpr int SPW = WV / kSliceWaves;                    // slices per workgroup
+    constexpr int BPW = kBlocksPerChunk / (S * kSliceWaves); // score blocks per wave
+    constexpr int NU = DK / 32;                              // score chain steps
+    static_assert(BPW >= 1 && BPW * S * kSliceWaves == kBlocksPerChunk, "whole blocks");
+    static_assert(SPW >= 1 && S % SPW == 0 && kBlocksPerChunk % WV == 0, "whole slices");
 
     // V of each wave's 16 dims for the chunk's 256 keys, 1 KiB per 16-key
     // block: slot j of a block (64 bytes, 16 dims) holds key 4(j % 4) + j / 4
     // of the block, so the four keys 4g + r an MFMA step reads sit in four
     // different 64-byte bank groups
-    __shared__ float vlds[kSpreadWaves][kBlocksPerChunk][16][16];
-    // the chunk's raw scores, [block][r][lane], gathered by both waves
+    __shared__ float vlds[WV][kBlocksPerChunk][16][16];
+    // the chunk's raw scores, [block][r][lane], gathered by all waves
     __shared__ float slds[kBlocksPerChunk][4][64];
-    const int slice = blockIdx.x;
     const int ci = blockIdx.y; // the launch's chunk index
     const int c = p.c_lo + ci;
     const int unit = blockIdx.z % p.units;
     const int kvl = blockIdx.z / p.units;
     const int64_t item = ((int64_t)blockIdx.z * p.nch + ci);
     const int w = threadIdx.x >> 6;
+    const int slice = blockIdx.x * SPW + w / kSliceWaves;
+    const int ws = w % kSliceWaves; // the wave within its slice
     const int lane = threadIdx.x & 63;
     const int col = lane & 15;
     const int g = lane >> 4;
@@ -145,7 +148,7 @@ __global__ __launch_bounds__(kSpreadThreads, 2) void spread_kv_kernel(Params p)
     const int64_t hoff = (int64_t)kh * p.dim;
     // the item's words: [block][r][lane]
     uint64_t *words = p.ws_tag + item * (kBlocksPerChunk * 64 * 4);
-    const int d0 = kSpreadSliceDims * slice + 16 * w; // the wave's output dims
+    const int d0 = kSpreadSliceDims * slice + 16 * ws; // the wave's output dims
 
     {
         // K of this wave's score blocks (MFMA A operands), Q^T (B operands:
@@ -154,7 +157,7 @@ __global__ __launch_bounds__(kSpreadThreads, 2) void spread_kv_kernel(Params p)
         // 16 bytes (dims d0 + 4(L % 4) ..) of key 16i + 4(s % 4) + s / 4
         // into LDS slot s = L / 4. A dim past the head's last reads the
         // head's first dims instead (that output is dropped).
-        const int blk0 = (slice * kSpreadWaves + w) * BPW;
+        const int blk0 = (slice * kSliceWaves + ws) * BPW;
         f4 kb[BPW][NU][2];
         float q[NU][8];
         f4 vr[EARLY ? kBlocksPerChunk : 1];
@@ -280,9 +283,10 @@ __global__ __launch_bounds__(kSpreadThreads, 2) void spread_kv_kernel(Params p)
     }
 
     // The chunk's raw scores once every word carries this launch's epoch
-    // (bounded): each wave takes half of the blocks and leaves them in LDS.
+    // (bounded): each wave takes its share of the blocks and leaves them in
+    // LDS.
     {
-        constexpr int HB = kBlocksPerChunk / kSpreadWaves;
+        constexpr int HB = kBlocksPerChunk / WV;
         uint64_t x[HB][4];
         for (int polls = 0;;) {
             // an opaque base each pass: the loads' addresses are formed here
@@ -374,7 +378,7 @@ __global__ __launch_bounds__(kSpreadThreads, 2) void spread_kv_kernel(Params p)
             tile_step(t, ok, __any(any));
         }
     }
-    if (bad && slice == 0 && w == 0)
+    if (bad && slice == 0 && ws == 0)
         atomicOr(p.err, kErrScore);
 
     // O[i] is dim d0 + 4g + i of row `row`.
@@ -410,7 +414,7 @@ __global__ __launch_bounds__(kSpreadThreads, 2) void spread_kv_kernel(Params p)
         for (int i = 0; i < 4; ++i)
             publish(pw + d + i, p.epoch, O[i]);
     }
-    if (slice == 0 && w == 0 && g == 0) {
+    if (slice == 0 && ws == 0 && g == 0) {
         publish(pw + p.dk, p.epoch, m);
         publish(pw + p.dk + 1, p.epoch, l);
     }
@@ -423,33 +427,41 @@ int spread_slices(int dk)
     return dk / kSpreadSliceDims;
 }
 
+template <int DK, bool CAP, bool EARLY, int WV>
+static void launch_form(const Params &p, int merge_planes, hipStream_t stream)
+{
+    const dim3 grid(DK / kSpreadSliceDims / (WV / kSliceWaves), p.nch,
+                    p.nkv * p.units + merge_planes);
+    if (p.dim == DK)
+        spread_kv_kernel<DK, true, CAP, EARLY, WV><<<grid, 64 * WV, 0, stream>>>(p);
+    else
+        spread_kv_kernel<DK, false, CAP, EARLY, WV><<<grid, 64 * WV, 0, stream>>>(p);
+}
+
 template <int DK, bool CAP>
 static hipError_t launch_cap(const Params &p, hipStream_t stream)
 {
+    constexpr int S = DK / kSpreadSliceDims;
     // merge workgroups (one thread per four dims of a row) as whole planes
-    // after the items' planes
+    // after the items' planes (S x 128 threads a chunk in every form)
     int merge_planes = 0;
     if (p.ws_ptag) {
         const int64_t threads = (int64_t)p.nkv * p.nrows * (p.dim / 4);
-        const int64_t per_plane = (int64_t)(DK / kSpreadSliceDims) * p.nch * kSpreadThreads;
+        const int64_t per_plane = (int64_t)S * p.nch * 64 * kSliceWaves;
         merge_planes = (int)((threads + per_plane - 1) / per_plane);
     }
-    const dim3 grid(DK / kSpreadSliceDims, p.nch, p.nkv * p.units + merge_planes);
-    // every request up front when the item workgroups take at most one per CU
-    const int64_t wgs = (int64_t)(DK / kSpreadSliceDims) * p.nch * p.nkv * p.units;
+    // Every request goes out up front when the item workgroups take at most
+    // one CU each: two-wave workgroups (one slice) when they fit so, four-wave
+    // ones (two slices) when those do; otherwise two-wave workgroups, two or
+    // three per CU, in the compiler's order.
+    const int64_t slices = (int64_t)S * p.nch * p.nkv * p.units;
     const int cus = device_cus();
-    const bool early = cus > 0 && wgs <= cus;
-    if (p.dim == DK) {
-        if (early)
-            spread_kv_kernel<DK, true, CAP, true><<<grid, kSpreadThreads, 0, stream>>>(p);
-        else
-            spread_kv_kernel<DK, true, CAP, false><<<grid, kSpreadThreads, 0, stream>>>(p);
-    } else {
-        if (early)
-            spread_kv_kernel<DK, false, CAP, true><<<grid, kSpreadThreads, 0, stream>>>(p);
-        else
-            spread_kv_kernel<DK, false, CAP, false><<<grid, kSpreadThreads, 0, stream>>>(p);
-    }
+    if (cus > 0 && slices <= cus)
+        launch_form<DK, CAP, true, 2>(p, merge_planes, stream);
+    else if (cus > 0 && S % 2 == 0 && slices <= 2 * (int64_t)cus)
+        launch_form<DK, CAP, true, 4>(p, merge_planes, stream);
+    else
+        launch_form<DK, CAP, false, 2>(p, merge_planes, stream);
     return hipGetLastError();
 }
 
