@@ -46,8 +46,9 @@ constexpr int kPipeMaxDk = 512;
 // Up to head dim 256 the pipelined kernel was as fast or faster at every
 // size tried (16 to 1024 items, d64/128/256).
 constexpr int64_t kPipeMinItemsWide = 512;
-// The spread decode's workgroups (dk/32 per item, two waves and 48 KiB of
-// LDS each, so three per CU) all fit on the chip at once up to this many:
+// The spread decode's slices (dk/32 per item; a two-wave workgroup with 48
+// KiB of LDS each, three per CU, or two per four-wave workgroup when they
+// take at most two per CU) all fit on the chip at once up to this many:
 // 256 CUs x 3. Its workgroups wait for each other, so it is chosen only
 // within that bound and within the items its score-word region holds
 // (requested beyond them, the pipelined kernel runs).
