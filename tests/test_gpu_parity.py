@@ -550,6 +550,41 @@ def test_spread_waits_give_up_at_the_host_limit_then_recover(pcl, torch, ctx):
         other.close()
 
 
+SPREAD_FORM_CASES = [
+    # qheads, kvh, dim, nq, nkeys, first_query. The spread decode's launch
+    # forms on a 256-CU MI355X: two-wave workgroups with every request up
+    # front (at most one 32-dim slice per CU), four-wave workgroups of two
+    # slices (two slices per CU), two-wave workgroups in the compiler's order
+    # (up to three per CU)
+    (16, 8, 256, 1, 1024, 1023),  # 32 items, 256 slices: two-wave, early
+    (16, 8, 256, 1, 2048, 2047),  # 64 items, 512 slices: four-wave
+    (16, 8, 256, 1, 3072, 3071),  # 96 items, 768 slices: two-wave, compiler order
+    (16, 8, 208, 1, 2048, 2047),  # head dim below the padded 256: four-wave
+    (16, 8, 128, 1, 4096, 4095),  # 128 items, 512 slices at d128: four-wave
+    (16, 8, 128, 1, 2000, 1999),  # ragged last chunk at d128: two-wave, early
+    (8, 4, 64, 4, 1500, 1496),    # d64, four queries of two heads per KV head
+]
+
+
+@pytest.mark.parametrize("case", SPREAD_FORM_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_spread_forms_match_the_pipelined_kernel_and_the_oracle(pcl, torch, ctx, oracle, case):
+    qheads, kvh, dim, nq, nkeys, fq = case
+    g = np.random.default_rng(sum(case))
+    q = prescale(g.standard_normal((nq, qheads * dim), dtype=np.float32), dim)
+    k = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+    v = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+    got, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, pcl.KERNEL_SPREAD_KV, 1, 0, 0, fq)
+    assert err == 0
+    ref, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, pcl.KERNEL_PIPE_KV, 1, 0, 0, fq)
+    assert err == 0
+    assert np.array_equal(bits(got), bits(ref))
+    for i in range(nq):
+        ok, want = oracle.heads(q[i], k, v, qheads, kvh, dim, nkeys,
+                                oracle.encoder_mask(0, nkeys, fq + i, None))
+        assert ok
+        assert_parity(got[i], want, dim)
+
+
 def test_split_launch_tail_with_masks_segments_and_kv_ranges(torch, ctx, oracle):
     # the canvas shape (4 row blocks x 8 KV heads x 9 chunks = 288 items on
     # 256 CUs) leaves one chunk's items for a last round, which runs as
