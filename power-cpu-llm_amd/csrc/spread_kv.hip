@@ -222,10 +222,11 @@ __global__ __launch_bounds__(64 * WV, 2) void spread_kv_kernel(Params p)
                     }
                 }
         } else {
-            // Two workgroups per CU: Q, then K, then V copied HBM -> LDS
-            // with no register staging behind each wave's K (all requested
-            // up front measured slower here: the second workgroup's K then
-            // queues behind the first one's V).
+            // Two or three workgroups per CU: Q, then K, then V copied
+            // HBM -> LDS with no register staging behind each wave's K (all
+            // requested up front measured slower with two two-wave
+            // workgroups per CU: the second one's K then queued behind the
+            // first one's V).
 #pragma unroll
             for (int u = 0; u < NU; ++u)
 #pragma unroll
