@@ -48,6 +48,18 @@ WORKLOADS = {
     "decode_32k_window1024": (16, 8, 256, 1, 32768, True, 1024, 32767, "decode", False),
     "decode_32k": (16, 8, 256, 1, 32768, True, 0, 32767, "decode", False),
     "decode_128k_d512": (16, 2, 512, 1, 131072, True, 0, 131071, "decode", True),
+    # the same global-layer decode (16/2/512, unit-norm K) at shorter caches
+    "decode_2k_d512": (16, 2, 512, 1, 2048, True, 0, 2047, "decode", True),
+    "decode_8k_d512": (16, 2, 512, 1, 8192, True, 0, 8191, "decode", True),
+    "decode_32k_d512": (16, 2, 512, 1, 32768, True, 0, 32767, "decode", True),
+    # the reference's own attention throughput probe
+    # (src/kernels/quantized/int8/tests.rs:770-809): 8 queries over every key
+    # (no mask) of a sliding-layer and a global-layer geometry, device-resident
+    # and through the AttentionMulti entry over host arrays (the engine's call)
+    "probe_sliding_q8": (16, 8, 256, 8, 1279, False, 0, 0, "decode", False),
+    "probe_global_q8": (16, 2, 512, 8, 3194, False, 0, 0, "decode", False),
+    "probe_sliding_q8_host": (16, 8, 256, 8, 1279, False, 0, 0, "host", False),
+    "probe_global_q8_host": (16, 2, 512, 8, 3194, False, 0, 0, "host", False),
     "prefill_4k_window1024": (16, 8, 256, 4096, 4096, True, 1024, 0, "prefill", False),
     "prefill_4k": (16, 8, 256, 4096, 4096, True, 0, 0, "prefill", False),
     "canvas_256x2304": (16, 8, 256, 256, 2304, False, 0, 2048, "canvas", False),
@@ -84,6 +96,17 @@ WORKLOADS = {
     "decode_32k_host_fanout": (16, 8, 256, 1, 32768, True, 0, 32767, "host", False),
 }
 HEADLINE = "decode_32k"
+# host-array workloads timed in a default run (the others only when named)
+DEFAULT_HOST = ("probe_sliding_q8_host", "probe_global_q8_host")
+# BASELINE.json's configs (and the reference's probe shapes): each carries a
+# CPU baseline beside its GPU figure
+CPU_LEGS = ("decode_2k", "decode_32k_window1024", "decode_32k", "decode_128k_d512",
+            "prefill_4k_window1024", "prefill_4k", "canvas_256x2304", "probe_sliding_q8",
+            "probe_global_q8")
+# rows of a prefill or canvas the CPU leg computes: every n-th query row
+# (on all threads; on one thread)
+ROW_SAMPLE = {"prefill_4k": (16, 128), "prefill_4k_window1024": (16, 128),
+              "canvas_256x2304": (8, 64)}
 # hidden width of the layer workload's output block (that of output_decode)
 LAYER_HIDDEN = 2816
 # the metric's second half: f32 prefill attention at 4K tokens (the global
@@ -268,7 +291,7 @@ def time_host_workload(torch, pcl, name, steps, warmup, seed):
     q, k, v = make_inputs(torch, name, seed)
     hq, hk, hv = (np.ascontiguousarray(x.cpu().numpy().reshape(-1)) for x in (q, k, v))
     del q, k, v
-    out = np.empty(qh * dim, np.float32)
+    out = np.empty(nq * qh * dim, np.float32)
     lib = pcl.load()
     fptr = ctypes.POINTER(ctypes.c_float)
 
@@ -276,7 +299,14 @@ def time_host_workload(torch, pcl, name, steps, warmup, seed):
 
     def one(h0, h1):
         # all keys allowed: the decode position is the last key (no mask)
-        if not lib.pcl_hip_attention_f32_heads(
+        if nq > 1:
+            # AttentionMulti over every KV head (the probe's attention_multi)
+            if not lib.pcl_hip_attention_f32_multi_kv(
+                    hq.ctypes.data_as(fptr), nq, qh * dim, hk.ctypes.data_as(fptr),
+                    hv.ctypes.data_as(fptr), qh, kvh, dim, nkeys, None, nkeys, None,
+                    out.ctypes.data_as(fptr), qh * dim, 0, kvh):
+                raise RuntimeError("pcl_hip_attention_f32_multi_kv failed for %s" % name)
+        elif not lib.pcl_hip_attention_f32_heads(
                 hq.ctypes.data_as(fptr), hk.ctypes.data_as(fptr), hv.ctypes.data_as(fptr),
                 qh, kvh, dim, nkeys, None, None,
                 out[h0 * dim:].ctypes.data_as(fptr), h0, h1):
@@ -493,75 +523,94 @@ def time_cache_workload(torch, pcl, ctx, name, steps, warmup, nsets, seed, trans
     return ev, wall, kernel, host, roles, nsets
 
 
+def host_inputs(name, host):
+    """Q, K, V of a timed input set as flat host arrays (a canvas's two K/V
+    segments joined in key order)."""
+    q = host["q"].cpu().numpy().reshape(-1)
+    k, v = host["k"].cpu().numpy(), host["v"].cpu().numpy()
+    if host.get("kc") is not None:
+        k = np.concatenate([k, host["kc"].cpu().numpy()])
+        v = np.concatenate([v, host["vc"].cpu().numpy()])
+    return q, k.reshape(-1), v.reshape(-1)
+
+
+def reference_gmacs(name, sec):
+    """The reference probe's own rate (int8/tests.rs:800-806): 2 nq qheads
+    nkeys dim multiply-adds (scores and P.V) per call."""
+    qh, kvh, dim, nq, nkeys = WORKLOADS[name][:5]
+    return 2.0 * nq * qh * nkeys * dim / sec / 1e9
+
+
 def cpu_baseline(name, host, threads, budget_s=20.0):
     """The oracle's exact path (port of p9_ref_attention_heads), engine
-    threading, timed on a bounded sample: whole decode calls, repeated."""
+    threading, timed on a bounded sample: whole calls of the workload,
+    repeated (median); the same on one core and the binary32 twin (port of
+    pa_attention_f32_heads, the portable-int8 backends' path)."""
     from oracle import binding as orc
     qh, kvh, dim, nq, nkeys, causal, window, fq, kind, _ = WORKLOADS[name]
-    q = host["q"].cpu().numpy().reshape(-1)
-    k = host["k"].cpu().numpy().reshape(-1)
-    v = host["v"].cpu().numpy().reshape(-1)
-    times = []
-    out = None
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 50):
-        t0 = time.perf_counter()
-        ok, out = orc.threaded(q, nq, k, v, qh, kvh, dim, nkeys, causal, 0, fq, window,
-                               threads=threads)
-        times.append(time.perf_counter() - t0)
-        if not ok:
-            raise RuntimeError("oracle error")
-        if time.perf_counter() > t_end and len(times) >= 5:
-            break
-    med = float(np.median(times))
+    q, k, v = host_inputs(name, host)
+
+    def timed(nthreads, reps, budget, binary32=False):
+        times, out = [], None
+        t_end = time.perf_counter() + budget
+        while len(times) < 1 or (time.perf_counter() < t_end and len(times) < reps):
+            t0 = time.perf_counter()
+            ok, out = orc.threaded(q, nq, k, v, qh, kvh, dim, nkeys, causal, 0, fq, window,
+                                   threads=nthreads, binary32=binary32)
+            times.append(time.perf_counter() - t0)
+            if not ok:
+                raise RuntimeError("oracle error")
+        return float(np.median(times)), len(times), out
+
+    med, runs, out = timed(threads, 50, budget_s)
     gpu = host["out"].cpu().numpy().reshape(-1)
     maxerr = float(np.max(np.abs(gpu - out)))
-    # the same call on one host core (median of 5)
-    one = []
-    for _ in range(5):
-        t0 = time.perf_counter()
-        orc.threaded(q, nq, k, v, qh, kvh, dim, nkeys, causal, 0, fq, window, threads=1)
-        one.append(time.perf_counter() - t0)
-    # the binary32 twin (port of pa_attention_f32_heads, the portable-int8
-    # backends' path) with the same threads (median of 5)
-    b32 = []
-    for _ in range(5):
-        t0 = time.perf_counter()
-        ok, _ = orc.threaded(q, nq, k, v, qh, kvh, dim, nkeys, causal, 0, fq, window,
-                             threads=threads, binary32=True)
-        b32.append(time.perf_counter() - t0)
-        if not ok:
-            raise RuntimeError("oracle error")
-    return med, len(times), maxerr, float(np.median(one)), float(np.median(b32))
+    med1, runs1, _ = timed(1, 5, budget_s / 2)
+    med32, runs32, _ = timed(threads, 5, budget_s / 4, binary32=True)
+    _, bytes_, _ = work(name)
+    cpu = {"value": bytes_ / med / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+           "sample": "%d whole %s calls (exact f64 path, engine head split), median %.4f s"
+                     % (runs, name, med),
+           "value_1core": bytes_ / med1 / 1e9,
+           "sample_1core": "%d whole calls on one thread, median %.4f s" % (runs1, med1),
+           "value_binary32": bytes_ / med32 / 1e9,
+           "sample_binary32": "%d whole calls of the binary32 twin (pa_attention_f32 path), "
+                              "%d threads, median %.4f s" % (runs32, threads, med32),
+           "gpu_vs_oracle_maxabs": maxerr}
+    if nq > 1:
+        cpu["GMAC/s"] = reference_gmacs(name, med)
+        cpu["GMAC/s_1core"] = reference_gmacs(name, med1)
+        cpu["GMAC/s_binary32"] = reference_gmacs(name, med32)
+    return cpu
 
 
-def cpu_baseline_prefill(name, host, threads, budget_s=20.0):
-    """The oracle's exact path over a prefill, as the engine runs a prompt
-    (contiguous query ranges per worker, each query its own call with its
-    causal mask), on a sample: every PREFILL_SAMPLE_STEP-th query row of the
-    prompt, timed whole and repeated; rates count the sampled rows' own
-    algorithmic flops."""
+def cpu_baseline_rows(name, host, threads, budget_s=20.0):
+    """The oracle's exact path over a prefill or canvas, as the engine runs
+    one (contiguous query ranges per worker, each query its own call with
+    its own mask), on a sample: every n-th query row (ROW_SAMPLE), timed
+    whole and repeated; rates count the sampled rows' own algorithmic
+    flops."""
     from oracle import binding as orc
     qh, kvh, dim, nq, nkeys, causal, window, fq, kind, _ = WORKLOADS[name]
-    q = host["q"].cpu().numpy().reshape(nq, qh * dim)
-    k = host["k"].cpu().numpy().reshape(-1)
-    v = host["v"].cpu().numpy().reshape(-1)
+    q, k, v = host_inputs(name, host)
+    q = q.reshape(nq, qh * dim)
     gpu = host["out"].cpu().numpy().reshape(nq, qh * dim)
+    step, step1 = ROW_SAMPLE[name]
 
-    def sample_flops(step):
+    def sample_flops(stride):
         pairs = 0
-        for i in range(0, nq, step):
+        for i in range(0, nq, stride):
             pairs += allowed_pairs(1, nkeys, causal, window, fq + i)
         return 4 * dim * qh * pairs
 
-    def run(step, nthreads, reps):
-        rows = np.ascontiguousarray(q[::step])
+    def run(stride, nthreads, reps):
+        rows = np.ascontiguousarray(q[::stride])
         times, out = [], None
         t_end = time.perf_counter() + budget_s
         while len(times) < reps or (time.perf_counter() < t_end and len(times) < 2 * reps):
             t0 = time.perf_counter()
             ok, out = orc.threaded(rows.reshape(-1), rows.shape[0], k, v, qh, kvh, dim, nkeys,
-                                   causal, 0, fq, window, threads=nthreads, query_step=step)
+                                   causal, 0, fq, window, threads=nthreads, query_step=stride)
             times.append(time.perf_counter() - t0)
             if not ok:
                 raise RuntimeError("oracle error")
@@ -569,20 +618,34 @@ def cpu_baseline_prefill(name, host, threads, budget_s=20.0):
                 break
         return float(np.median(times)), len(times), out.reshape(rows.shape[0], -1)
 
-    med, runs, out = run(PREFILL_SAMPLE_STEP, threads, 3)
-    maxerr = float(np.max(np.abs(gpu[::PREFILL_SAMPLE_STEP] - out)))
-    med1, _, _ = run(PREFILL_SAMPLE_STEP_1CORE, 1, 3)
-    return {"value": sample_flops(PREFILL_SAMPLE_STEP) / med / 1e12, "unit": "TFLOP/s",
+    med, runs, out = run(step, threads, 3)
+    maxerr = float(np.max(np.abs(gpu[::step] - out)))
+    med1, _, _ = run(step1, 1, 3)
+    if causal:
+        masks = "their own causal%s masks" % (" + window %d" % window if window else "")
+    else:
+        masks = "every key, no mask"
+    return {"value": sample_flops(step) / med / 1e12, "unit": "TFLOP/s",
             "cores": threads, "kind": "port",
-            "sample": "every %dth query row of the %d-token prompt (%d rows, all heads, "
-                      "their own causal%s masks), exact f64 path, %d whole runs, "
-                      "median %.3f s" % (PREFILL_SAMPLE_STEP, nq, len(range(0, nq,
-                                         PREFILL_SAMPLE_STEP)),
-                                         " + window %d" % window if window else "", runs, med),
-            "value_1core": sample_flops(PREFILL_SAMPLE_STEP_1CORE) / med1 / 1e12,
-            "sample_1core": "every %dth query row on one thread, median %.3f s"
-                            % (PREFILL_SAMPLE_STEP_1CORE, med1),
+            "sample": "every %dth query row of the %d queries (%d rows, all heads, %s), exact "
+                      "f64 path, %d whole runs, median %.3f s"
+                      % (step, nq, len(range(0, nq, step)), masks, runs, med),
+            "value_1core": sample_flops(step1) / med1 / 1e12,
+            "sample_1core": "every %dth query row on one thread, median %.3f s" % (step1, med1),
             "gpu_vs_oracle_maxabs": maxerr}
+
+
+def cpu_leg(name, host, threads, budget_s):
+    """The CPU baseline of one workload (whole decode calls, or sampled
+    prefill/canvas rows), with the host's core counts and model."""
+    kind = WORKLOADS[name][8]
+    if kind in ("prefill", "canvas"):
+        cpu = cpu_baseline_rows(name, host, threads, budget_s)
+    else:
+        cpu = cpu_baseline(name, host, threads, budget_s)
+    cpu["affinity_cores"] = len(os.sched_getaffinity(0))
+    cpu["cpu"] = cpu_model()
+    return cpu
 
 
 def cpu_share():
@@ -678,7 +741,8 @@ def main():
     # sets), which is the harness's doing, not the kernel's.
     names = ([args.workload] if args.workload
              else [HEADLINE] + [n for n in WORKLOADS
-                                if n != HEADLINE and WORKLOADS[n][8] != "host"])
+                                if n != HEADLINE and WORKLOADS[n][8] != "host"] +
+             list(DEFAULT_HOST))
     results = {}
     hosts = {}
     for name in names:
@@ -707,8 +771,10 @@ def main():
             r["frac_hbm"] = r["GB/s"] / HBM_PEAK_GBS
         else:
             r["frac_mfma"] = r["TFLOP/s"] / FP32_MFMA_PEAK_TFS
+        if nq_of(name) > 1 and name.startswith("probe_"):
+            r["GMAC/s"] = reference_gmacs(name, ev * 1e-3)
         results[name] = r
-        if name == HEADLINE or name == PREFILL[0]:
+        if name in CPU_LEGS or name == args.workload:
             hosts[name] = host
         else:
             del host
@@ -719,29 +785,22 @@ def main():
     head = args.workload or HEADLINE
     hr = results[head]
     kind = WORKLOADS[head][8]
-    cpu = None
     threads, affinity = cpu_share()
-    if not args.no_cpu and head in hosts and kind == "decode":
-        med, runs, maxerr, med1, med32 = cpu_baseline(head, hosts[head], threads,
-                                                      args.cpu_budget)
-        flops, bytes_, _ = work(head)
-
-        def rate(sec):
-            return (bytes_ / sec / 1e9) if kind == "decode" else (flops / sec / 1e12)
-
-        cpu = {"value": rate(med),
-               "unit": "GB/s" if kind == "decode" else "TFLOP/s", "cores": threads,
-               "kind": "port",
-               "sample": "%d whole %s calls (exact f64 path, engine head split), median %.3f s"
-                         % (runs, head, med),
-               "value_1core": rate(med1),
-               "sample_1core": "5 whole calls on one thread, median %.3f s" % med1,
-               "value_binary32": rate(med32),
-               "sample_binary32": "5 whole calls of the binary32 twin (pa_attention_f32 "
-                                  "path), %d threads, median %.3f s" % (threads, med32),
-               "affinity_cores": affinity,
-               "cpu": cpu_model(),
-               "gpu_vs_oracle_maxabs": maxerr}
+    # the CPU baseline beside each BASELINE config (the headline's with the
+    # full budget, the others with a shorter one), after every GPU timing
+    if not args.no_cpu:
+        for name in results:
+            if name not in hosts or hosts[name] is None:
+                continue
+            if name not in CPU_LEGS and name != args.workload:
+                continue
+            if WORKLOADS[name][8] not in ("decode", "prefill", "canvas"):
+                continue
+            budget = args.cpu_budget if name == head else min(args.cpu_budget, 8.0)
+            results[name]["cpu_baseline"] = cpu_leg(name, hosts[name], threads, budget)
+            print("# cpu %s: %s" % (name, results[name]["cpu_baseline"]["sample"]),
+                  file=sys.stderr)
+    cpu = results[head].get("cpu_baseline")
     qh, kvh, dim, nq, nkeys, causal, window, fq, _, _ = WORKLOADS[head]
     if kind == "host":
         # host buffers: the copies dominate; no kernel roofline applies
@@ -766,11 +825,7 @@ def main():
         block = {"metric": "prefill attn TFLOP/s (% fp32 MFMA peak) at 4K tokens",
                  "value": r["TFLOP/s"], "unit": "TFLOP/s", "ms_per_step": r["ms"],
                  "steps": r["steps"], "roofline": roofline(name, r), "cpu_baseline": None}
-        if not args.no_cpu and name in hosts:
-            cb = cpu_baseline_prefill(name, hosts[name], threads, args.cpu_budget)
-            cb["affinity_cores"] = affinity
-            cb["cpu"] = cpu_model()
-            block["cpu_baseline"] = cb
+        block["cpu_baseline"] = r.get("cpu_baseline")
         prefill[name] = block
     line = {
         "metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": hr["steps"],
@@ -784,6 +839,7 @@ def main():
         "prefill": prefill or None,
         "configs": {n: {k: (round(x, 5) if isinstance(x, float) else x) for k, x in r.items()}
                     for n, r in results.items()},
+        "host_cores": {"share": threads, "affinity": affinity, "cpu": cpu_model()},
     }
     print(json.dumps(line))
 

@@ -110,13 +110,19 @@ enum pcl_kernel {
     PCL_KERNEL_TILED_SPLIT = 3, /* LDS-tiled prefill, one key chunk per block */
     PCL_KERNEL_PIPE_KV = 4,     /* pipelined split-KV decode (score/value wave
                                    pairs, head dim <= 256) + ordered combine */
-    PCL_KERNEL_TWO_PASS = 5,    /* split-KV decode as a K-streaming pass and a
-                                   V-streaming pass + ordered combine */
+    /* 5 is retired (a two-launch decode that no choice selected) and is
+       refused with PCL_INVALID_PARAMETER */
     PCL_KERNEL_SPREAD_KV = 6,   /* split-KV decode with each key chunk spread
                                    over head_dim/32 workgroups that exchange
                                    raw scores (head dim <= 256, short
                                    launches); the launch's own merge
                                    workgroups run the ordered combine */
+    PCL_KERNEL_FAN_KV = 7,      /* split-KV decode with each (key chunk,
+                                   16-row unit, KV head) item fanned over the
+                                   eight waves of one workgroup (head dims
+                                   above 64, launches of two or more chunks;
+                                   otherwise the pipelined kernel runs) +
+                                   ordered combine */
 };
 
 /* Attention of nq query positions over keys [0, n0+n1): keys 0..n0-1 come
@@ -206,12 +212,15 @@ size_t pcl_attention_workspace_bytes(const pcl_attention_desc *desc);
  * more than 64 Mi floats of running totals; the 32K and 128K decodes, the
  * 4K prefills and the 256 x 2304 canvas fit). Calls no hipMalloc, hipFree
  * or other allocating routine and records no timing spans. Every call on
- * one GPU shares that GPU's array, which keeps the last call's contents (no
- * part of it needs to start at zero: each launch writes every partial
- * before its combine reads it): calls that overlap on one GPU, on
- * different streams or contexts, race and must be serialised by the
- * caller. PCL_NON_FINITE_VALUE if the scratch address could not be taken
- * for this context's device. */
+ * one GPU shares that GPU's array, which keeps the last call's contents.
+ * The partials need no clearing (each launch writes every partial before
+ * its combine reads it); the region of published words at the array's
+ * start must hold no word of the current epoch, which the array's zero
+ * contents at load give and the library restores (a fill kernel on the
+ * call's stream) whenever the device's epoch counter has wrapped since.
+ * Calls that overlap on one GPU, on different streams or contexts, race
+ * and must be serialised by the caller. PCL_NON_FINITE_VALUE if the scratch
+ * address could not be taken for this context's device. */
 int pcl_attention_launch_noalloc(pcl_context *ctx, const pcl_attention_desc *desc);
 int pcl_context_reserve(pcl_context *ctx, size_t bytes);
 /* Wait for the stream; *device_error receives the error flag (bit 0: a
@@ -223,19 +232,28 @@ int pcl_context_sync(pcl_context *ctx, int *device_error);
 /* Kernel the descriptor resolves to under PCL_KERNEL_AUTO. */
 int pcl_attention_resolve_kernel(const pcl_attention_desc *desc);
 
-/* Bound of the waits between workgroups of one launch (the spread decode's
- * score exchange and its merge of chunk partials), in polls of a few hundred
- * cycles each; 0 restores the default (65536, some tens of milliseconds).
- * A wait that runs out sets bit 4 (16) of the device error flag and its
- * workgroup finishes without its result: the launch's output is then not
- * valid. Callers whose GPU is shared with other work may lower or raise it;
- * tests use a tiny limit to exercise the failure path. ctx NULL sets the
- * limit of the context the host-pointer entries (section 1) use; those
- * entries rerun a launch whose waits ran out with the pipelined kernel,
- * which never waits, so their result is unaffected. No counterpart in the
- * reference (its CPU threads do not wait on each other inside an attention
- * call). PCL_INVALID_PARAMETER for a negative limit. */
+/* Bound of the spread decode's waits for the scores of the other
+ * workgroups of a key chunk, in polls of a few hundred cycles each; 0
+ * restores the default (65536, some tens of milliseconds). A wave whose wait
+ * runs out forms the missing score blocks itself by the same chain (the
+ * same bits), so the launch's result stays valid: a GPU shared with other
+ * work, on which some of a launch's workgroups may not run alongside the
+ * others, costs time, not correctness. Tests use a tiny limit to exercise
+ * that path. The launch's merge workgroups wait only for workgroups
+ * dispatched before them, under a fixed guard of about a second; bit 4 (16)
+ * of the device error flag reports a guard that ran out (then the output is
+ * not valid; the host-pointer entries of section 1 rerun such a launch with
+ * the pipelined kernel, which never waits). ctx NULL sets the limit of the
+ * context the host-pointer entries use. No counterpart in the reference
+ * (its CPU threads do not wait on each other inside an attention call).
+ * PCL_INVALID_PARAMETER for a negative limit. */
 int pcl_context_set_wait_limit(pcl_context *ctx, int polls);
+/* Testing hook, no counterpart in the reference: sets the device's epoch
+ * counter (the spread decode's launches each take the next value; its low
+ * 32 bits are the epoch its published words carry, its high bits count
+ * wraps) so that a test can run launches across a wrap. PCL_INVALID_SHAPE
+ * for a device index outside the library's table. */
+int pcl_debug_set_epoch_counter(int device, uint64_t value);
 
 /* Per-kernel timing, the device-side counterpart of the engine's stage
  * timers (stats::Span, src/engine/stats.rs:9-64). While enabled, every launch

@@ -15,6 +15,18 @@
  * table-driven IBM exp) differs from it in the last bit on some inputs, so
  * the exact path matches the reference to the last bit except where such an
  * ulp decides a rounding.
+ *
+ * Licence notice for the two libm restatements (power8_expf and
+ * glibc228_sincosf, with their helpers and constants): they restate
+ * algorithms of the GNU C Library 2.28, sysdeps/powerpc/powerpc64/power8/
+ * fpu/e_expf.S (Copyright (C) 2016-2018 Free Software Foundation, Inc.) and
+ * sysdeps/ieee754/flt-32/s_sincosf.c and s_sincosf.h (Copyright (C)
+ * 2017-2018 Free Software Foundation, Inc.), which are licensed under the
+ * GNU Lesser General Public License version 2.1 or (at your option) any
+ * later version, as are the reference's own ports of them (src/libm.rs;
+ * the reference's LICENSE and THIRD-PARTY-NOTICES). Those parts of this file
+ * are distributed under the same licence. They are test infrastructure: no
+ * product code includes or links them.
  */
 #include "attention_oracle.h"
 

@@ -35,10 +35,13 @@ OK, INVALID_SHAPE, INVALID_PARAMETER, NON_FINITE_VALUE, RESOURCE_LIMIT = 0, 1, 2
 ERROR_NAMES = {INVALID_SHAPE: "InvalidShape", INVALID_PARAMETER: "InvalidParameter",
                NON_FINITE_VALUE: "NonFiniteValue", RESOURCE_LIMIT: "ResourceLimit"}
 (KERNEL_AUTO, KERNEL_SPLIT_KV, KERNEL_TILED, KERNEL_TILED_SPLIT, KERNEL_PIPE_KV,
- KERNEL_TWO_PASS, KERNEL_SPREAD_KV) = 0, 1, 2, 3, 4, 5, 6
+ KERNEL_SPREAD_KV, KERNEL_FAN_KV) = 0, 1, 2, 3, 4, 6, 7
+# every explicit kernel choice (5 is retired and refused)
+KERNELS = (KERNEL_SPLIT_KV, KERNEL_TILED, KERNEL_TILED_SPLIT, KERNEL_PIPE_KV, KERNEL_SPREAD_KV,
+           KERNEL_FAN_KV)
 KERNEL_NAMES = {KERNEL_SPLIT_KV: "split_kv", KERNEL_TILED: "tiled",
                 KERNEL_TILED_SPLIT: "tiled_split", KERNEL_PIPE_KV: "pipe_kv",
-                KERNEL_TWO_PASS: "two_pass", KERNEL_SPREAD_KV: "spread_kv"}
+                KERNEL_SPREAD_KV: "spread_kv", KERNEL_FAN_KV: "fan_kv"}
 
 # Every symbol include/pcl_attention.h declares.
 EXPORTS = (
@@ -57,6 +60,7 @@ EXPORTS = (
     "pcl_context_sync",
     "pcl_attention_resolve_kernel",
     "pcl_context_set_wait_limit",
+    "pcl_debug_set_epoch_counter",
     "pcl_context_set_timing",
     "pcl_context_timing",
     "pcl_kv_cache_create",

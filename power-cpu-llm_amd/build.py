@@ -12,7 +12,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libpcl_attention.so")
 OBJ_DIR = os.path.join(HERE, "_build")
-SOURCES = ["csrc/split_kv.hip", "csrc/pipe_kv.hip", "csrc/two_pass.hip", "csrc/spread_kv.hip",
+SOURCES = ["csrc/split_kv.hip", "csrc/pipe_kv.hip", "csrc/spread_kv.hip",
            "csrc/tiled.hip", "csrc/tiled_wide.hip", "csrc/fan_kv.hip",
            "csrc/api.hip", "csrc/kv_cache.hip", "csrc/head_transform.hip",
            "csrc/output_block.hip"]

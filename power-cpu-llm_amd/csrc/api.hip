@@ -16,11 +16,11 @@ hipError_t launch_split_kv(const Params &p, hipStream_t stream);
 hipError_t launch_combine(const Params &p, hipStream_t stream);
 hipError_t launch_pipe_kv(const Params &p, hipStream_t stream);
 hipError_t launch_tiled(const Params &p, int split, hipStream_t stream, bool *merged);
-hipError_t launch_two_pass(const Params &p, hipStream_t stream);
+hipError_t launch_fan_kv(const Params &p, hipStream_t stream);
 hipError_t launch_spread_kv(const Params &p, hipStream_t stream);
 int tiled_rows(int dk);
-int rec_floats();
 int spread_slices(int dk);
+int device_cus();
 // published score words (64-bit) of one spread item: 16 key blocks x 4 x 64
 // lanes
 constexpr size_t kSpreadWordsPerItem = 2 * kTilesPerChunk * 4 * 64;
@@ -48,11 +48,13 @@ constexpr int kPipeMaxDk = 512;
 constexpr int64_t kPipeMinItemsWide = 512;
 // The spread decode's slices (dk/32 per item; a two-wave workgroup with 48
 // KiB of LDS each, three per CU, or two per four-wave workgroup when they
-// take at most two per CU) all fit on the chip at once up to this many:
-// 256 CUs x 3. Its workgroups wait for each other, so it is chosen only
+// take at most two per CU) all fit on the chip at once up to this many per
+// CU of the device the launch runs on (768 on a whole MI355X; fewer on a
+// partitioned one). Its workgroups wait for each other, so it is chosen only
 // within that bound and within the items its score-word region holds
 // (requested beyond them, the pipelined kernel runs).
-constexpr int64_t kSpreadMaxWorkgroups = 768;
+constexpr int64_t kSpreadSlicesPerCu = 3;
+constexpr int kMi355xCus = 256;
 // Every non-empty workspace begins with the spread decode's region of
 // published words: the score words of up to kSpreadMaxItems (chunk, unit,
 // KV head) items, then their chunk partials (16 rows x (256 + 2) words an
@@ -64,17 +66,40 @@ constexpr size_t kSpreadPartWords = (size_t)kSpreadMaxItems * pcl::kRows * (256 
 constexpr size_t kTagFloats = 2 * (kSpreadScoreWords + kSpreadPartWords);
 
 // Epochs of spread launches, per device: every launch on a device takes a
-// new one (shared by all contexts and the allocation-free scratch).
+// new one (shared by all contexts and the allocation-free scratch). The
+// counter is 64-bit: its low word is the epoch a kernel compares, its high
+// word the generation, which grows each time the epoch wraps. A region of
+// published words holds only zeros and words of one generation's launches
+// (whose epochs are unique); a launch of a later generation zeroes the
+// region first, so a word left from before a wrap can never carry the
+// current epoch.
 constexpr int kMaxEpochDevices = 64;
-std::atomic<uint32_t> g_epoch[kMaxEpochDevices];
+std::atomic<uint64_t> g_epoch[kMaxEpochDevices];
 
-uint32_t next_epoch(int device)
+struct Epoch {
+    uint32_t epoch;
+    uint32_t generation;
+};
+
+std::atomic<uint64_t> &epoch_counter(int device)
 {
-    std::atomic<uint32_t> &e = g_epoch[device >= 0 && device < kMaxEpochDevices ? device : 0];
-    uint32_t v = e.fetch_add(1, std::memory_order_relaxed) + 1;
-    while (v == 0) // 0 is the value of a flag never written
+    return g_epoch[device >= 0 && device < kMaxEpochDevices ? device : 0];
+}
+
+Epoch next_epoch(int device)
+{
+    std::atomic<uint64_t> &e = epoch_counter(device);
+    uint64_t v = e.fetch_add(1, std::memory_order_relaxed) + 1;
+    while ((uint32_t)v == 0) // 0 is the value of a word never written
         v = e.fetch_add(1, std::memory_order_relaxed) + 1;
-    return v;
+    return Epoch{(uint32_t)v, (uint32_t)(v >> 32)};
+}
+
+// The generation of the device's next launch (what a region zeroed now is
+// valid for).
+uint32_t current_generation(int device)
+{
+    return (uint32_t)((epoch_counter(device).load(std::memory_order_relaxed) + 1) >> 32);
 }
 
 void report(const char *what, hipError_t e)
@@ -97,11 +122,9 @@ struct Plan {
     Params p;
     int kernel = PCL_KERNEL_SPLIT_KV;
     // workspace floats: the spread decode's score words, then chunk and
-    // span partials (or the tiled kernel's running totals) and the two-pass
-    // tile records
+    // span partials (or the tiled kernel's running totals)
     size_t ws_floats = 0;
     size_t part_floats = 0;
-    size_t rec_floats = 0;
     bool empty = false;    // nothing to compute
 };
 
@@ -132,10 +155,12 @@ int64_t spread_workgroups(int dk, int64_t nrows, int64_t nkv, int64_t nch)
     return nch * nkv * units * pcl::spread_slices(dk);
 }
 
-int choose_kernel(int requested, int dk, int64_t nrows, int64_t nkv, int64_t nch)
+// cus: compute units of the device the launch runs on (the spread decode's
+// workgroups must all be resident at once).
+int choose_kernel(int requested, int dk, int64_t nrows, int64_t nkv, int64_t nch, int cus)
 {
     const int64_t spread = spread_workgroups(dk, nrows, nkv, nch);
-    const bool spread_fits = spread > 0 && spread <= kSpreadMaxWorkgroups;
+    const bool spread_fits = spread > 0 && spread <= kSpreadSlicesPerCu * (int64_t)cus;
     if (requested == PCL_KERNEL_SPREAD_KV)
         return spread_fits ? requested : dk <= kPipeMaxDk ? PCL_KERNEL_PIPE_KV
                                                            : PCL_KERNEL_SPLIT_KV;
@@ -145,8 +170,8 @@ int choose_kernel(int requested, int dk, int64_t nrows, int64_t nkv, int64_t nch
         return requested;
     if (requested == PCL_KERNEL_PIPE_KV)
         return dk <= kPipeMaxDk ? requested : PCL_KERNEL_SPLIT_KV;
-    if (requested == PCL_KERNEL_TWO_PASS)
-        return requested;
+    if (requested == PCL_KERNEL_FAN_KV)
+        return dk >= 128 && nch >= 2 ? requested : PCL_KERNEL_PIPE_KV;
     if (dk > kTiledMaxDk || nrows < 64) {
         // decode: short launches spread each chunk over several workgroups;
         // otherwise the pipelined kernel; at head dim 512 short launches (few
@@ -174,7 +199,7 @@ int make_plan(const pcl_attention_desc &d, int64_t h_lo, int64_t h_hi, int64_t h
         d.dim % 16 != 0 || d.dim > kMaxDim || d.nq < 0 || d.n0 < 0 || d.n1 < 0 ||
         d.kh_first < 0 || d.kh_first > d.kh_end || d.kh_end > d.kvheads || d.window < 0)
         return PCL_INVALID_SHAPE;
-    if (d.kernel < PCL_KERNEL_AUTO || d.kernel > PCL_KERNEL_SPREAD_KV)
+    if (d.kernel < PCL_KERNEL_AUTO || d.kernel > PCL_KERNEL_FAN_KV || d.kernel == 5)
         return PCL_INVALID_PARAMETER;
     // negative, NaN, infinite or subnormal caps, and caps whose f32
     // reciprocal (what the kernels multiply by) would be subnormal
@@ -255,7 +280,10 @@ int make_plan(const pcl_attention_desc &d, int64_t h_lo, int64_t h_hi, int64_t h
     p.nch = (int)nch;
     p.dk = dk;
 
-    plan->kernel = choose_kernel(d.kernel, dk, nrows, nkv, nch);
+    // the current device's CU count; with no device to ask (host-only
+    // queries: nothing launches there) a whole MI355X's
+    const int cus = pcl::device_cus();
+    plan->kernel = choose_kernel(d.kernel, dk, nrows, nkv, nch, cus > 0 ? cus : kMi355xCus);
     if (plan->kernel == PCL_KERNEL_TILED_SPLIT) {
         // the tiled kernel's rows come in whole workgroup blocks
         p.nrows_pad = (int)round_up(nrows, pcl::tiled_rows(dk));
@@ -267,7 +295,7 @@ int make_plan(const pcl_attention_desc &d, int64_t h_lo, int64_t h_hi, int64_t h
     const bool partials = plan->kernel == PCL_KERNEL_TILED_SPLIT ||
                           ((plan->kernel == PCL_KERNEL_SPLIT_KV ||
                             plan->kernel == PCL_KERNEL_PIPE_KV ||
-                            plan->kernel == PCL_KERNEL_TWO_PASS) && nch > 1);
+                            plan->kernel == PCL_KERNEL_FAN_KV) && nch > 1);
     plan->part_floats = 0;
     if (partials) {
         plan->part_floats = (size_t)nkv * p.nrows_pad * nch * (dk + 2);
@@ -278,10 +306,7 @@ int make_plan(const pcl_attention_desc &d, int64_t h_lo, int64_t h_hi, int64_t h
         plan->part_floats = (size_t)nkv * p.nrows_pad * dk;
     }
     plan->part_floats = round_up((int64_t)plan->part_floats, 4);
-    plan->rec_floats = 0;
-    if (plan->kernel == PCL_KERNEL_TWO_PASS)
-        plan->rec_floats = (size_t)nkv * p.units * nch * pcl::rec_floats();
-    const size_t body = plan->part_floats + plan->rec_floats;
+    const size_t body = plan->part_floats;
     plan->ws_floats = body || plan->kernel == PCL_KERNEL_SPREAD_KV ? kTagFloats + body : 0;
     return PCL_OK;
 }
@@ -291,6 +316,23 @@ __global__ void zero_words_kernel(uint32_t *words, int n)
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n)
         words[i] = 0;
+}
+
+// Zeroes the published-word region at the start of a workspace of `bytes`
+// on ctx's stream (a fill kernel rather than a memset node, should a caller
+// capture this) and records the generation it is valid for in *gen.
+int zero_tag_region(pcl_context *ctx, void *ws, size_t bytes, uint32_t *gen)
+{
+    const int nwords = (int)std::min<size_t>(kTagFloats, bytes / sizeof(uint32_t));
+    *gen = current_generation(ctx->device);
+    zero_words_kernel<<<(nwords + 255) / 256, 256, 0, ctx->stream>>>(
+        static_cast<uint32_t *>(ws), nwords);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        report("workspace score words", e);
+        return PCL_NON_FINITE_VALUE;
+    }
+    return PCL_OK;
 }
 
 int ensure_workspace(pcl_context *ctx, size_t bytes)
@@ -311,17 +353,8 @@ int ensure_workspace(pcl_context *ctx, size_t bytes)
     }
     ctx->ws_bytes = bytes;
     // a new buffer's score-word region starts at zero, an epoch no launch
-    // takes (a fill kernel rather than a memset node, should a caller
-    // capture this)
-    const int nwords = (int)std::min<size_t>(kTagFloats, bytes / sizeof(uint32_t));
-    zero_words_kernel<<<(nwords + 255) / 256, 256, 0, ctx->stream>>>(
-        static_cast<uint32_t *>(ctx->ws), nwords);
-    e = hipGetLastError();
-    if (e != hipSuccess) {
-        report("workspace score words", e);
-        return PCL_NON_FINITE_VALUE;
-    }
-    return PCL_OK;
+    // takes
+    return zero_tag_region(ctx, ctx->ws, bytes, &ctx->ws_tag_gen);
 }
 
 hipEvent_t take_event(pcl_context *ctx)
@@ -364,8 +397,9 @@ void close_span(pcl_context *ctx, int idx)
         (void)hipEventRecord(ctx->spans[idx].stop, ctx->stream);
 }
 
-// Launches a plan with its workspace at `ws` (plan.ws_floats floats).
-int run_plan_ws(pcl_context *ctx, Plan &plan, float *ws)
+// Launches a plan with its workspace at `ws` (plan.ws_floats floats; its
+// published-word region last zeroed for generation *tag_gen).
+int run_plan_ws(pcl_context *ctx, Plan &plan, float *ws, uint32_t *tag_gen)
 {
     Params &p = plan.p;
     p.err = ctx->err;
@@ -381,20 +415,27 @@ int run_plan_ws(pcl_context *ctx, Plan &plan, float *ws)
                 p.ws2_ml = p.ws2_o + (size_t)p.nkv * p.nrows_pad * p.nspan * p.dk;
             }
         }
-        if (plan.rec_floats)
-            p.ws_rec = body + plan.part_floats;
         if (plan.kernel == PCL_KERNEL_SPREAD_KV) {
             p.ws_tag = reinterpret_cast<uint64_t *>(ws);
             if (p.nch > 1) // the launch merges its own chunk partials
                 p.ws_ptag = p.ws_tag + kSpreadScoreWords;
-            p.epoch = next_epoch(ctx->device);
+            const Epoch ep = next_epoch(ctx->device);
+            if (ep.generation != *tag_gen) {
+                // the epoch wrapped since the region was zeroed: words of
+                // the previous generation could carry this epoch
+                const int rc = zero_tag_region(ctx, ws, kTagFloats * sizeof(float), tag_gen);
+                if (rc != PCL_OK)
+                    return rc;
+                *tag_gen = ep.generation;
+            }
+            p.epoch = ep.epoch;
             p.max_polls = ctx->wait_polls;
         }
     }
     hipError_t e = hipSuccess;
     bool combine = plan.kernel == PCL_KERNEL_TILED_SPLIT ||
                          ((plan.kernel == PCL_KERNEL_SPLIT_KV || plan.kernel == PCL_KERNEL_PIPE_KV ||
-                           plan.kernel == PCL_KERNEL_TWO_PASS) &&
+                           plan.kernel == PCL_KERNEL_FAN_KV) &&
                           p.ws_o);
     int span = open_span(ctx, 0);
     switch (plan.kernel) {
@@ -404,8 +445,8 @@ int run_plan_ws(pcl_context *ctx, Plan &plan, float *ws)
     case PCL_KERNEL_PIPE_KV:
         e = pcl::launch_pipe_kv(p, ctx->stream);
         break;
-    case PCL_KERNEL_TWO_PASS:
-        e = pcl::launch_two_pass(p, ctx->stream);
+    case PCL_KERNEL_FAN_KV:
+        e = pcl::launch_fan_kv(p, ctx->stream);
         break;
     case PCL_KERNEL_TILED: {
         bool merged = false;
@@ -446,7 +487,7 @@ int run_plan(pcl_context *ctx, Plan &plan)
         if (rc != PCL_OK)
             return rc;
     }
-    return run_plan_ws(ctx, plan, static_cast<float *>(ctx->ws));
+    return run_plan_ws(ctx, plan, static_cast<float *>(ctx->ws), &ctx->ws_tag_gen);
 }
 
 // ---- the allocation-free entry's scratch ------------------------------------
@@ -463,6 +504,10 @@ constexpr int kMaxScratchDevices = 64;
 std::mutex g_scratch_mutex;
 void *g_scratch_ptr[kMaxScratchDevices];
 bool g_scratch_done[kMaxScratchDevices];
+// epoch generation for which each device's scratch was last zeroed (its
+// published-word region starts at zero, as the array does when the
+// library loads, in generation 0)
+uint32_t g_scratch_gen[kMaxScratchDevices];
 
 // This device's scratch address (the device must be current), or null when
 // its lookup failed.
@@ -827,10 +872,11 @@ int launch_plan(pcl_context *ctx, const pcl_attention_desc &desc, Plan *plan)
         return PCL_INVALID_SHAPE;
     const int64_t group = desc.qheads / desc.kvheads;
     const int64_t h_lo = desc.kh_first * group, h_hi = desc.kh_end * group;
+    // the kernel choice reads the current device's CU count
+    (void)hipSetDevice(ctx->device);
     int rc = make_plan(desc, h_lo, h_hi, h_lo, plan);
     if (rc != PCL_OK || plan->empty || plan->kernel != PCL_KERNEL_SPREAD_KV)
         return rc;
-    (void)hipSetDevice(ctx->device);
     if (!capturing(ctx->stream))
         return PCL_OK;
     if (desc.kernel != PCL_KERNEL_AUTO)
@@ -874,7 +920,9 @@ int pcl_attention_launch_noalloc(pcl_context *ctx, const pcl_attention_desc *des
     // no timing spans here: recording them creates events and grows a list
     const bool timing = ctx->timing;
     ctx->timing = false;
-    const int out = run_plan_ws(ctx, plan, static_cast<float *>(ctx->noalloc_scratch));
+    const int dev = ctx->device >= 0 && ctx->device < kMaxScratchDevices ? ctx->device : 0;
+    const int out = run_plan_ws(ctx, plan, static_cast<float *>(ctx->noalloc_scratch),
+                                &g_scratch_gen[dev]);
     ctx->timing = timing;
     return out;
 }
@@ -888,6 +936,14 @@ int pcl_context_set_wait_limit(pcl_context *ctx, int polls)
         return PCL_OK;
     }
     ctx->wait_polls = polls == 0 ? 1 << 16 : polls;
+    return PCL_OK;
+}
+
+int pcl_debug_set_epoch_counter(int device, uint64_t value)
+{
+    if (device < 0 || device >= kMaxEpochDevices)
+        return PCL_INVALID_SHAPE;
+    epoch_counter(device).store(value, std::memory_order_relaxed);
     return PCL_OK;
 }
 

@@ -103,8 +103,6 @@ struct Params {
     int s_lo;      // first span of the launch (absolute span index)
     int nspan;     // spans of the launch
     int dk;        // padded head dim of the launch
-    // tile records of the two-pass decode: [nkv][units][nch][kRecFloats]
-    float *ws_rec;
     // the spread decode's published scores, [items][16 blocks][4][64 lanes]
     // words of (epoch, score bits), and the launch's epoch
     uint64_t *ws_tag;
@@ -443,10 +441,14 @@ __device__ __forceinline__ Merged4 merge_chunks4(const Params &p, int64_t slot0,
 // accepts a word only when it carries the current epoch. The words live in
 // a workspace region that holds nothing else (zero when allocated; epochs
 // are never zero), so a stale word carries an earlier epoch. Every wait is
-// bounded by the launch's max_polls polls (kMaxPolls unless the context set
-// another limit).
+// bounded: a wait for another workgroup's scores by the launch's max_polls
+// polls (kMaxPolls unless the context set another limit), after which the
+// waiting wave forms what is missing itself; a wait of the merge workgroups
+// (which only ever wait for workgroups dispatched before them, and those
+// always finish) by kMergeMaxPolls, a guard against a fault elsewhere.
 
 constexpr int kMaxPolls = 1 << 16;
+constexpr int kMergeMaxPolls = 1 << 20;
 // Chunks whose partial words a merging thread requests per batch of loads.
 constexpr int kMergeBatch = 8;
 
@@ -486,7 +488,7 @@ __device__ __forceinline__ bool wait_partials(const Params &p, int64_t slot0, in
             fresh &= (uint32_t)(take(p.ws_ptag + (slot0 + ci) * stride + p.dk) >> 32) == p.epoch;
         if (__all(fresh))
             return true;
-        if (polls >= p.max_polls)
+        if (polls >= kMergeMaxPolls)
             return false;
         __builtin_amdgcn_s_sleep(8);
     }
@@ -528,7 +530,7 @@ __device__ __forceinline__ bool merge_words_batch(const Params &p, int64_t slot0
         }
         if (__all(fresh))
             break;
-        if (polls >= p.max_polls) {
+        if (polls >= kMergeMaxPolls) {
             ok = false;
             break;
         }

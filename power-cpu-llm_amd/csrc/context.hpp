@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
+#include <cstdint>
 #include <vector>
 
 // Event pair of one timed kernel role in one launch.
@@ -21,6 +22,9 @@ struct pcl_context {
     bool own_stream = false;
     void *ws = nullptr;
     size_t ws_bytes = 0;
+    // epoch generation for which the workspace's published-word region was
+    // last zeroed
+    uint32_t ws_tag_gen = 0;
     int *err = nullptr;
     // this device's scratch of pcl_attention_launch_noalloc (never freed)
     void *noalloc_scratch = nullptr;

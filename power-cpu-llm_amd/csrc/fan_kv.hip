@@ -139,6 +139,10 @@ __global__ __launch_bounds__(kFanThreads, 2) __attribute__((amdgpu_waves_per_eu(
 void fan_kv_kernel(Params p, int ci)
 {
     using C = FanCfg<DK>;
+    if constexpr (!MERGE) {
+        if (ci < 0) // a decode launch: one item per (chunk, unit, KV head)
+            ci = (int)blockIdx.y;
+    }
     constexpr int VD = C::VD, VW = C::VW, KU = C::KU, KPN = C::KPN, KB = C::KB;
     constexpr int VB = C::VB, VB0 = C::VB0, NK = C::NK;
     constexpr int NQC = kRows * DK / 256 / kFanWaves; // Q copies per wave
@@ -580,14 +584,15 @@ template <int DK, bool FULL, bool CAP, bool MERGE> static hipError_t configure_f
     return hipSuccess;
 }
 
+// ci < 0: every chunk of the launch (grid y), partials for the combine.
 template <int DK, bool FULL, bool CAP, bool MERGE>
 static hipError_t launch_fan_dk(const Params &p, int ci, hipStream_t stream)
 {
     const hipError_t e = configure_fan<DK, FULL, CAP, MERGE>();
     if (e != hipSuccess)
         return e;
-    fan_kv_kernel<DK, FULL, CAP, MERGE>
-        <<<dim3(p.units * p.nkv), kFanThreads, FanCfg<DK>::bytes, stream>>>(p, ci);
+    const dim3 grid(p.units * p.nkv, ci < 0 ? p.nch : 1);
+    fan_kv_kernel<DK, FULL, CAP, MERGE><<<grid, kFanThreads, FanCfg<DK>::bytes, stream>>>(p, ci);
     return hipGetLastError();
 }
 
@@ -621,12 +626,28 @@ bool fan_supported(int dk)
 // partial is written for the combine kernels.
 hipError_t launch_fan_chunk(const Params &p, int ci, bool merge_out, hipStream_t stream)
 {
-    if (merge_out && (p.nspan != 1 || ci < 1 || ci != p.nch - 1 || p.nch > kSpanChunks))
+    if (ci < 0 || ci >= p.nch ||
+        (merge_out && (p.nspan != 1 || ci < 1 || ci != p.nch - 1 || p.nch > kSpanChunks)))
         return hipErrorInvalidValue;
     switch (p.dk) {
     case 128: return launch_fan_cap<128>(p, ci, merge_out, stream);
     case 256: return launch_fan_cap<256>(p, ci, merge_out, stream);
     case 512: return launch_fan_cap<512>(p, ci, merge_out, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+// A decode (or any split-KV launch of at least two chunks): every (chunk,
+// 16-row unit, KV head) item as one fanned workgroup, each writing its chunk
+// partial for the combine kernels.
+hipError_t launch_fan_kv(const Params &p, hipStream_t stream)
+{
+    if (p.nch < 2 || !p.ws_o)
+        return hipErrorInvalidValue;
+    switch (p.dk) {
+    case 128: return launch_fan_cap<128>(p, -1, false, stream);
+    case 256: return launch_fan_cap<256>(p, -1, false, stream);
+    case 512: return launch_fan_cap<512>(p, -1, false, stream);
     default: return hipErrorInvalidValue;
     }
 }

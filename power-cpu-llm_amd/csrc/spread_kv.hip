@@ -25,11 +25,13 @@
 // workspace that holds nothing else (zero when allocated; epochs are never
 // zero), so a stale word carries an earlier epoch.
 //
-// The wait is bounded: after max_polls reads a wave gives up, sets kErrWait
-// in the error flag and finishes (its results are then not valid and the
-// host reports the failure), so every wave exits. The host picks this kernel
-// only for launches whose workgroups all fit on the chip at once, and a wave
-// waits only for the workgroups of its own item, adjacent in dispatch order.
+// The wait is bounded: after max_polls reads a wave stops waiting and forms
+// every score block whose words have not arrived itself, by the same chain
+// from K and Q (the same bits), so every wave exits with a valid result even
+// when some workgroups of its item never ran alongside it. The host picks
+// this kernel only for launches whose workgroups all fit on the chip at
+// once, and a wave waits only for the workgroups of its own item, adjacent
+// in dispatch order, so the fallback is for a GPU shared with other work.
 //
 // Output: for a launch of a single chunk, the output itself. Otherwise each
 // workgroup publishes its chunk partial (m, l, O) as (epoch, bits) words,
@@ -103,6 +105,44 @@ __device__ __forceinline__ void spread_merge(const Params &p, int64_t e)
     stg4(o + d, v);
     if (nonfinite)
         atomicOr(p.err, kErrOutput);
+}
+
+// The canonical score chain of the 16-key block at key0 for the rows of the
+// lane's unit (lane (col, g): row `row`, keys key0 + 4g + r in the result),
+// loaded and formed on its own: the operands and the order of the kernel's
+// own chains, for a block whose published words did not arrive.
+template <int DK, bool FULL>
+__device__ __forceinline__ f4 spread_block_scores(const Params &p, int64_t key0, int kh, int row,
+                                               bool rin, int col, int g)
+{
+    constexpr int NU = DK / 32;
+    const int64_t klast = p.nkeys - 1;
+    const int64_t key = key0 + col;
+    const float *kp = key_row(p, key < klast ? key : klast) + (int64_t)kh * p.dim;
+    const int query = rin ? row / p.group : 0;
+    const int h = kh * p.group + (rin ? row % p.group : 0);
+    const float *qp = p.q + (int64_t)query * p.q_stride + (int64_t)h * p.dim;
+    f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+    for (int u = 0; u < NU; ++u) {
+        float q[8], k[8];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const int d = 32 * u + 8 * g + 4 * hh;
+            const bool din = FULL || d < p.dim;
+            const f4 x = ldg4(qp + (din ? d : 0)) * p.q_scale;
+            const f4 y = ldg4(kp + (din ? d : 0));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                q[4 * hh + j] = (rin && din) ? x[j] : 0.f;
+                k[4 * hh + j] = din ? y[j] : 0.f;
+            }
+        }
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+            acc = mfma(k[jj], q[jj], acc);
+    }
+    return acc;
 }
 
 template <int DK, bool FULL, bool CAP, bool EARLY, int WV>
@@ -285,10 +325,14 @@ __global__ __launch_bounds__(64 * WV, 2) void spread_kv_kernel(Params p)
 
     // The chunk's raw scores once every word carries this launch's epoch
     // (bounded): each wave takes its share of the blocks and leaves them in
-    // LDS.
+    // LDS. A block whose words have not all arrived when the wait runs out
+    // (a workgroup of the item that is not running: a GPU shared with other
+    // work, or too few CUs) is formed here by the same score chain from K and
+    // Q, so the launch completes with the same bits either way.
     {
         constexpr int HB = kBlocksPerChunk / WV;
         uint64_t x[HB][4];
+        bool gave_up = false;
         for (int polls = 0;;) {
             // an opaque base each pass: the loads' addresses are formed here
             // from it (otherwise the compiler keeps them all live across the
@@ -306,11 +350,26 @@ __global__ __launch_bounds__(64 * WV, 2) void spread_kv_kernel(Params p)
             if (__all(fresh))
                 break;
             if (++polls >= p.max_polls) {
-                if (lane == 0)
-                    atomicOr(p.err, kErrWait);
+                gave_up = true;
                 break;
             }
             __builtin_amdgcn_s_sleep(2);
+        }
+        if (gave_up) {
+#pragma unroll
+            for (int b = 0; b < HB; ++b) {
+                bool got = true;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    got &= (uint32_t)(x[b][r] >> 32) == p.epoch;
+                if (__all(got))
+                    continue;
+                const f4 acc = spread_block_scores<DK, FULL>(p, cbase + 16 * (w * HB + b),
+                                                             kh, row, rin, col, g);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    x[b][r] = (uint64_t)__float_as_uint(acc[r]);
+            }
         }
 #pragma unroll
         for (int b = 0; b < HB; ++b)

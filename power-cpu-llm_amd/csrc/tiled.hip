@@ -317,6 +317,12 @@ void tiled_kernel(Params p, int split, int z0)
                 if (!first1 && 64 * a + 16 * g + 4 * i < p.dim)
                     s1v[a][i] = a < NL ? lacc(a, i) : ldg4(a1 + acc_pos(a, i));
             }
+        // Write-after-read across lanes: lane (g, i)'s slot 64a + 16i + 4g is
+        // where the lane with g' = i stores dims 64a + 16g' + 4i' below, so
+        // every load above must complete before the first store. The wait
+        // (and its memory clobber, which keeps the compiler from sinking a
+        // load past a store it cannot prove disjoint) orders them.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         bool nonfinite = false;
 #pragma unroll
         for (int a = 0; a < NQ; ++a)

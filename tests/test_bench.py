@@ -35,6 +35,13 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     ("output_decode", 23_068_672, 46_176_256, None),
     # the whole decode layer: the 32K attention plus that output block
     ("decode_32k_layer", 536_870_912 + 23_068_672, 536_903_680 + 46_176_256, None),
+    # the global-layer decode at 32K keys: 2 x 32768 x 2 x 512 x 4 + 2 x 16 x 512 x 4
+    ("decode_32k_d512", None, 268_500_992, None),
+    # the reference's probe shapes (int8/tests.rs:770-809), 8 queries over
+    # every key: K + V = 2 x 1279 x 8 x 256 x 4, Q + O = 2 x 8 x 16 x 256 x 4
+    ("probe_sliding_q8", 4 * 256 * 8 * 1279 * 16, 20_955_136 + 262_144, 8 * 1279),
+    # K + V = 2 x 3194 x 2 x 512 x 4, Q + O = 2 x 8 x 16 x 512 x 4
+    ("probe_global_q8", 4 * 512 * 8 * 3194 * 16, 26_165_248 + 524_288, 8 * 3194),
 ])
 def test_algorithmic_work_matches_the_configs(name, flops, bytes_, pairs):
     f, b, p = bench.work(name)
@@ -60,3 +67,17 @@ def test_more_than_one_gpu_is_refused():
     assert res.returncode == 2
     assert res.stdout == ""
     assert "single MI355X" in res.stderr
+
+
+def test_probe_rate_is_the_references_gmacs():
+    # int8/tests.rs:800-806: macs = 2 nq qheads nkeys dim per call
+    assert bench.reference_gmacs("probe_sliding_q8", 1.0) * 1e9 == 2 * 8 * 16 * 1279 * 256
+    assert bench.reference_gmacs("probe_global_q8", 0.5) * 1e9 == 4 * 8 * 16 * 3194 * 512
+
+
+def test_every_baseline_config_has_a_cpu_leg():
+    for name in ("decode_2k", "decode_32k_window1024", "decode_32k", "decode_128k_d512",
+                 "prefill_4k_window1024", "prefill_4k", "canvas_256x2304"):
+        assert name in bench.CPU_LEGS
+        if bench.WORKLOADS[name][8] != "decode":
+            assert name in bench.ROW_SAMPLE

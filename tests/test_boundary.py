@@ -99,8 +99,10 @@ def test_descriptor_validation_on_the_host(pcl):
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_SPREAD_KV
     d.kernel = pcl.KERNEL_PIPE_KV  # forced choices are kept where the kernel exists
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
-    d.kernel = pcl.KERNEL_TWO_PASS
-    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_TWO_PASS
+    d.kernel = pcl.KERNEL_FAN_KV
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_FAN_KV
+    d.kernel = 5  # retired
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == -1
     d.kernel = pcl.KERNEL_PIPE_KV
     d.dim, d.q_stride, d.o_stride = 512, 16 * 512, 16 * 512
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
@@ -112,7 +114,7 @@ def test_descriptor_validation_on_the_host(pcl):
     d.window = 1024
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_SPREAD_KV
     d.dim, d.q_stride, d.o_stride = 512, 16 * 512, 16 * 512
-    d.kernel = 7  # no such kernel
+    d.kernel = 8  # no such kernel
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == -1
     d.kernel, d.dim, d.q_stride, d.o_stride = 0, 256, 16 * 256, 16 * 256
     d.dim = 24

@@ -155,11 +155,11 @@ def test_concurrent_head_range_calls_share_one_upload_and_see_rewrites(kernels, 
     pool.shutdown()
 
 
-def test_host_entry_reruns_a_spread_launch_whose_waits_ran_out(pcl, kernels):
-    # the engine-facing entry's context with a one-poll wait bound: its 2K
-    # decode (the spread kernel) gives up waiting, and the entry reruns it
-    # with the pipelined kernel, which never waits: the same bits as at the
-    # default bound
+def test_host_entry_keeps_the_bits_when_spread_waits_run_out(pcl, kernels):
+    # the engine-facing entry's context with a one-poll wait bound: the
+    # waves of its 2K decode (the spread kernel) stop waiting for each other
+    # and form the missing scores themselves: the same bits as at the default
+    # bound
     qheads, kvh, dim, nkeys = 16, 8, 256, 2048
     g = np.random.default_rng(0x3A17)
     q = prescale(g.standard_normal(qheads * dim, dtype=np.float32), dim)
@@ -307,7 +307,7 @@ def test_a_context_per_thread_gives_the_single_context_bits(pcl, torch, ctx):
 
     ctx.launch(desc(ctx, outs[workers], pcl.KERNEL_SPLIT_KV))
     assert ctx.sync() == 0
-    kernels = (pcl.KERNEL_PIPE_KV, pcl.KERNEL_SPLIT_KV, pcl.KERNEL_TWO_PASS)
+    kernels = (pcl.KERNEL_PIPE_KV, pcl.KERNEL_SPLIT_KV, pcl.KERNEL_FAN_KV)
 
     def worker(i):
         c = pcl.Context(0)
@@ -360,8 +360,10 @@ def test_raw_entries_report_bad_geometry(pcl):
 # ---- device descriptors: every kernel gives the same bits ------------------
 
 def run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel, causal=0, window=0, first_key=0,
-             first_query=0, mask=None, split_at=None, kv=None, q_scale=1.0, softcap=None):
-    """One device launch over numpy inputs; returns (out, error flag)."""
+             first_query=0, mask=None, split_at=None, kv=None, q_scale=1.0, softcap=None,
+             noalloc=False):
+    """One device launch over numpy inputs (through the allocation-free
+    entry with noalloc); returns (out, error flag)."""
     dev = torch.device("cuda:0")
     nq = q.shape[0]
     nkeys = k.shape[0]
@@ -393,7 +395,10 @@ def run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel, causal=0, window=0, 
         kw.update(mask=tm.data_ptr(), mask_stride=nkeys)
         keep.append(tm)
     d = ctx.desc(**kw)
-    ctx.launch(d)
+    if noalloc:
+        ctx.launch_noalloc(d)
+    else:
+        ctx.launch(d)
     err = ctx.sync()
     return out.cpu().numpy(), err
 
@@ -445,11 +450,11 @@ def test_every_kernel_gives_identical_bits(torch, ctx, oracle, case):
     k = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
     v = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
     outs = {}
-    for kernel in (1, 2, 3, 4, 5, 6):
+    for kernel in (1, 2, 3, 4, 6, 7):
         outs[kernel], err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel, causal,
                                      window, 0, fq)
         assert err == 0
-    for kernel in (2, 3, 4, 5, 6):
+    for kernel in (2, 3, 4, 6, 7):
         assert np.array_equal(bits(outs[1]), bits(outs[kernel])), kernel
     for i in sorted({0, nq // 2, nq - 1}):
         m = oracle.encoder_mask(0, nkeys, fq + i, window or None) if causal else None
@@ -481,11 +486,11 @@ def test_softcap_every_kernel_identical_and_matches_the_oracle(torch, ctx, oracl
     k = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
     v = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
     outs = {}
-    for kernel in (0, 1, 2, 3, 4, 5, 6):
+    for kernel in (0, 1, 2, 3, 4, 6, 7):
         outs[kernel], err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel, causal,
                                      window, 0, fq, softcap=cap)
         assert err == 0
-    for kernel in (1, 2, 3, 4, 5, 6):
+    for kernel in (1, 2, 3, 4, 6, 7):
         assert np.array_equal(bits(outs[0]), bits(outs[kernel])), kernel
     plain, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, 0, causal, window, 0, fq)
     assert err == 0 and np.max(np.abs(plain - outs[0])) > 1e-3
@@ -518,36 +523,68 @@ def test_softcap_off_is_bitwise_inert(torch, ctx):
             assert err == 0 and np.max(np.abs(huge - base)) < 1e-6, kernel
 
 
-def test_spread_waits_give_up_at_the_host_limit_then_recover(pcl, torch, ctx):
-    # a limit of one poll on the waits between workgroups of the spread decode
-    # (its score exchange and the merge of its chunk partials): the waits run
-    # out while the items still run, which sets bit 4 of the error flag and
-    # every workgroup finishes (no hang); back at the default limit the same
-    # context reproduces the bits of another context
-    qheads, kvh, dim, nkeys = 16, 8, 256, 2048
+def test_spread_waits_give_up_at_the_host_limit_and_keep_the_bits(pcl, torch, ctx, oracle):
+    # a limit of one poll on the spread decode's waits for the other
+    # workgroups' scores: the waits run out while the items still run, and
+    # each wave then forms the missing score blocks itself by the same chain,
+    # so the device entry returns the pipelined kernel's bits with no error
+    # bit (one chunk: the output straight from the item workgroups; several:
+    # through the launch's merge workgroups); back at the default limit the
+    # same context reproduces them too
+    qheads, kvh, dim = 16, 8, 256
     g = np.random.default_rng(77)
+    for nkeys in (2048, 1024, 256, 200):
+        q = prescale(g.standard_normal((1, qheads * dim), dtype=np.float32), dim)
+        k = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+        v = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+        want, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, pcl.KERNEL_PIPE_KV, 1, 0, 0,
+                             nkeys - 1)
+        assert err == 0
+        other = pcl.Context(0, torch.cuda.current_stream().cuda_stream)
+        try:
+            with pytest.raises(pcl.AttentionError) as e:
+                other.set_wait_limit(-1)
+            assert e.value.kind == "InvalidParameter"
+            other.set_wait_limit(1)
+            for _ in range(2):
+                got, err = run_desc(torch, other, q, k, v, qheads, kvh, dim,
+                                    pcl.KERNEL_SPREAD_KV, 1, 0, 0, nkeys - 1)
+                assert err == 0, (nkeys, err)
+                assert np.array_equal(bits(got), bits(want)), nkeys
+            other.set_wait_limit(0)
+            got, err = run_desc(torch, other, q, k, v, qheads, kvh, dim, pcl.KERNEL_SPREAD_KV, 1,
+                                0, 0, nkeys - 1)
+            assert err == 0
+            assert np.array_equal(bits(got), bits(want))
+        finally:
+            other.close()
+        ok, ref = oracle.heads(q[0], k, v, qheads, kvh, dim, nkeys,
+                               oracle.encoder_mask(0, nkeys, nkeys - 1, None))
+        assert ok
+        assert_parity(want[0], ref, dim)
+
+
+def test_spread_epochs_across_a_counter_wrap(pcl, torch, ctx):
+    # the device's epoch counter set just below a wrap of its low 32 bits:
+    # the launches before and after the wrap (when the workspace's published
+    # words are zeroed again) keep the pipelined kernel's bits, through a
+    # context's workspace and through the allocation-free scratch
+    lib = pcl.load()
+    qheads, kvh, dim, nkeys = 16, 8, 256, 2048
+    g = np.random.default_rng(0xE90C)
     q = prescale(g.standard_normal((1, qheads * dim), dtype=np.float32), dim)
     k = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
     v = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
-    want, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, pcl.KERNEL_SPREAD_KV, 1, 0, 0,
+    want, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, pcl.KERNEL_PIPE_KV, 1, 0, 0,
                          nkeys - 1)
     assert err == 0
-    other = pcl.Context(0, torch.cuda.current_stream().cuda_stream)
-    try:
-        with pytest.raises(pcl.AttentionError) as e:
-            other.set_wait_limit(-1)
-        assert e.value.kind == "InvalidParameter"
-        other.set_wait_limit(1)
-        _, err = run_desc(torch, other, q, k, v, qheads, kvh, dim, pcl.KERNEL_SPREAD_KV, 1, 0, 0,
-                          nkeys - 1)
-        assert err & 16, err
-        other.set_wait_limit(0)
-        got, err = run_desc(torch, other, q, k, v, qheads, kvh, dim, pcl.KERNEL_SPREAD_KV, 1, 0,
-                            0, nkeys - 1)
-        assert err == 0
-        assert np.array_equal(bits(got), bits(want))
-    finally:
-        other.close()
+    for noalloc in (False, True):
+        assert lib.pcl_debug_set_epoch_counter(0, (5 << 32) | 0xFFFFFFFD) == 0
+        for i in range(6):
+            got, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, pcl.KERNEL_SPREAD_KV, 1,
+                                0, 0, nkeys - 1, noalloc=noalloc)
+            assert err == 0, (noalloc, i)
+            assert np.array_equal(bits(got), bits(want)), (noalloc, i)
 
 
 SPREAD_FORM_CASES = [
@@ -599,14 +636,14 @@ def test_split_launch_tail_with_masks_segments_and_kv_ranges(torch, ctx, oracle)
     mask = g.random((nq, nkeys)) < 0.7
     mask[:, -1] = True
     outs = {}
-    for kernel in (1, 2, 3, 4, 5, 6):
+    for kernel in (1, 2, 3, 4, 6, 7):
         for kv in [(0, kvh), (2, 7)]:
             out, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel, mask=mask,
                                 split_at=nkeys - nq, kv=kv)
             assert err == 0
             outs[(kernel, kv)] = out
     for kv in [(0, kvh), (2, 7)]:
-        for kernel in (2, 3, 4, 5, 6):
+        for kernel in (2, 3, 4, 6, 7):
             assert np.array_equal(bits(outs[(1, kv)]), bits(outs[(kernel, kv)])), (kernel, kv)
     group = qheads // kvh
     for i in (0, nq - 1):
@@ -628,7 +665,7 @@ def test_explicit_masks_segments_scale_and_kv_ranges_keep_bits(torch, ctx):
     scale = np.float32(1.0 / 16.0)
     base, err = run_desc(torch, ctx, prescale(q, dim), k, v, qheads, kvh, dim, 1, 1, 300, 0, fq)
     assert err == 0
-    for kernel in (1, 2, 3, 4, 5, 6):
+    for kernel in (1, 2, 3, 4, 6, 7):
         # explicit byte masks equal the descriptor's causal window
         got, err = run_desc(torch, ctx, prescale(q, dim), k, v, qheads, kvh, dim, kernel,
                             mask=mask)
@@ -659,7 +696,7 @@ def test_long_launch_combines_agree_across_kernels(torch, ctx, oracle):
     k = gpu_normals(torch, 0x5EED0778, (nkeys, kvh, dim))
     v = gpu_normals(torch, 0x5EED0779, (nkeys, kvh, dim))
     outs = {}
-    for kernel in (1, 2, 3, 4, 5, 6):
+    for kernel in (1, 2, 3, 4, 6, 7):
         out = torch.full((nq, qheads, dim), float("nan"), device="cuda:0")
         d = ctx.desc(q=q.data_ptr(), q_stride=qheads * dim, nq=nq, k0=k.data_ptr(),
                      v0=v.data_ptr(), n0=nkeys, qheads=qheads, kvheads=kvh, dim=dim, kh_first=0,
@@ -669,7 +706,7 @@ def test_long_launch_combines_agree_across_kernels(torch, ctx, oracle):
         ctx.launch(d)
         assert ctx.sync() == 0
         outs[kernel] = out.cpu().numpy()
-    for kernel in (2, 3, 4, 5, 6):
+    for kernel in (2, 3, 4, 6, 7):
         assert np.array_equal(bits(outs[1]), bits(outs[kernel])), kernel
     qn, kn, vn = (x.cpu().numpy().reshape(-1) for x in (q, k, v))
     for i in (0, nq - 1):
@@ -707,7 +744,7 @@ def test_device_error_flags(torch, ctx):
     bad_k[10, 1, 5] = np.nan
     bad_v = v.copy()
     bad_v[20, 0, 3] = np.inf
-    for kernel in (1, 2, 3, 4, 5, 6):
+    for kernel in (1, 2, 3, 4, 6, 7):
         _, err = run_desc(torch, ctx, q, bad_k, v, qheads, kvh, dim, kernel)
         assert err & 1
         _, err = run_desc(torch, ctx, q, k, bad_v, qheads, kvh, dim, kernel)
@@ -716,12 +753,14 @@ def test_device_error_flags(torch, ctx):
         assert err == 0
 
 
-@pytest.mark.parametrize("dim", [48, 80, 144, 208])
+@pytest.mark.parametrize("dim", [48, 80, 144, 208, 320, 400])
 def test_padded_head_dims_read_only_the_callers_rows(torch, ctx, oracle, dim):
-    """Head dims below the kernels' padded size (64, 128, 256): K and V end
-    where a NaN-filled tail of their allocation begins, so any read past the
-    last key row's last head would turn a score or an output non-finite.
-    Every kernel stays finite, error-free and bitwise equal."""
+    """Head dims below the kernels' padded size (64, 128, 256, 512): K and V
+    end where a NaN-filled tail of their allocation begins, so any read past
+    the last key row's last head would turn a score or an output non-finite.
+    Every kernel stays finite, error-free and bitwise equal (at 320 and 400
+    the head-dim-512 forms: the wave-pair tiled kernel and its fanned last
+    round, the four-phase, pipelined and fanned decodes)."""
     qheads, kvh, nq, nkeys = 8, 2, 160, 300
     g = np.random.default_rng(dim)
     q = prescale(g.standard_normal((nq, qheads * dim), dtype=np.float32), dim)
@@ -734,7 +773,7 @@ def test_padded_head_dims_read_only_the_callers_rows(torch, ctx, oracle, dim):
     vbuf[:n] = torch.from_numpy(v.reshape(-1)).to("cuda:0")
     tq = torch.from_numpy(q).to("cuda:0")
     outs = {}
-    for kernel in (2, 3, 1, 4, 5, 6):
+    for kernel in (2, 3, 1, 4, 6, 7):
         out = torch.full((nq, qheads * dim), float("nan"), device="cuda:0")
         d = ctx.desc(q=tq.data_ptr(), q_stride=qheads * dim, nq=nq, k0=kbuf.data_ptr(),
                      v0=vbuf.data_ptr(), n0=nkeys, qheads=qheads, kvheads=kvh, dim=dim,
@@ -746,7 +785,7 @@ def test_padded_head_dims_read_only_the_callers_rows(torch, ctx, oracle, dim):
         assert ctx.sync() == 0, kernel
         outs[kernel] = out.cpu().numpy()
         assert np.all(np.isfinite(outs[kernel])), kernel
-    for kernel in (3, 1, 4, 5, 6):
+    for kernel in (3, 1, 4, 6, 7):
         assert np.array_equal(bits(outs[2]), bits(outs[kernel])), kernel
     for i in (0, nq - 1):
         m = oracle.encoder_mask(0, nkeys, nkeys - nq + i, None)
@@ -771,7 +810,7 @@ def decode_config(torch, ctx, oracle, qheads, kvh, dim, nkeys, window, seed, uni
         k = k / k.norm(dim=-1, keepdim=True)
     outs = {}
     # the automatic choice, then every split-KV kernel: all bitwise equal
-    for kernel in (0, 1, 4, 5, 6):
+    for kernel in (0, 1, 4, 6, 7):
         out = torch.full((1, qheads, dim), float("nan"), device="cuda:0")
         d = ctx.desc(q=q.data_ptr(), q_stride=qheads * dim, nq=1, k0=k.data_ptr(),
                      v0=v.data_ptr(), n0=nkeys, qheads=qheads, kvheads=kvh, dim=dim, kh_first=0,
