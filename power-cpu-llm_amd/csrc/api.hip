@@ -37,15 +37,32 @@ constexpr int64_t kMaxKeys = (int64_t)1 << 30;
 constexpr int64_t kMaxRowsTimesKvHeads = (int64_t)1 << 22;
 constexpr int kTiledMaxDk = 512;
 constexpr int kPipeMaxDk = 512;
-// Decode launches take the pipelined kernel, except at head dims above 256
-// with fewer than this many (chunk, unit, KV head) items: there each
-// pipelined wave needs 32 round trips per chunk (8 KiB pieces), while the
-// four-phase kernel spreads a chunk over DK/64 waves. Measured on MI355X
-// (2 KV heads, d512): four-phase 13-30 % faster from 2K to 32K keys (16-256
-// items), pipelined 24-27 % faster at 64K and 128K (512 and 1024 items).
-// Up to head dim 256 the pipelined kernel was as fast or faster at every
-// size tried (16 to 1024 items, d64/128/256).
-constexpr int64_t kPipeMinItemsWide = 512;
+// Launches of few (chunk, 16-row unit, KV head) items, each latency-bound
+// in one workgroup, take the fanned kernel (each item over eight waves),
+// where it was measured faster on MI355X (A/B of every kernel per shape,
+// inputs larger than the last-level cache): at head dim 512 below 512
+// items (2K-32K-key decodes of 2 KV heads: 34-58 us against 48-61 us for
+// the four-phase and 59-67 us for the pipelined kernel; 8 queries over
+// 1279 keys 34 against 97 us chunk-split tiled; at 512 items, a 64K decode,
+// the pipelined kernel is 9 % faster); at head dim 256 up to 128 items
+// (4K-key decode 28 against 33 us pipelined; at 256 items pipelined is
+// 11 % faster), or up to 512 items of at least two units (8-32 queries over
+// 3194 keys: 27-46 against 36-55 us). Head dim 128 never (pipelined 8 %
+// faster at 256 items).
+constexpr int64_t kFanMaxItems512 = 512;
+constexpr int64_t kFanMaxItems256 = 128;
+constexpr int64_t kFanMaxItems256Units = 512;
+
+bool fan_preferred(int dk, int64_t units, int64_t items, int64_t nch)
+{
+    if (nch < 2)
+        return false;
+    if (dk == 512)
+        return items < kFanMaxItems512;
+    if (dk == 256)
+        return items <= kFanMaxItems256 || (units >= 2 && items <= kFanMaxItems256Units);
+    return false;
+}
 // The spread decode's slices (dk/32 per item; a two-wave workgroup with 48
 // KiB of LDS each, three per CU, or two per four-wave workgroup when they
 // take at most two per CU) all fit on the chip at once up to this many per
@@ -172,14 +189,18 @@ int choose_kernel(int requested, int dk, int64_t nrows, int64_t nkv, int64_t nch
         return dk <= kPipeMaxDk ? requested : PCL_KERNEL_SPLIT_KV;
     if (requested == PCL_KERNEL_FAN_KV)
         return dk >= 128 && nch >= 2 ? requested : PCL_KERNEL_PIPE_KV;
+    const int64_t units = (nrows + pcl::kRows - 1) / pcl::kRows;
+    const bool fan = fan_preferred(dk, units, nch * nkv * units, nch);
     if (dk > kTiledMaxDk || nrows < 64) {
-        // decode: short launches spread each chunk over several workgroups;
-        // otherwise the pipelined kernel; at head dim 512 short launches (few
-        // workgroups, so latency-bound) take the four-phase kernel
+        // decode: short launches spread each chunk over several workgroups,
+        // or fan each item over a workgroup's eight waves; otherwise the
+        // pipelined kernel; a single chunk at head dim 512 the four-phase
+        // kernel
         if (spread_fits)
             return PCL_KERNEL_SPREAD_KV;
-        const int64_t units = (nrows + pcl::kRows - 1) / pcl::kRows;
-        if (dk > 256 && nch * nkv * units < kPipeMinItemsWide)
+        if (fan)
+            return PCL_KERNEL_FAN_KV;
+        if (dk > 256 && nch == 1)
             return PCL_KERNEL_SPLIT_KV;
         return PCL_KERNEL_PIPE_KV;
     }
@@ -187,7 +208,9 @@ int choose_kernel(int requested, int dk, int64_t nrows, int64_t nkv, int64_t nch
     const int64_t blocks = (nrows + rows - 1) / rows * nkv;
     if (blocks >= 128 || nch <= 1)
         return PCL_KERNEL_TILED;
-    return PCL_KERNEL_TILED_SPLIT;
+    // a chunk-split launch of few row blocks: fanned items where they are
+    // few enough
+    return fan ? PCL_KERNEL_FAN_KV : PCL_KERNEL_TILED_SPLIT;
 }
 
 // Validate a descriptor and build the plan. h_lo/h_hi/h_base select and place

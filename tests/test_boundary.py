@@ -91,8 +91,11 @@ def test_descriptor_validation_on_the_host(pcl):
     d.dim, d.q_stride, d.o_stride = 512, 16 * 512, 16 * 512
     # also at head dim 512 (two score waves, two value waves)
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
-    d.window = 1024  # five chunks per head: short, so at d512 the four-phase kernel
+    d.window = 1024  # five chunks per head: short, so at d512 the fanned kernel
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_FAN_KV
+    d.window = 200  # one chunk at d512: the four-phase kernel
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_SPLIT_KV
+    d.window = 1024
     d.dim, d.q_stride, d.o_stride = 256, 16 * 256, 16 * 256
     # up to head dim 256 a short decode (4 chunks x 8 KV heads) spreads each
     # chunk over 8 workgroups
@@ -128,6 +131,22 @@ def test_descriptor_validation_on_the_host(pcl):
         d.softcap = cap
         assert (lib.pcl_attention_resolve_kernel(ctypes.byref(d)) != -1) == valid, cap
     d.softcap = 0.0
+    # the reference's probe shapes (8 queries over every key): the global
+    # layer (16/2/512, 3194 keys) fanned, the sliding one (16/8/256, 1279
+    # keys) spread; 32 queries at head dim 256 (two row blocks' worth of
+    # rows, 416 items) fanned, over 8192 keys (1024 items) chunk-split tiled
+    d.causal, d.window, d.first_query = 0, 0, 0
+    d.nq, d.n0, d.kvheads, d.kh_end = 8, 3194, 2, 2
+    d.dim, d.q_stride, d.o_stride = 512, 16 * 512, 16 * 512
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_FAN_KV
+    d.nq, d.n0, d.kvheads, d.kh_end = 8, 1279, 8, 8
+    d.dim, d.q_stride, d.o_stride = 256, 16 * 256, 16 * 256
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_SPREAD_KV
+    d.nq, d.n0 = 32, 3194
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_FAN_KV
+    d.n0 = 8192
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_TILED_SPLIT
+    d.causal = 1
     d.dim, d.nq, d.first_query, d.window, d.n0 = 256, 4096, 0, 0, 4096
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_TILED
     d.first_key = 5000  # no query sees a key

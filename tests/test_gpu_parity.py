@@ -846,6 +846,42 @@ def test_config3_global_decode_131072_d512(torch, ctx, oracle):
     decode_config(torch, ctx, oracle, 16, 2, 512, 131072, 0, 0x5EED0003, unit_k=True)
 
 
+@pytest.mark.parametrize("nkeys", [2048, 8192, 32768])
+def test_global_layer_decode_below_128k_d512(torch, ctx, oracle, nkeys):
+    # config 3's geometry (16/2/512, unit-norm K) at the cache lengths of a
+    # conversation before 128K: AUTO fans each chunk item over a workgroup
+    decode_config(torch, ctx, oracle, 16, 2, 512, nkeys, 0, 0x5EED0030 + nkeys, unit_k=True)
+
+
+@pytest.mark.parametrize("label,qheads,kvh,dim,nkeys", [
+    ("sliding", 16, 8, 256, 1279), ("global", 16, 2, 512, 3194)])
+def test_reference_probe_shapes(pcl, torch, ctx, kernels, oracle, label, qheads, kvh, dim,
+                                nkeys):
+    # the reference's attention throughput probe (int8/tests.rs:770-809): 8
+    # queries (Rng(7) units x 0.1), keys and values (Rng units), every key
+    # allowed, through AttentionMulti (attention_multi over host arrays) and
+    # through the device entry with every kernel: all bitwise equal, each
+    # query within 1e-4 of the exact oracle with the same argmax per head
+    nq = 8
+    rng = Rng(7)
+    queries = [rng.units_c(qheads * dim, 0.1) for _ in range(nq)]
+    keys = rng.units_c(nkeys * kvh * dim)
+    values = rng.units_c(nkeys * kvh * dim)
+    got = kernels.attention_multi(queries, keys, values, kvh, dim, None)
+    q = np.stack(queries)
+    k = keys.reshape(nkeys, kvh, dim)
+    v = values.reshape(nkeys, kvh, dim)
+    for kernel in (0, 1, 2, 3, 4, 6, 7):
+        out, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, kernel)
+        assert err == 0, kernel
+        for i in range(nq):
+            assert np.array_equal(bits(out[i]), bits(got[i])), (kernel, i)
+    for i in range(nq):
+        ok, want = oracle.heads(queries[i], keys, values, qheads, kvh, dim, nkeys, None)
+        assert ok
+        assert_parity(got[i], want, dim)
+
+
 @pytest.mark.parametrize("window", [1024, 0], ids=["window1024", "global"])
 def test_config4_prefill_4096(torch, ctx, oracle, window):
     """Both 4K prefills (sliding window 1024 and global) compared elementwise
