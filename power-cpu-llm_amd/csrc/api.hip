@@ -187,8 +187,13 @@ int choose_kernel(int requested, int dk, int64_t nrows, int64_t nkv, int64_t nch
         return requested;
     if (requested == PCL_KERNEL_PIPE_KV)
         return dk <= kPipeMaxDk ? requested : PCL_KERNEL_SPLIT_KV;
-    if (requested == PCL_KERNEL_FAN_KV)
-        return dk >= 128 && nch >= 2 ? requested : PCL_KERNEL_PIPE_KV;
+    if (requested == PCL_KERNEL_FAN_KV) {
+        // its one-dimensional grid of 512-thread workgroups stays below 2^32
+        // work-items up to 2^22 items
+        const int64_t items = nch * nkv * ((nrows + pcl::kRows - 1) / pcl::kRows);
+        return dk >= 128 && nch >= 2 && items <= ((int64_t)1 << 22) ? requested
+                                                                    : PCL_KERNEL_PIPE_KV;
+    }
     const int64_t units = (nrows + pcl::kRows - 1) / pcl::kRows;
     const bool fan = fan_preferred(dk, units, nch * nkv * units, nch);
     if (dk > kTiledMaxDk || nrows < 64) {

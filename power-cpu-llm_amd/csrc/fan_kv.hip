@@ -139,9 +139,26 @@ __global__ __launch_bounds__(kFanThreads, 2) __attribute__((amdgpu_waves_per_eu(
 void fan_kv_kernel(Params p, int ci)
 {
     using C = FanCfg<DK>;
+    // consecutive workgroups cycle over the KV heads (each XCD's L2 then
+    // serves one head's K and V when there are eight)
+    int kvl = (int)blockIdx.x % p.nkv;
+    int unit = (int)blockIdx.x / p.nkv;
     if constexpr (!MERGE) {
-        if (ci < 0) // a decode launch: one item per (chunk, unit, KV head)
-            ci = (int)blockIdx.y;
+        if (ci < 0) {
+            // A launch of every chunk: item group gi = (chunk, KV head) has
+            // its units in workgroups congruent mod 8, which the dispatcher
+            // deals to one XCD, so they share the chunk's K and V in its L2:
+            // workgroup b runs unit (b / 8) % units of group
+            // ((b / 8) / units) * 8 + b % 8.
+            const int b = (int)blockIdx.x;
+            const int k = b >> 3;
+            const int gi = (k / p.units) * 8 + (b & 7);
+            if (gi >= p.nkv * p.nch)
+                return; // padding to whole groups of eight
+            unit = k % p.units;
+            kvl = gi % p.nkv;
+            ci = gi / p.nkv;
+        }
     }
     constexpr int VD = C::VD, VW = C::VW, KU = C::KU, KPN = C::KPN, KB = C::KB;
     constexpr int VB = C::VB, VB0 = C::VB0, NK = C::NK;
@@ -156,10 +173,6 @@ void fan_kv_kernel(Params p, int ci)
     float *mlst = tany + kTilesPerChunk;        // [row] (m, l)
 
     const int c = p.c_lo + ci;
-    // consecutive workgroups cycle over the KV heads (each XCD's L2 then
-    // serves one head's K and V when there are eight)
-    const int kvl = (int)blockIdx.x % p.nkv;
-    const int unit = (int)blockIdx.x / p.nkv;
     const int tid = threadIdx.x;
     const int w = tid >> 6;
     const int lane = tid & 63;
@@ -591,7 +604,10 @@ static hipError_t launch_fan_dk(const Params &p, int ci, hipStream_t stream)
     const hipError_t e = configure_fan<DK, FULL, CAP, MERGE>();
     if (e != hipSuccess)
         return e;
-    const dim3 grid(p.units * p.nkv, ci < 0 ? p.nch : 1);
+    // every chunk: (chunk, KV head) groups padded to a multiple of eight,
+    // each group's units on one XCD (see the kernel)
+    const int groups8 = (p.nkv * p.nch + 7) / 8 * 8;
+    const dim3 grid(ci < 0 ? groups8 * p.units : p.units * p.nkv);
     fan_kv_kernel<DK, FULL, CAP, MERGE><<<grid, kFanThreads, FanCfg<DK>::bytes, stream>>>(p, ci);
     return hipGetLastError();
 }
