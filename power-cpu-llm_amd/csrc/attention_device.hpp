@@ -454,15 +454,27 @@ constexpr int kMergeBatch = 8;
 
 typedef __attribute__((address_space(1))) uint64_t *gu64_ptr;
 
-__device__ __forceinline__ void publish(uint64_t *p, uint32_t epoch, float v)
-{
-    const uint64_t word = ((uint64_t)epoch << 32) | (uint64_t)__float_as_uint(v);
-    __hip_atomic_store((gu64_ptr)p, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 __device__ __forceinline__ uint64_t take(const uint64_t *p)
 {
     return __hip_atomic_load((gu64_ptr)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Words of a launch whose writing and reading workgroups share one XCD (the
+// spread decode's local form) are stored plainly: the store lands in that
+// XCD's L2, where the readers' device-coherent loads (take) find it, and
+// goes no further. Measured on MI355X (a workgroup writing one word, others
+// polling it): a device-coherent store is seen 400 ns later on the same XCD
+// and 530 ns later on another; a plain store 240 ns later on the same XCD
+// (850 ns on another: it is still seen); plain and workgroup-scope loads
+// never see another CU's store (they hit the reader's L1).
+template <bool LOCAL>
+__device__ __forceinline__ void publish_to(uint64_t *p, uint32_t epoch, float v)
+{
+    const uint64_t word = ((uint64_t)epoch << 32) | (uint64_t)__float_as_uint(v);
+    if (LOCAL)
+        __hip_atomic_store((gu64_ptr)p, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    else
+        __hip_atomic_store((gu64_ptr)p, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Published chunk partials of the spread decode: row `row` (a real row) of

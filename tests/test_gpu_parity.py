@@ -592,7 +592,9 @@ SPREAD_FORM_CASES = [
     # forms on a 256-CU MI355X: two-wave workgroups with every request up
     # front (at most one 32-dim slice per CU), four-wave workgroups of two
     # slices (two slices per CU), two-wave workgroups in the compiler's order
-    # (up to three per CU)
+    # (up to three per CU); each in the local form when the (KV head, unit)
+    # groups come in whole eights (8 KV heads here), otherwise (4 KV heads)
+    # the three-dimensional grid
     (16, 8, 256, 1, 1024, 1023),  # 32 items, 256 slices: two-wave, early
     (16, 8, 256, 1, 2048, 2047),  # 64 items, 512 slices: four-wave
     (16, 8, 256, 1, 3072, 3071),  # 96 items, 768 slices: two-wave, compiler order
@@ -600,6 +602,9 @@ SPREAD_FORM_CASES = [
     (16, 8, 128, 1, 4096, 4095),  # 128 items, 512 slices at d128: four-wave
     (16, 8, 128, 1, 2000, 1999),  # ragged last chunk at d128: two-wave, early
     (8, 4, 64, 4, 1500, 1496),    # d64, four queries of two heads per KV head
+    # the local form (each (KV head, unit) group's workgroups on one XCD)
+    # with two groups per XCD: 16 queries, two 16-row units per KV head
+    (16, 8, 128, 16, 1000, 984),
 ]
 
 
