@@ -490,6 +490,7 @@ __device__ __forceinline__ uint64_t *partial_words(const Params &p, int kvl, int
 // wave's lanes together cover their rows' chunks). Polling every word of
 // every partial instead slowed the producing workgroups' own loads. False
 // when the wait gave up.
+template <int SLEEP = 8>
 __device__ __forceinline__ bool wait_partials(const Params &p, int64_t slot0, int first,
                                               int step, int last)
 {
@@ -502,7 +503,7 @@ __device__ __forceinline__ bool wait_partials(const Params &p, int64_t slot0, in
             return true;
         if (polls >= kMergeMaxPolls)
             return false;
-        __builtin_amdgcn_s_sleep(8);
+        __builtin_amdgcn_s_sleep(SLEEP);
     }
 }
 
@@ -511,7 +512,7 @@ __device__ __forceinline__ bool wait_partials(const Params &p, int64_t slot0, in
 // with no loads) of row slot0, four dims from d, merged into s in ascending
 // order. Every word is re-checked (and the batch reloaded until all carry
 // the epoch). False when the wait gave up.
-template <int B = kMergeBatch>
+template <int B = kMergeBatch, int SLEEP = 2>
 __device__ __forceinline__ bool merge_words_batch(const Params &p, int64_t slot0, int c0,
                                                   int b0, int c1, int d, Merged4 &s)
 {
@@ -546,7 +547,7 @@ __device__ __forceinline__ bool merge_words_batch(const Params &p, int64_t slot0
             ok = false;
             break;
         }
-        __builtin_amdgcn_s_sleep(2);
+        __builtin_amdgcn_s_sleep(SLEEP);
     }
 #pragma unroll
     for (int i = 0; i < B; ++i) {

@@ -69,12 +69,13 @@ typedef const __attribute__((address_space(1))) void *spread_gptr_t;
 // and merges them exactly as the combine kernels do (per span the span's
 // kSpanChunks slots in ascending order from (-inf, 0, 0), absent chunks as
 // empty parts; then the spans in ascending order), then writes the output.
+template <bool LOCAL>
 __device__ __forceinline__ void spread_merge_row(const Params &p, int kvl, int row, int d)
 {
     const int q4 = p.dim / 4;
     const int64_t slot0 = ((int64_t)kvl * p.nrows + row) * p.nch;
     // the row's threads poll one word of each chunk partial between them
-    if (!wait_partials(p, slot0, d / 4, q4, p.nch)) {
+    if (!wait_partials<LOCAL ? 1 : 8>(p, slot0, d / 4, q4, p.nch)) {
         atomicOr(p.err, kErrWait);
         return;
     }
@@ -86,7 +87,7 @@ __device__ __forceinline__ void spread_merge_row(const Params &p, int kvl, int r
         const int c1 = min((span + 1) * kSpanChunks, p.c_lo + p.nch) - p.c_lo;
         Merged4 sm = {kNegInf, 0.f, f4{0.f, 0.f, 0.f, 0.f}};
         for (int b0 = 0; b0 < kSpanChunks; b0 += kMergeBatch)
-            ok &= merge_words_batch(p, slot0, c0, b0, c1, d, sm);
+            ok &= merge_words_batch<kMergeBatch, LOCAL ? 1 : 2>(p, slot0, c0, b0, c1, d, sm);
         merge_into4(tot, sm.M, sm.L, sm.acc);
     }
     if (!ok) {
@@ -119,7 +120,7 @@ __device__ __forceinline__ void spread_merge(const Params &p, int64_t e)
     const int64_t per_kv = (int64_t)p.nrows * q4;
     if (e >= p.nkv * per_kv)
         return;
-    spread_merge_row(p, (int)(e / per_kv), (int)(e % per_kv) / q4,
+    spread_merge_row<false>(p, (int)(e / per_kv), (int)(e % per_kv) / q4,
                             4 * (int)(e % per_kv % q4));
 }
 
@@ -132,7 +133,7 @@ __device__ __forceinline__ void spread_merge_group(const Params &p, int z, int e
     const int row = unit * kRows + e / q4;
     if (e >= kRows * q4 || row >= p.nrows)
         return;
-    spread_merge_row(p, z / p.units, row, 4 * (e % q4));
+    spread_merge_row<true>(p, z / p.units, row, 4 * (e % q4));
 }
 
 // The local form's merge workgroups per (KV head, unit) group: one thread
@@ -419,7 +420,7 @@ __global__ __launch_bounds__(64 * WV, 2) void spread_kv_kernel(Params p)
                 gave_up = true;
                 break;
             }
-            __builtin_amdgcn_s_sleep(2);
+            __builtin_amdgcn_s_sleep(LOCAL ? 1 : 2);
         }
         if (gave_up) {
 #pragma unroll
