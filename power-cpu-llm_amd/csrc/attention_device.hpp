@@ -112,6 +112,17 @@ struct Params {
     // below), which the launch's own merge workgroups combine
     uint64_t *ws_ptag;
     int *err;
+    // A one-token decode step's head transform, fused (sq null: none; q
+    // unused): the token's raw rows (Q [qheads][dim], K and V
+    // [kvheads][dim]; sv null: V is the raw K), the learned Q and K scales,
+    // the (sin, cos) pairs of its position and the norm epsilon. Its
+    // prepared K and V rows (snk, snv: [kvheads][dim]) are the launch's
+    // last key, which the workgroups of that key's chunk write before they
+    // read the chunk; the workgroups of the launch's first chunk write the
+    // prepared queries to sqo ([qheads][dim]).
+    const float *sq, *sk, *sv, *sqs, *sks, *srot;
+    float *snk, *snv, *sqo;
+    float seps;
 };
 
 // Global-memory accessors. Pointers taken from Params are generic, and a

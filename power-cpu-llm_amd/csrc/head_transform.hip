@@ -3,7 +3,9 @@
 // tokens at once on the device, with K and V optionally written straight
 // into a layer cache's rows (no staging copy).
 //
-// Per head (p9_ref_rms_norm, src/kernels/portable/reference.rs:11-33):
+// Per head (p9_ref_rms_norm, src/kernels/portable/reference.rs:11-33; the
+// arithmetic of step_prologue.hpp, which a decode kernel also runs when a
+// one-token step's transform is folded into its launch):
 //   sum = sequential f64 sum of f64(x_j)^2, j ascending;
 //   inv = 1 / sqrt(sum / dim + f64(eps))            (f64, correctly rounded);
 //   y_j = f32(f64(x_j) * inv), times scale_j in f32 for Q and K.
@@ -26,6 +28,7 @@
 #include "context.hpp"
 #include "pcl_attention.h"
 #include "rotation.hpp"
+#include "step_prologue.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -120,16 +123,8 @@ __global__ __launch_bounds__(64) void head_transform_kernel(TransformParams p)
         }
     }
     __syncthreads();
-    if (lane < count) {
-        double sum = 0.0;
-        const float *row = rows + lane * kStride;
-#pragma unroll 8
-        for (int j = 0; j < DK; ++j) {
-            const double v = (double)row[j];
-            sum = sum + v * v;
-        }
-        inv[lane] = 1.0 / __builtin_sqrt(sum / (double)DK + (double)p.eps);
-    }
+    if (lane < count)
+        inv[lane] = norm_inverse<DK>(rows + lane * kStride, p.eps);
     __syncthreads();
     for (int r = 0; r < count; ++r) {
         const int s = s0 + r;
@@ -144,21 +139,12 @@ __global__ __launch_bounds__(64) void head_transform_kernel(TransformParams p)
             const int j = lane + 64 * m;
             if (j >= kHalf)
                 continue;
-            float a = (float)((double)row[j] * iv);
-            float b = (float)((double)row[j + kHalf] * iv);
-            if (kind == 0) {
-                a = a * qa[m];
-                b = b * qb[m];
-            } else if (kind == 1) {
-                a = a * ka[m];
-                b = b * kb[m];
-            }
-            if (kind != 2) {
-                const float ac = a * sc[m].y, bs = b * sc[m].x;
-                const float bc = b * sc[m].y, as = a * sc[m].x;
-                a = ac - bs;
-                b = bc + as;
-            }
+            float a, b;
+            if (kind == 2)
+                transform_pair<false>(row[j], row[j + kHalf], iv, 0.f, 0.f, 0.f, 0.f, &a, &b);
+            else
+                transform_pair<true>(row[j], row[j + kHalf], iv, kind == 0 ? qa[m] : ka[m],
+                                     kind == 0 ? qb[m] : kb[m], sc[m].x, sc[m].y, &a, &b);
             bad |= !is_finite(a) || !is_finite(b);
             stg(out + j, a);
             stg(out + j + kHalf, b);

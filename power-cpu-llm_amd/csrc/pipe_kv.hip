@@ -94,16 +94,19 @@ template <int DK, bool WIDE> constexpr bool pipe_slice_loads()
 }
 
 // LDS hand-over between the score wave and the value waves.
-template <int DK, bool WIDE> struct PipeLds {
+// 16-byte aligned, with q and sb at 16-byte offsets: their 16-byte reads
+// and writes stay single ds_read_b128 / ds_write_b128 instructions (at
+// 4-byte alignment each one split into two ds_read2_b32).
+template <int DK, bool WIDE> struct __attribute__((aligned(16))) PipeLds {
     float p[2][8][64];    // probabilities, [slot][4b + r][lane]
     float alpha[2][kRows];
     float rs[2][kRows];
-    int any[2];
     float m[kRows];       // chunk maximum
-    float q[pipe_q_lds<DK, WIDE>() ? kRows * (DK + 4) : 1];
+    float q[pipe_q_lds<DK, WIDE>() ? kRows * (DK + 4) : 4];
     // raw scores of a tile's second 16-key block from the second score
     // wave, [tile & 1][r][lane]
     float sb[pipe_score_waves<DK, WIDE>() > 1 ? 2 : 1][4][64];
+    int any[2];
 };
 
 template <int DK, bool FULL>
