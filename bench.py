@@ -75,7 +75,8 @@ WORKLOADS = {
     "decode_32k_cache": (16, 8, 256, 1, 32768, True, 0, 32767, "cache", False),
     # the head-transform prologue over a 4K-token prompt (norms and rotation
     # of 16 Q, 8 K and 8 V heads per token), and a whole decode step from raw
-    # projections: transform fused with the cache append, then attention
+    # projections: transform, cache append and attention in one call (the
+    # transform inside the pipelined decode's launch)
     "transform_4k": (16, 8, 256, 4096, 0, True, 0, 0, "transform", False),
     "decode_32k_step": (16, 8, 256, 1, 32768, True, 0, 32767, "step", False),
     # the whole attention layer of one decode token on the device: the step
@@ -435,8 +436,10 @@ def time_cache_workload(torch, pcl, ctx, name, steps, warmup, nsets, seed, trans
                         output=False):
     """Decode steps through pcl.LayerCache: per step, append one token's K/V
     after nkeys-1 cached rows (as device rows, or with transform=True from the
-    token's raw Q/K/V projections through the head transform, fused with the
-    append), attend over the cache's rows in place (its encoder descriptor),
+    token's raw Q/K/V projections through the head transform, in one
+    pcl_kv_cache_attend_token call that folds the transform into the
+    pipelined decode's launch), attend over the cache's rows in place (its
+    encoder descriptor),
     with output=True run the output block (LAYER_HIDDEN-wide projection,
     post-norm, residual) on the attended row, and roll the step back. Each
     input set is its own cache and output weights."""
@@ -472,17 +475,20 @@ def time_cache_workload(torch, pcl, ctx, name, steps, warmup, nsets, seed, trans
     def step(i):
         host, cache = sets[i % nsets]
         if transform:
-            pending = cache.append_transformed(t, host["raw_q"].data_ptr(), host["kt"].data_ptr(),
-                                               host["vt"].data_ptr(), 1,
-                                               host["q_prepared"].data_ptr())
-            qptr = host["q_prepared"].data_ptr()
+            # the token's transform, cache append and attention in one call
+            # (the transform folded into the decode's launch where it can be)
+            pending = cache.attend_token(t, host["raw_q"].data_ptr(), host["kt"].data_ptr(),
+                                         host["vt"].data_ptr(), host["q_prepared"].data_ptr(),
+                                         host["out"].data_ptr())
+            d = cache.encoder_desc(pending, q=host["q_prepared"].data_ptr(), q_stride=qh * dim,
+                                   nq=nq, qheads=qh, kh_first=0, kh_end=kvh,
+                                   out=host["out"].data_ptr(), o_stride=qh * dim)
         else:
             pending = cache.append(host["kt"].data_ptr(), host["vt"].data_ptr(), 1)
-            qptr = host["q"].data_ptr()
-        d = cache.encoder_desc(pending, q=qptr, q_stride=qh * dim, nq=nq,
-                               qheads=qh, kh_first=0, kh_end=kvh, out=host["out"].data_ptr(),
-                               o_stride=qh * dim)
-        ctx.launch(d)
+            d = cache.encoder_desc(pending, q=host["q"].data_ptr(), q_stride=qh * dim, nq=nq,
+                                   qheads=qh, kh_first=0, kh_end=kvh,
+                                   out=host["out"].data_ptr(), o_stride=qh * dim)
+            ctx.launch(d)
         if output:
             ctx.attention_output(host["out"].data_ptr(), nq, width, host["w"].data_ptr(),
                                  LAYER_HIDDEN, host["post"].data_ptr(), 1e-6,

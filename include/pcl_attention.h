@@ -401,6 +401,26 @@ int pcl_kv_cache_append_transformed(pcl_kv_cache *cache, pcl_head_transform *tra
                                     const float *raw_q, const float *raw_k, const float *raw_v,
                                     int64_t n, float *q_out, pcl_kv_pending *pending);
 
+/* One decode token of a layer in one call: pcl_kv_cache_append_transformed
+ * for n = 1 (the token's raw rows prepared, K and V written after the
+ * retained rows, the prepared queries to q_out [qheads][dim]), then the
+ * attention of the prepared queries over the cache's rows with the step's
+ * new key (pcl_kv_cache_encoder_desc of the step, every KV head, q_scale as
+ * the descriptor's, kernel an enum pcl_kernel) into out [qheads][dim]: the
+ * one-position decode of encode_in_place (src/engine/attention.rs:949-1080,
+ * prepare 102-156 then the attention pass 755-777). Where the kernel that
+ * runs is the pipelined decode at head dim 64, 128, 256 or 512, the
+ * transform is folded into its launch: every workgroup prepares its own
+ * query rows and the workgroups of the new key's chunk write that key's K
+ * and V rows before reading them (one launch fewer, the same bits);
+ * otherwise the transform's own launch runs first. Limits, errors and
+ * *pending as pcl_kv_cache_append_transformed and pcl_attention_launch; on
+ * an error nothing was launched and the cache is unchanged. */
+int pcl_kv_cache_attend_token(pcl_kv_cache *cache, pcl_head_transform *transform,
+                              const float *raw_q, const float *raw_k, const float *raw_v,
+                              float q_scale, int kernel, float *q_out, float *out,
+                              pcl_kv_pending *pending);
+
 /* ---- 6. attention output block ---------------------------------------------
  *
  * The step after attention (src/engine/attention.rs:866-884): projected =

@@ -83,6 +83,7 @@ EXPORTS = (
     "pcl_head_transform_prepare",
     "pcl_head_transform_query",
     "pcl_kv_cache_append_transformed",
+    "pcl_kv_cache_attend_token",
     "pcl_attention_output",
     "pcl_version",
 )
@@ -213,6 +214,8 @@ def load():
             ("pcl_head_transform_query", ctypes.c_int, [vp, vp, i64, i64, vp]),
             ("pcl_kv_cache_append_transformed", ctypes.c_int,
              [vp, vp, vp, vp, vp, i64, vp, pend]),
+            ("pcl_kv_cache_attend_token", ctypes.c_int,
+             [vp, vp, vp, vp, vp, ctypes.c_float, ctypes.c_int, vp, vp, pend]),
             ("pcl_attention_output", ctypes.c_int,
              [vp, vp, i64, i64, vp, i64, vp, ctypes.c_float, vp, vp, vp])):
         fn = getattr(lib, name)
@@ -537,6 +540,20 @@ class LayerCache:
             self.handle, transform.handle, ctypes.c_void_p(raw_q_ptr),
             ctypes.c_void_p(raw_k_ptr), ctypes.c_void_p(raw_v_ptr or None), int(n),
             ctypes.c_void_p(q_out_ptr), ctypes.byref(pending)))
+        return pending
+
+    def attend_token(self, transform, raw_q_ptr, raw_k_ptr, raw_v_ptr, q_out_ptr, out_ptr,
+                     q_scale=1.0, kernel=KERNEL_AUTO):
+        """One decode token: its raw projections through `transform`, K/V
+        appended, prepared queries to q_out, and the attention of the token
+        over the cache into out ([qheads][dim]), in one call (the transform
+        folded into the pipelined decode's launch where that kernel runs)."""
+        pending = PclPending()
+        self._check(self.lib.pcl_kv_cache_attend_token(
+            self.handle, transform.handle, ctypes.c_void_p(raw_q_ptr),
+            ctypes.c_void_p(raw_k_ptr), ctypes.c_void_p(raw_v_ptr or None), float(q_scale),
+            int(kernel), ctypes.c_void_p(q_out_ptr), ctypes.c_void_p(out_ptr),
+            ctypes.byref(pending)))
         return pending
 
     def advance(self, n):

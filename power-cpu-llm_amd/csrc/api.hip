@@ -916,6 +916,36 @@ int launch_plan(pcl_context *ctx, const pcl_attention_desc &desc, Plan *plan)
 
 } // namespace
 
+int pcl::launch_step(pcl_context *ctx, const pcl_attention_desc &desc, const StepFold &f,
+                     const std::function<int()> &separate)
+{
+    if (desc.nq != 1)
+        return PCL_INVALID_SHAPE;
+    Plan plan;
+    int rc = launch_plan(ctx, desc, &plan);
+    if (rc != PCL_OK)
+        return rc;
+    (void)hipSetDevice(ctx->device);
+    Params &p = plan.p;
+    if (!plan.empty && plan.kernel == PCL_KERNEL_PIPE_KV && p.dim == p.dk) {
+        p.sq = f.rq;
+        p.sk = f.rk;
+        p.sv = f.rv;
+        p.sqs = f.qs;
+        p.sks = f.ks;
+        p.srot = f.rot;
+        p.snk = f.nk;
+        p.snv = f.nv;
+        p.sqo = f.qo;
+        p.seps = f.eps;
+    } else {
+        rc = separate();
+        if (rc != PCL_OK)
+            return rc;
+    }
+    return run_plan(ctx, plan);
+}
+
 extern "C" {
 
 int pcl_attention_launch(pcl_context *ctx, const pcl_attention_desc *desc)

@@ -4,8 +4,11 @@
 
 #include <hip/hip_runtime.h>
 
+#include "pcl_attention.h"
+
 #include <cstddef>
 #include <cstdint>
+#include <functional>
 #include <vector>
 
 // Event pair of one timed kernel role in one launch.
@@ -62,5 +65,23 @@ namespace pcl {
 int kv_cache_reserve(pcl_kv_cache *c, int64_t n);
 // Records the step in *pending and counts its n rows (written at row len).
 void kv_cache_advance_rows(pcl_kv_cache *c, int64_t n, pcl_kv_pending *pending);
+
+// A one-token decode step's head transform (the token's raw rows, the
+// learned scales, the (sin, cos) pairs of its position, the norm epsilon)
+// and where its prepared rows go: the new key's K and V rows and the
+// prepared queries.
+struct StepFold {
+    const float *rq, *rk, *rv, *qs, *ks, *rot;
+    float *nk, *nv, *qo;
+    float eps;
+};
+
+// The attention launch of `desc` (one query) with the step's transform:
+// folded into the launch when the planned kernel runs it (the pipelined
+// decode at head dims 64-512), otherwise `separate` (the transform's own
+// launch on the same stream) runs first. Validation errors return before
+// anything is launched.
+int launch_step(pcl_context *ctx, const pcl_attention_desc &desc, const StepFold &fold,
+                const std::function<int()> &separate);
 
 } // namespace pcl

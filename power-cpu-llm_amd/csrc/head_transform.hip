@@ -33,6 +33,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstring>
 #include <new>
 #include <vector>
 
@@ -434,6 +435,62 @@ int pcl_kv_cache_append_transformed(pcl_kv_cache *c, pcl_head_transform *t, cons
     if (rc != PCL_OK)
         return rc;
     pcl::kv_cache_advance_rows(c, n, pending);
+    return PCL_OK;
+}
+
+int pcl_kv_cache_attend_token(pcl_kv_cache *c, pcl_head_transform *t, const float *raw_q,
+                              const float *raw_k, const float *raw_v, float q_scale, int kernel,
+                              float *q_out, float *out, pcl_kv_pending *pending)
+{
+    if (!c || !t || !pending || !raw_q || !raw_k || !q_out || !out)
+        return PCL_INVALID_SHAPE;
+    if (t->ctx != c->ctx || t->kvheads != c->kvheads || t->dim != c->dim)
+        return PCL_INVALID_SHAPE; // "cache owner/layer/geometry mismatch"
+    if (!raw_v && t->sliding)
+        return PCL_INVALID_SHAPE;
+    if (c->total > kMaxPositions - 1)
+        return PCL_RESOURCE_LIMIT;
+    int rc = pcl::kv_cache_reserve(c, 1);
+    if (rc != PCL_OK)
+        return rc;
+    (void)hipSetDevice(t->ctx->device);
+    rc = ensure_table(t, c->total + 1);
+    if (rc != PCL_OK)
+        return rc;
+    // the encoder descriptor of the step, its row counted (encoder_desc
+    // after the append)
+    const int64_t width = c->width, retained = c->len - c->start + 1;
+    float *nk = c->k + c->len * width, *nv = c->v + c->len * width;
+    pcl_attention_desc d;
+    std::memset(&d, 0, sizeof d);
+    d.q = q_out;
+    d.q_stride = t->qheads * t->dim;
+    d.nq = 1;
+    d.k0 = c->k + c->start * width;
+    d.v0 = c->v + c->start * width;
+    d.n0 = retained;
+    d.qheads = t->qheads;
+    d.kvheads = c->kvheads;
+    d.dim = c->dim;
+    d.kh_first = 0;
+    d.kh_end = c->kvheads;
+    d.causal = 1;
+    d.window = c->window;
+    d.first_key = c->total + 1 - retained;
+    d.first_query = c->total;
+    d.q_scale = q_scale;
+    d.out = out;
+    d.o_stride = t->qheads * t->dim;
+    d.kernel = kernel;
+    const pcl::StepFold fold{raw_q, raw_k, raw_v, t->scales, t->scales + t->dim,
+                             t->tab + c->total * t->dim, nk, nv, q_out, t->eps};
+    const int64_t position = c->total;
+    rc = pcl::launch_step(c->ctx, d, fold, [&] {
+        return run(t, raw_q, raw_k, raw_v, 1, position, q_out, nk, nv, width);
+    });
+    if (rc != PCL_OK)
+        return rc;
+    pcl::kv_cache_advance_rows(c, 1, pending);
     return PCL_OK;
 }
 

@@ -33,6 +33,7 @@ template <int DK, bool WIDE> constexpr bool pipe_slice_loads();
 // Output: for a launch of a single chunk, the output itself; otherwise the
 // chunk partial (m, l, O) for the combine kernel (split_kv.hip).
 #include "attention_device.hpp"
+#include "step_prologue.hpp"
 
 namespace pcl {
 
@@ -97,21 +98,37 @@ template <int DK, bool WIDE> constexpr bool pipe_slice_loads()
 // 16-byte aligned, with q and sb at 16-byte offsets: their 16-byte reads
 // and writes stay single ds_read_b128 / ds_write_b128 instructions (at
 // 4-byte alignment each one split into two ds_read2_b32).
-template <int DK, bool WIDE> struct __attribute__((aligned(16))) PipeLds {
+// With a one-token step's head transform folded in (STEP), the narrow
+// layout's score wave prepares its unit's query rows in q as well, and the
+// new key's K and V rows are prepared through `row` there (the score wave
+// may be in its first tile meanwhile) and through sb and p in the wide
+// layout (free until its prologue barriers).
+template <int DK, bool WIDE, bool STEP> struct __attribute__((aligned(16))) PipeLds {
     float p[2][8][64];    // probabilities, [slot][4b + r][lane]
     float alpha[2][kRows];
     float rs[2][kRows];
     float m[kRows];       // chunk maximum
-    float q[pipe_q_lds<DK, WIDE>() ? kRows * (DK + 4) : 4];
+    float q[pipe_q_lds<DK, WIDE>() || STEP ? kRows * (DK + 4) : 4];
+    float row[STEP && !pipe_dual<DK, WIDE>() ? DK : 4];
     // raw scores of a tile's second 16-key block from the second score
     // wave, [tile & 1][r][lane]
     float sb[pipe_score_waves<DK, WIDE>() > 1 ? 2 : 1][4][64];
     int any[2];
 };
 
-template <int DK, bool FULL>
-__device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, int c,
-                                           PipeLds<DK, false> &s)
+// With a one-token step's transform folded in: whether chunk c holds the
+// step's new key (the launch's last key) among its first `keys` keys, so
+// that its first K or V requests would read that key's row (directly, or
+// as the clamped row of a padding key) before it is written.
+__device__ __forceinline__ bool step_row_wait(const Params &p, int c, int keys)
+{
+    const int64_t cbase = (int64_t)c * kChunk;
+    return cbase + kChunk >= p.nkeys && p.nkeys - 1 < cbase + keys;
+}
+
+template <int DK, bool FULL, bool STEP>
+__device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, int c, int ci,
+                                           PipeLds<DK, false, STEP> &s)
 {
     static_assert(!pipe_dual<DK, false>(), "head dims above 256 take the two score waves");
     constexpr int NU = DK / 32; // score chain steps
@@ -124,26 +141,6 @@ __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, i
     const int64_t klast = p.nkeys - 1;
     const int64_t hoff = (int64_t)kh * p.dim;
 
-    // Q^T B operands: Q[row][32u + 8g + jj] * q_scale (0 for padding rows).
-    float q[NU][8];
-    {
-        const bool rin = row < p.nrows;
-        const int query = rin ? row / p.group : 0;
-        const int h = kh * p.group + (rin ? row % p.group : 0);
-        const float *qp = p.q + (int64_t)query * p.q_stride + (int64_t)h * p.dim;
-#pragma unroll
-        for (int u = 0; u < NU; ++u)
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const int d = 32 * u + 8 * g + 4 * hh;
-                const bool din = FULL || d < p.dim;
-                const f4 x = ldg4(qp + (din ? d : 0)) * p.q_scale;
-                const f4 v = (rin && din) ? x : f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    q[u][4 * hh + j] = v[j];
-            }
-    }
     // The K piece in flight: a whole 16-key block (16 keys x DK dims).
     constexpr int PD = DK;
     constexpr int PU = PD / 32; // u-steps per piece
@@ -182,7 +179,56 @@ __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, i
                 kb[uu][h] = din ? x : f4{0.f, 0.f, 0.f, 0.f};
             }
     };
-    load_k(0, 0, 0);
+    // Q^T B operands: Q[row][32u + 8g + jj] * q_scale (0 for padding rows).
+    float q[NU][8];
+    if constexpr (STEP) {
+        // The step's query rows, prepared here while the first K block is
+        // in flight. The step's new key (the launch's last) is written into
+        // the cache by the value wave of its chunk before that wave's first
+        // barrier (tile 0 handed over); the K blocks requested before this
+        // wave reaches it, (0,0), (0,1) and (1,0), hold the chunk's first 48
+        // keys, so only a chunk whose new key is among those (a block past
+        // the key reads the key's row: clamped) waits for the row first
+        // (#S), and the others stream from the start.
+        const bool wait = step_row_wait(p, c, 48);
+        StepQueryRows<DK> sqr;
+        sqr.issue(p, unit, kh);
+        if (!wait)
+            load_k(0, 0, 0);
+        if (sqr.finish(p, unit, kh, s.q, DK + 4, ci == 0 && p.sqo))
+            atomicOr(p.err, kErrTransform);
+        if (wait) {
+            __syncthreads(); // #S: the new key's rows written
+            load_k(0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const f4 v = *(const f4 *)(s.q + col * (DK + 4) + 32 * u + 8 * g + 4 * hh);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    q[u][4 * hh + j] = v[j];
+            }
+    } else {
+        const bool rin = row < p.nrows;
+        const int query = rin ? row / p.group : 0;
+        const int h = kh * p.group + (rin ? row % p.group : 0);
+        const float *qp = p.q + (int64_t)query * p.q_stride + (int64_t)h * p.dim;
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int d = 32 * u + 8 * g + 4 * hh;
+                const bool din = FULL || d < p.dim;
+                const f4 x = ldg4(qp + (din ? d : 0)) * p.q_scale;
+                const f4 v = (rin && din) ? x : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    q[u][4 * hh + j] = v[j];
+            }
+        load_k(0, 0, 0);
+    }
     const ChunkKeys ck = chunk_keys(p, row, cbase);
     float m = kNegInf;
     bool bad = false;
@@ -270,9 +316,9 @@ __device__ __forceinline__ void score_wave(const Params &p, int unit, int kvl, i
 // Barriers (the value waves keep the same count): #Q after Q^T is staged,
 // #0 after the second wave's tile-0 scores, #t+1 after tile t is handed over,
 // and one after the chunk maximum.
-template <int DK, bool FULL, int ROLE, bool WIDE>
-__device__ __forceinline__ void score_wave_dual(const Params &p, int unit, int kvl, int c,
-                                                PipeLds<DK, WIDE> &s)
+template <int DK, bool FULL, int ROLE, bool WIDE, bool STEP>
+__device__ __forceinline__ void score_wave_dual(const Params &p, int unit, int kvl, int c, int ci,
+                                                PipeLds<DK, WIDE, STEP> &s)
 {
     static_assert(pipe_q_lds<DK, WIDE>(), "the two score waves share Q^T in LDS");
     constexpr int QLD = DK + 4;
@@ -303,39 +349,65 @@ __device__ __forceinline__ void score_wave_dual(const Params &p, int unit, int k
             }
     };
     // the first piece is requested before Q^T is staged, so the two loads'
-    // latencies overlap (a barrier waits on LDS traffic only)
-    load_k(0, 0);
+    // latencies overlap (a barrier waits on LDS traffic only); with a step's
+    // transform folded in (STEP), the new key's K and V rows are written
+    // before #Q, so only a chunk whose first tile holds the new key (or a
+    // clamped key past it) requests the tile after #Q
+    const bool last = STEP && (int64_t)(c + 1) * kChunk >= p.nkeys;
+    const bool wait = STEP && step_row_wait(p, c, kTile);
+    StepQueryRows<DK> sqr;
+    if constexpr (STEP && ROLE == 0)
+        sqr.issue(p, unit, kh);
+    if (!wait)
+        load_k(0, 0);
 
-    // Q^T, staged by both score waves: every load is issued before the first
-    // LDS store (a load-store loop would wait out one round trip per row).
-    // Padding rows and dims read a valid row and store zeros.
-    constexpr int QN = kRows * (DK / 4) / 128; // f4 per lane
-    auto q_in = [&](int it, int *f, int *d) {
-        const int i = lane + 64 * ROLE + 128 * it;
-        *f = unit * kRows + i / (DK / 4);
-        *d = (i % (DK / 4)) * 4;
-        return *f < p.nrows && (FULL || *d < p.dim);
-    };
-    f4 qs[QN];
+    if constexpr (STEP) {
+        // the first score wave prepares the unit's query rows; in the new
+        // key's chunk the second prepares its K row (V: the first value wave)
+        if constexpr (ROLE == 0) {
+            if (sqr.finish(p, unit, kh, s.q, QLD, ci == 0 && p.sqo))
+                atomicOr(p.err, kErrTransform);
+        } else if (last) {
+            if (step_kv_row<DK, true>(p, kh, &s.sb[0][0][0]))
+                atomicOr(p.err, kErrTransform);
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // the row is in L2 before #Q
+        }
+        __syncthreads(); // #Q: Q^T staged, the new key's rows written
+        if (wait)
+            load_k(0, 0);
+    } else {
+        // Q^T, staged by both score waves: every load is issued before the
+        // first LDS store (a load-store loop would wait out one round trip
+        // per row). Padding rows and dims read a valid row and store zeros.
+        constexpr int QN = kRows * (DK / 4) / 128; // f4 per lane
+        auto q_in = [&](int it, int *f, int *d) {
+            const int i = lane + 64 * ROLE + 128 * it;
+            *f = unit * kRows + i / (DK / 4);
+            *d = (i % (DK / 4)) * 4;
+            return *f < p.nrows && (FULL || *d < p.dim);
+        };
+        f4 qs[QN];
 #pragma unroll
-    for (int it = 0; it < QN; ++it) {
-        int f, d;
-        const bool in = q_in(it, &f, &d);
-        const int ff = in ? f : 0;
-        qs[it] = ldg4(p.q + (int64_t)(ff / p.group) * p.q_stride +
-                      (int64_t)(kh * p.group + ff % p.group) * p.dim + (in ? d : 0));
-    }
+        for (int it = 0; it < QN; ++it) {
+            int f, d;
+            const bool in = q_in(it, &f, &d);
+            const int ff = in ? f : 0;
+            qs[it] = ldg4(p.q + (int64_t)(ff / p.group) * p.q_stride +
+                          (int64_t)(kh * p.group + ff % p.group) * p.dim + (in ? d : 0));
+        }
 #pragma unroll
-    for (int it = 0; it < QN; ++it) {
-        int f, d;
-        const bool in = q_in(it, &f, &d);
-        f4 x = qs[it];
-        // an unconditional use: keeps the (wave-uniform) row test from
-        // sinking each load into a branch that waits for it alone
-        asm volatile("" : "+v"(x));
-        *(f4 *)(s.q + (f - unit * kRows) * QLD + d) = in ? x * p.q_scale : f4{0.f, 0.f, 0.f, 0.f};
+        for (int it = 0; it < QN; ++it) {
+            int f, d;
+            const bool in = q_in(it, &f, &d);
+            f4 x = qs[it];
+            // an unconditional use: keeps the (wave-uniform) row test from
+            // sinking each load into a branch that waits for it alone
+            asm volatile("" : "+v"(x));
+            *(f4 *)(s.q + (f - unit * kRows) * QLD + d) =
+                in ? x * p.q_scale : f4{0.f, 0.f, 0.f, 0.f};
+        }
+        __syncthreads(); // #Q: Q^T staged
     }
-    __syncthreads(); // #Q: Q^T staged
 
     // this wave's block of tile t: its canonical score chain (run: any key of
     // the block allowed for the unit), the next piece loaded as registers free
@@ -457,9 +529,9 @@ __device__ __forceinline__ void score_wave_dual(const Params &p, int unit, int k
 // (split_kv.hip) without its launch.
 enum PipeMode { kDirect = 0, kPartial = 1, kMergeOut = 2 };
 
-template <int DK, int MODE, bool FULL, bool WIDE>
+template <int DK, int MODE, bool FULL, bool WIDE, bool STEP>
 __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, int c,
-                                           PipeLds<DK, WIDE> &s, int vw, int ci)
+                                           PipeLds<DK, WIDE, STEP> &s, int vw, int ci)
 {
     constexpr int VD = pipe_value_dims<DK, WIDE>();
     static_assert(VD % 64 == 0, "whole 64-dim output groups per value wave");
@@ -504,14 +576,51 @@ __device__ __forceinline__ void value_wave(const Params &p, int unit, int kvl, i
         for (int sl = 0; sl < VS; ++sl)
             load_next_sl(t, grp, sl);
     };
+    // With a step's transform folded in (STEP), the chunk of the step's new
+    // key prepares that key's V row (and in the narrow layout its K row) and
+    // writes both into the cache before the wave's first barrier. The first
+    // V group is requested before that unless its tile (the first) holds
+    // the new key or a clamped key past it; the narrow layout's score wave
+    // requests blocks of the first 48 keys before that barrier, so there
+    // a chunk whose new key is among them waits for the rows first (#S).
+    const bool last = STEP && (int64_t)(c + 1) * kChunk >= p.nkeys;
+    const bool wait_s = STEP && pipe_score_waves<DK, WIDE>() == 1 && step_row_wait(p, c, 48);
+    const bool early = !(STEP && step_row_wait(p, c, kTile)) && !wait_s;
+    if (early) {
 #pragma unroll
-    for (int sl = 0; sl < VS; ++sl)
-        load_v_sl(0, 0, sl);
+        for (int sl = 0; sl < VS; ++sl)
+            load_v_sl(0, 0, sl);
+    }
+    if constexpr (STEP) {
+        if (last) {
+            bool bad = false;
+            if constexpr (pipe_score_waves<DK, WIDE>() == 1) {
+                bad = step_kv_row<DK, true>(p, kh, s.row);
+                bad |= step_kv_row<DK, false>(p, kh, s.row);
+            } else if (vw == 0) {
+                bad = step_kv_row<DK, false>(p, kh, &s.p[0][0][0]);
+            }
+            if (bad)
+                atomicOr(p.err, kErrTransform);
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // the rows are in L2 before the barrier
+        }
+    }
     if constexpr (pipe_score_waves<DK, WIDE>() > 1) {
         // the score waves' prologue barriers (Q^T staged, the first block
         // scored) pass with the first group already requested
         __syncthreads(); // #Q
+        if (!early) {
+#pragma unroll
+            for (int sl = 0; sl < VS; ++sl)
+                load_v_sl(0, 0, sl);
+        }
         __syncthreads(); // #0
+    } else if (!early) {
+        if (wait_s)
+            __syncthreads(); // #S: the new key's rows written
+#pragma unroll
+        for (int sl = 0; sl < VS; ++sl)
+            load_v_sl(0, 0, sl);
     }
     float l = 0.f;
     f4 O[NQ][4];
@@ -631,11 +740,11 @@ template <int DK, bool FULL> constexpr int pipe_waves_per_simd()
 
 // FULL: the head dim equals the padded head dim (no dim clamping). WIDE: the
 // wide layout at head dims up to 256.
-template <int DK, int MODE, bool FULL, bool WIDE>
+template <int DK, int MODE, bool FULL, bool WIDE, bool STEP>
 __global__ __launch_bounds__((pipe_threads<DK, WIDE>()), (pipe_waves_per_simd<DK, FULL>()))
 void pipe_kv_kernel(Params p, int c0)
 {
-    __shared__ PipeLds<DK, WIDE> s;
+    __shared__ PipeLds<DK, WIDE, STEP> s;
     const int ci = c0 + (int)blockIdx.x; // the launch's chunk index
     const int c = p.c_lo + ci;
     const int unit = blockIdx.y % p.units;
@@ -645,16 +754,16 @@ void pipe_kv_kernel(Params p, int c0)
     constexpr int VMODE = MODE == kMergeOut ? kPartial : MODE;
     if constexpr (pipe_score_waves<DK, WIDE>() == 1) {
         if (wave == 0)
-            score_wave<DK, FULL>(p, unit, kvl, c, s);
+            score_wave<DK, FULL, STEP>(p, unit, kvl, c, ci, s);
         else
-            value_wave<DK, VMODE, FULL, WIDE>(p, unit, kvl, c, s, wave - 1, ci);
+            value_wave<DK, VMODE, FULL, WIDE, STEP>(p, unit, kvl, c, s, wave - 1, ci);
     } else {
         if (wave == 0) {
-            score_wave_dual<DK, FULL, 0, WIDE>(p, unit, kvl, c, s);
+            score_wave_dual<DK, FULL, 0, WIDE, STEP>(p, unit, kvl, c, ci, s);
         } else if (wave == 1) {
-            score_wave_dual<DK, FULL, 1, WIDE>(p, unit, kvl, c, s);
+            score_wave_dual<DK, FULL, 1, WIDE, STEP>(p, unit, kvl, c, ci, s);
         } else {
-            value_wave<DK, VMODE, FULL, WIDE>(p, unit, kvl, c, s, wave - 2, ci);
+            value_wave<DK, VMODE, FULL, WIDE, STEP>(p, unit, kvl, c, s, wave - 2, ci);
         }
     }
     if constexpr (MODE == kMergeOut) {
@@ -700,38 +809,50 @@ void pipe_kv_kernel(Params p, int c0)
 // at 1024 items, the 32K decode, the narrow layout is 5 % faster).
 constexpr int64_t kPipeWideMaxItems256 = 512;
 
-template <int DK, int MODE, bool FULL, bool WIDE>
+template <int DK, int MODE, bool FULL, bool WIDE, bool STEP>
 static void launch_dk(const Params &p, dim3 grid, int c0, hipStream_t stream)
 {
-    pipe_kv_kernel<DK, MODE, FULL, WIDE><<<grid, pipe_threads<DK, WIDE>(), 0, stream>>>(p, c0);
+    pipe_kv_kernel<DK, MODE, FULL, WIDE, STEP>
+        <<<grid, pipe_threads<DK, WIDE>(), 0, stream>>>(p, c0);
 }
 
 // Chunks [c0, c0 + n) of the launch.
-template <int MODE, bool FULL>
+template <int MODE, bool FULL, bool STEP>
 hipError_t launch_mode(const Params &p, int c0, int n, hipStream_t stream)
 {
     const dim3 grid(n, p.nkv * p.units);
     const bool wide = (int64_t)n * p.nkv * p.units < kPipeWideMaxItems256;
     switch (p.dk) {
-    case 64: launch_dk<64, MODE, FULL, false>(p, grid, c0, stream); break;
-    case 128: launch_dk<128, MODE, FULL, true>(p, grid, c0, stream); break;
+    case 64: launch_dk<64, MODE, FULL, false, STEP>(p, grid, c0, stream); break;
+    case 128: launch_dk<128, MODE, FULL, true, STEP>(p, grid, c0, stream); break;
     case 256:
-        wide ? launch_dk<256, MODE, FULL, true>(p, grid, c0, stream)
-             : launch_dk<256, MODE, FULL, false>(p, grid, c0, stream);
+        wide ? launch_dk<256, MODE, FULL, true, STEP>(p, grid, c0, stream)
+             : launch_dk<256, MODE, FULL, false, STEP>(p, grid, c0, stream);
         break;
-    case 512: launch_dk<512, MODE, FULL, true>(p, grid, c0, stream); break;
+    case 512: launch_dk<512, MODE, FULL, true, STEP>(p, grid, c0, stream); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
+// A one-token step's head transform folds in (Params::sq) only where the
+// head dim is the padded one (the transform's own head dims from 64 up).
 template <bool FULL>
 hipError_t launch_full(const Params &p, int c0, int n, bool merge_out, hipStream_t stream)
 {
+    if (p.sq) {
+        if constexpr (FULL) {
+            if (merge_out || c0 != 0 || n != p.nch || p.nq != 1)
+                return hipErrorInvalidValue;
+            return p.ws_o == nullptr ? launch_mode<kDirect, true, true>(p, c0, n, stream)
+                                     : launch_mode<kPartial, true, true>(p, c0, n, stream);
+        }
+        return hipErrorInvalidValue;
+    }
     if (merge_out)
-        return launch_mode<kMergeOut, FULL>(p, c0, n, stream);
-    return p.ws_o == nullptr ? launch_mode<kDirect, FULL>(p, c0, n, stream)
-                             : launch_mode<kPartial, FULL>(p, c0, n, stream);
+        return launch_mode<kMergeOut, FULL, false>(p, c0, n, stream);
+    return p.ws_o == nullptr ? launch_mode<kDirect, FULL, false>(p, c0, n, stream)
+                             : launch_mode<kPartial, FULL, false>(p, c0, n, stream);
 }
 
 // Chunks [c0, c0 + n) of the launch, their partials in the launch's chunk

@@ -31,7 +31,9 @@ __device__ __forceinline__ double norm_inverse(const float *row, float eps)
     for (int i = 0; i < B / 4; ++i)
         cur[i] = *(const f4 *)(row + 4 * i);
     double sum = 0.0;
-#pragma unroll
+    // two batches per iteration (fully unrolled, the compiler would hoist
+    // every read of the row and hold it in registers)
+#pragma unroll 2
     for (int b = 0; b < D; b += B) {
         if (b + B < D) {
 #pragma unroll
@@ -81,6 +83,27 @@ __device__ __forceinline__ void wave_lds_sync()
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
 
+// This lane's rotation pairs j = lane + 64m of the step's position: (s, c)
+// and the learned scales of both halves (Q's or K's).
+template <int D> struct StepRotation {
+    static constexpr int H = D / 2;
+    static constexpr int PAIRS = (H + 63) / 64;
+    float s[PAIRS], c[PAIRS], sa[PAIRS], sb[PAIRS];
+
+    __device__ __forceinline__ void load(const Params &p, const float *scale)
+    {
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int m = 0; m < PAIRS; ++m) {
+            const int j = lane + 64 * m < H ? lane + 64 * m : 0;
+            s[m] = ldg(p.srot + 2 * j);
+            c[m] = ldg(p.srot + 2 * j + 1);
+            sa[m] = ldg(scale + j);
+            sb[m] = ldg(scale + j + H);
+        }
+    }
+};
+
 // The prepared K (KEY) or V row of KV head kh of the step's token, by one
 // wave: staged through buf (D floats of LDS, 16-byte aligned) and stored at
 // the step's new cache row. Whether an input or output is not finite.
@@ -88,32 +111,44 @@ template <int D, bool KEY>
 __device__ __forceinline__ bool step_kv_row(const Params &p, int kh, float *buf)
 {
     constexpr int H = D / 2;
+    constexpr int PAIRS = StepRotation<D>::PAIRS;
     const int lane = threadIdx.x & 63;
     const float *raw = (KEY || !p.sv ? p.sk : p.sv) + (int64_t)kh * D;
     float *dst = (KEY ? p.snk : p.snv) + (int64_t)kh * D;
+    // the row and (K) the rotation pairs requested together
+    StepRotation<D> rot;
+    f4 x[(D / 4 + 63) / 64];
+#pragma unroll
+    for (int k = 0; k < (D / 4 + 63) / 64; ++k)
+        if (lane + 64 * k < D / 4)
+            x[k] = ldg4(raw + 4 * (lane + 64 * k));
+    if (KEY)
+        rot.load(p, p.sks);
     bool bad = false;
 #pragma unroll
-    for (int i = lane; i < D / 4; i += 64) {
-        const f4 x = ldg4(raw + 4 * i);
+    for (int k = 0; k < (D / 4 + 63) / 64; ++k)
+        if (lane + 64 * k < D / 4) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            bad |= !is_finite(x[e]);
-        *(f4 *)(buf + 4 * i) = x;
-    }
+            for (int e = 0; e < 4; ++e)
+                bad |= !is_finite(x[k][e]);
+            *(f4 *)(buf + 4 * (lane + 64 * k)) = x[k];
+        }
     wave_lds_sync();
     double inv = 0.0;
     if (lane == 0)
         inv = norm_inverse<D>(buf, p.seps);
     inv = __shfl(inv, 0);
 #pragma unroll
-    for (int j = lane; j < H; j += 64) {
+    for (int m = 0; m < PAIRS; ++m) {
+        const int j = lane + 64 * m;
+        if (j >= H)
+            continue;
         float a, b;
-        if (KEY) {
-            const float s = p.srot[2 * j], c = p.srot[2 * j + 1];
-            transform_pair<true>(buf[j], buf[j + H], inv, p.sks[j], p.sks[j + H], s, c, &a, &b);
-        } else {
+        if (KEY)
+            transform_pair<true>(buf[j], buf[j + H], inv, rot.sa[m], rot.sb[m], rot.s[m],
+                                 rot.c[m], &a, &b);
+        else
             transform_pair<false>(buf[j], buf[j + H], inv, 0.f, 0.f, 0.f, 0.f, &a, &b);
-        }
         bad |= !is_finite(a) || !is_finite(b);
         stg(dst + j, a);
         stg(dst + j + H, b);
@@ -127,71 +162,102 @@ __device__ __forceinline__ bool step_kv_row(const Params &p, int kh, float *buf)
 // (query 0, head kh*group + row % group), pre-scaled by q_scale as the
 // kernels scale a loaded query; rows past nrows are zero. With `out`, the
 // prepared (unscaled) rows are also stored to the step's query output.
-// Whether an input or output is not finite.
-template <int D>
-__device__ __forceinline__ bool step_q_rows(const Params &p, int unit, int kh, float *qb, int ld,
-                                            bool out)
-{
-    constexpr int H = D / 2;
-    constexpr int NV = D / 4;              // 16-byte pieces per row
-    constexpr int BATCH = 8;               // pieces per lane in flight
-    constexpr int ALL = kRows * NV;        // pieces of the unit's rows
-    const int lane = threadIdx.x & 63;
-    const int r0 = unit * kRows;
-    const int nr = p.nrows - r0 < kRows ? p.nrows - r0 : kRows;
-    auto raw_row = [&](int r) {
-        return p.sq + (int64_t)(kh * p.group + (r0 + r) % p.group) * D;
-    };
-    bool bad = false;
-    for (int i0 = 0; i0 < ALL; i0 += 64 * BATCH) {
-        f4 x[BATCH];
+// issue() requests the first pieces of the rows and the rotation pairs, so
+// that a caller can request other data (its first K block) behind them and
+// finish() waits only for these.
+template <int D> struct StepQueryRows {
+    static constexpr int H = D / 2;
+    static constexpr int NV = D / 4;    // 16-byte pieces per row
+    static constexpr int BATCH = 8;     // pieces per lane in flight
+    static constexpr int PAIRS = StepRotation<D>::PAIRS;
+    f4 x[BATCH];
+    StepRotation<D> rot;
+    int nr; // real rows of the unit
+
+    __device__ __forceinline__ const float *raw_row(const Params &p, int unit, int kh, int r) const
+    {
+        return p.sq + (int64_t)(kh * p.group + (unit * kRows + r) % p.group) * D;
+    }
+
+    // pieces i = i0 + lane + 64k (k < BATCH) of the unit's real rows
+    __device__ __forceinline__ void load_batch(const Params &p, int unit, int kh, int i0)
+    {
+        const int lane = threadIdx.x & 63;
 #pragma unroll
         for (int k = 0; k < BATCH; ++k) {
             const int i = i0 + lane + 64 * k;
-            const int r = i / NV;
-            if (i < ALL && r < nr)
-                x[k] = ldg4(raw_row(r) + 4 * (i % NV));
+            if (i < nr * NV)
+                x[k] = ldg4(raw_row(p, unit, kh, i / NV) + 4 * (i % NV));
         }
+    }
+
+    __device__ __forceinline__ bool store_batch(float *qb, int ld, int i0)
+    {
+        const int lane = threadIdx.x & 63;
+        bool bad = false;
 #pragma unroll
         for (int k = 0; k < BATCH; ++k) {
             const int i = i0 + lane + 64 * k;
-            const int r = i / NV;
-            if (i < ALL) {
-                f4 v = f4{0.f, 0.f, 0.f, 0.f};
-                if (r < nr) {
-                    v = x[k];
+            if (i < nr * NV) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        bad |= !is_finite(v[e]);
+                for (int e = 0; e < 4; ++e)
+                    bad |= !is_finite(x[k][e]);
+                *(f4 *)(qb + (i / NV) * ld + 4 * (i % NV)) = x[k];
+            }
+        }
+        return bad;
+    }
+
+    __device__ __forceinline__ void issue(const Params &p, int unit, int kh)
+    {
+        const int r0 = unit * kRows;
+        nr = p.nrows - r0 < kRows ? p.nrows - r0 : kRows;
+        load_batch(p, unit, kh, 0);
+        rot.load(p, p.sqs);
+    }
+
+    __device__ __forceinline__ bool finish(const Params &p, int unit, int kh, float *qb, int ld,
+                                           bool out)
+    {
+        const int lane = threadIdx.x & 63;
+        bool bad = store_batch(qb, ld, 0);
+        // further batches (more than BATCH pieces per lane), one in flight
+#pragma unroll 1
+        for (int i0 = 64 * BATCH; i0 < nr * NV; i0 += 64 * BATCH) {
+            load_batch(p, unit, kh, i0);
+            bad |= store_batch(qb, ld, i0);
+        }
+        // padding rows are zero
+        for (int i = nr * NV + lane; i < kRows * NV; i += 64)
+            *(f4 *)(qb + (i / NV) * ld + 4 * (i % NV)) = f4{0.f, 0.f, 0.f, 0.f};
+        wave_lds_sync();
+        double inv = 0.0;
+        if (lane < nr)
+            inv = norm_inverse<D>(qb + lane * ld, p.seps);
+        for (int r = 0; r < nr; ++r) {
+            const double iv = __shfl(inv, r);
+            float *row = qb + r * ld;
+            float *qo = p.sqo + (int64_t)(kh * p.group + (unit * kRows + r) % p.group) * D;
+#pragma unroll
+            for (int m = 0; m < PAIRS; ++m) {
+                const int j = lane + 64 * m;
+                if (j >= H)
+                    continue;
+                float a, b;
+                transform_pair<true>(row[j], row[j + H], iv, rot.sa[m], rot.sb[m], rot.s[m],
+                                     rot.c[m], &a, &b);
+                bad |= !is_finite(a) || !is_finite(b);
+                if (out) {
+                    stg(qo + j, a);
+                    stg(qo + j + H, b);
                 }
-                *(f4 *)(qb + r * ld + 4 * (i % NV)) = v;
+                row[j] = a * p.q_scale;
+                row[j + H] = b * p.q_scale;
             }
         }
+        wave_lds_sync();
+        return bad;
     }
-    wave_lds_sync();
-    double inv = 0.0;
-    if (lane < nr)
-        inv = norm_inverse<D>(qb + lane * ld, p.seps);
-    for (int r = 0; r < nr; ++r) {
-        const double iv = __shfl(inv, r);
-        float *row = qb + r * ld;
-        float *qo = p.sqo + (int64_t)(kh * p.group + (r0 + r) % p.group) * D;
-#pragma unroll
-        for (int j = lane; j < H; j += 64) {
-            float a, b;
-            const float s = p.srot[2 * j], c = p.srot[2 * j + 1];
-            transform_pair<true>(row[j], row[j + H], iv, p.sqs[j], p.sqs[j + H], s, c, &a, &b);
-            bad |= !is_finite(a) || !is_finite(b);
-            if (out) {
-                stg(qo + j, a);
-                stg(qo + j + H, b);
-            }
-            row[j] = a * p.q_scale;
-            row[j + H] = b * p.q_scale;
-        }
-    }
-    wave_lds_sync();
-    return bad;
-}
+};
 
 } // namespace pcl

@@ -210,8 +210,11 @@ def _resource_remarks(source):
     ("spread_kv.hip", "_ZN3pcl16spread_kv_kernelILi256ELb1ELb0ELb1ELi4ELb0EEEvNS_6ParamsE"),
     ("spread_kv.hip", "_ZN3pcl16spread_kv_kernelILi256ELb1ELb0ELb1ELi2ELb1EEEvNS_6ParamsE"),
     ("spread_kv.hip", "_ZN3pcl16spread_kv_kernelILi256ELb1ELb0ELb1ELi4ELb1EEEvNS_6ParamsE"),
-    ("pipe_kv.hip", "_ZN3pcl14pipe_kv_kernelILi256ELi1ELb1ELb0EEEvNS_6ParamsEi"),
-    ("pipe_kv.hip", "_ZN3pcl14pipe_kv_kernelILi512ELi1ELb1ELb1EEEvNS_6ParamsEi"),
+    ("pipe_kv.hip", "_ZN3pcl14pipe_kv_kernelILi256ELi1ELb1ELb0ELb0EEEvNS_6ParamsEi"),
+    ("pipe_kv.hip", "_ZN3pcl14pipe_kv_kernelILi512ELi1ELb1ELb1ELb0EEEvNS_6ParamsEi"),
+    # the same with a one-token step's head transform folded in
+    ("pipe_kv.hip", "_ZN3pcl14pipe_kv_kernelILi256ELi1ELb1ELb0ELb1EEEvNS_6ParamsEi"),
+    ("pipe_kv.hip", "_ZN3pcl14pipe_kv_kernelILi512ELi1ELb1ELb1ELb1EEEvNS_6ParamsEi"),
     ("fan_kv.hip", "_ZN3pcl13fan_kv_kernelILi256ELb1ELb0ELb1EEEvNS_6ParamsEi"),
     ("fan_kv.hip", "_ZN3pcl13fan_kv_kernelILi256ELb0ELb1ELb0EEEvNS_6ParamsEi"),
 ])

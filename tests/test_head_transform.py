@@ -376,3 +376,108 @@ def test_fused_append_writes_prepared_rows_into_the_cache(pcl, torch, ctx, oracl
         ref.commit()
     cache.close()
     t.close()
+
+
+STEP_CASES = [
+    # qheads, kvh, dim, keys with the new token, window, K-as-V
+    (16, 8, 256, 16500, None, False),  # narrow pipelined layout (>= 512 items), chunk partials
+    (16, 8, 256, 3000, 1024, False),   # wide layout at head dim 256, sliding window
+    (16, 2, 512, 5000, None, True),    # two score waves, K as V
+    (8, 4, 64, 700, None, False),      # head dim 64 (narrow)
+    (8, 2, 128, 1500, None, False),    # head dim 128 (wide)
+    (16, 8, 256, 2049, None, False),   # the new key alone in its chunk
+    (16, 8, 256, 200, None, False),    # one chunk: direct output
+    # the new key among the first keys of its chunk, which the chunk's
+    # first requests would read: those wait for its row
+    (16, 8, 256, 16425, None, False),  # narrow layout, key 40 of its chunk
+    (16, 2, 512, 4865, None, True),    # two score waves, key 0 of its chunk
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", STEP_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_attend_token_folds_the_transform_into_the_decode(pcl, torch, ctx, oracle, case):
+    # one decode token of encode_in_place (attention.rs:949-1080): prepare
+    # (102-156), the cache append, the attention pass. Through the pipelined
+    # decode the transform runs inside the attention launch; its prepared
+    # queries, new K/V row and output equal the two-launch path bit for
+    # bit, whatever kernel AUTO picks, and the exact oracle within 1e-4
+    qh, kvh, dim, nkeys, window, k_as_v = case
+    width = kvh * dim
+    g = np.random.default_rng(nkeys + dim)
+    qs = (1 + 0.1 * g.standard_normal(dim)).astype(np.float32)
+    ks = (1 + 0.1 * g.standard_normal(dim)).astype(np.float32)
+    t = pcl.HeadTransform(ctx, qh, kvh, dim, qs, ks, 1e-6, 10000.0, sliding=not k_as_v)
+    cache = pcl.LayerCache(ctx, kvh, dim, nkeys + 8, window, 1 << 40)
+    cache.reserve_rows(nkeys + 1)
+    k0 = dev(torch, g.standard_normal((nkeys - 1, width), dtype=np.float32))
+    v0 = dev(torch, g.standard_normal((nkeys - 1, width), dtype=np.float32))
+    cache.append(k0.data_ptr(), v0.data_ptr(), nkeys - 1)
+    cache.commit()
+    position = cache.total_tokens()
+    rq = (g.standard_normal(qh * dim) * 3).astype(np.float32)
+    rk = g.standard_normal(width).astype(np.float32)
+    rv = None if k_as_v else g.standard_normal(width).astype(np.float32)
+    tq, tk = dev(torch, rq), dev(torch, rk)
+    tv = dev(torch, rv) if rv is not None else None
+    scale = np.float32(1.0 / np.sqrt(np.float64(dim)))
+
+    def run(mode, kernel):
+        q_out = torch.full((qh * dim,), float("nan"), device="cuda:0")
+        out = torch.full((qh * dim,), float("nan"), device="cuda:0")
+        if mode == "fused":
+            pending = cache.attend_token(t, tq.data_ptr(), tk.data_ptr(),
+                                         tv.data_ptr() if tv is not None else 0,
+                                         q_out.data_ptr(), out.data_ptr(), q_scale=float(scale),
+                                         kernel=kernel)
+        else:
+            pending = cache.append_transformed(t, tq.data_ptr(), tk.data_ptr(),
+                                               tv.data_ptr() if tv is not None else 0, 1,
+                                               q_out.data_ptr())
+            d = cache.encoder_desc(pending, q=q_out.data_ptr(), q_stride=qh * dim, nq=1,
+                                   qheads=qh, kh_first=0, kh_end=kvh, out=out.data_ptr(),
+                                   o_stride=qh * dim, q_scale=float(scale), kernel=kernel)
+            ctx.launch(d)
+        assert ctx.sync() == 0, (mode, kernel)
+        rows = cache.retained_tokens()
+        assert cache.total_tokens() == position + 1
+        new_k, new_v = cache.read(rows - 1, 1)
+        got = [q_out.cpu().numpy(), out.cpu().numpy(), new_k, new_v]
+        if mode == "fused" and kernel == pcl.KERNEL_PIPE_KV:
+            got.append(cache.read(0, rows))
+        cache.rollback(pending)
+        return got, rows
+
+    fused, rows = run("fused", pcl.KERNEL_PIPE_KV)
+    for mode, kernel in (("separate", pcl.KERNEL_PIPE_KV), ("fused", pcl.KERNEL_AUTO)):
+        other, _ = run(mode, kernel)
+        for a, b in zip(fused[:4], other):
+            assert np.array_equal(bits(a), bits(b)), (mode, kernel)
+    q_out, out, new_k, new_v, (keys, values) = fused
+    wq, wk, wv = oracle_tokens(oracle, rq[None], rk[None], None if rv is None else rv[None], 1,
+                               qh, kvh, dim, position, qs, ks, 1e-6, 10000.0, None)
+    assert_rotated_close(q_out, wq, dim)
+    assert_rotated_close(new_k, wk, dim)
+    assert np.array_equal(bits(new_v), bits(wv.reshape(-1)))
+    # the attention over the cache's rows with the prepared new row, from
+    # the device's prepared query pre-scaled in f32 as the kernels scale it
+    qsc = (q_out * scale).astype(np.float32)
+    ok, want = oracle.threaded(qsc, 1, keys, values, qh, kvh, dim, rows, True,
+                               position + 1 - rows, position, window or 0, threads=8)
+    assert ok
+    assert float(np.max(np.abs(out - want))) <= 1e-4
+    assert np.array_equal(out.reshape(qh, dim).argmax(1), want.reshape(qh, dim).argmax(1))
+    # a non-finite raw value sets the transform's error bit through the fold
+    bad_q = tq.clone()
+    bad_q[7] = float("nan")
+    q_out = torch.empty((qh * dim,), device="cuda:0")
+    out = torch.empty((qh * dim,), device="cuda:0")
+    pending = cache.attend_token(t, bad_q.data_ptr(), tk.data_ptr(),
+                                 tv.data_ptr() if tv is not None else 0, q_out.data_ptr(),
+                                 out.data_ptr(), q_scale=float(scale),
+                                 kernel=pcl.KERNEL_PIPE_KV)
+    assert ctx.sync() & 4
+    assert ctx.sync() == 0
+    cache.rollback(pending)
+    cache.close()
+    t.close()
