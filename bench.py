@@ -50,6 +50,7 @@ WORKLOADS = {
     "decode_128k_d512": (16, 2, 512, 1, 131072, True, 0, 131071, "decode", True),
     # the same global-layer decode (16/2/512, unit-norm K) at shorter caches
     "decode_2k_d512": (16, 2, 512, 1, 2048, True, 0, 2047, "decode", True),
+    "decode_4k_d512": (16, 2, 512, 1, 4096, True, 0, 4095, "decode", True),
     "decode_8k_d512": (16, 2, 512, 1, 8192, True, 0, 8191, "decode", True),
     "decode_32k_d512": (16, 2, 512, 1, 32768, True, 0, 32767, "decode", True),
     # the reference's own attention throughput probe

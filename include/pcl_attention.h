@@ -113,8 +113,9 @@ enum pcl_kernel {
     /* 5 is retired (a two-launch decode that no choice selected) and is
        refused with PCL_INVALID_PARAMETER */
     PCL_KERNEL_SPREAD_KV = 6,   /* split-KV decode with each key chunk spread
-                                   over head_dim/32 workgroups that exchange
-                                   raw scores (head dim <= 256, short
+                                   over head_dim/32 slices that exchange raw
+                                   scores (two-wave slices up to head dim
+                                   256, one-wave slices at 512; short
                                    launches); the launch's own merge
                                    workgroups run the ordered combine */
     PCL_KERNEL_FAN_KV = 7,      /* split-KV decode with each (key chunk,

@@ -63,11 +63,12 @@ bool fan_preferred(int dk, int64_t units, int64_t items, int64_t nch)
         return items <= kFanMaxItems256 || (units >= 2 && items <= kFanMaxItems256Units);
     return false;
 }
-// The spread decode's slices (dk/32 per item; a two-wave workgroup with 48
-// KiB of LDS each, three per CU, or two per four-wave workgroup when they
-// take at most two per CU) all fit on the chip at once up to this many per
-// CU of the device the launch runs on (768 on a whole MI355X; fewer on a
-// partitioned one). Its workgroups wait for each other, so it is chosen only
+// The spread decode's slices (dk/32 per item; up to head dim 256 a two-wave
+// workgroup with 48 KiB of LDS each, three per CU, or two per four-wave
+// workgroup when they take at most two per CU; at 512 a one-wave workgroup
+// with 48 KiB of LDS, three per CU) all fit on the chip at once up to this
+// many per CU of the device the launch runs on (768 on a whole MI355X;
+// fewer on a partitioned one). Its workgroups wait for each other, so it is chosen only
 // within that bound and within the items its score-word region holds
 // (requested beyond them, the pipelined kernel runs).
 constexpr int64_t kSpreadSlicesPerCu = 3;
@@ -161,13 +162,15 @@ void chunk_range(const pcl_attention_desc &d, int64_t nkeys, int64_t *c_lo, int6
     *c_hi = (k_hi + pcl::kChunk - 1) / pcl::kChunk;
 }
 
-// Workgroups of a spread launch, or 0 when the head dim has no spread form.
+// Workgroups of a spread launch (its slices: two-wave ones up to head dim
+// 256, one-wave ones at 512), or 0 when its items or their chunk partials
+// exceed the published-word region.
 int64_t spread_workgroups(int dk, int64_t nrows, int64_t nkv, int64_t nch)
 {
-    if (dk > 256)
-        return 0;
     const int64_t units = (nrows + pcl::kRows - 1) / pcl::kRows;
     if (nch * nkv * units > kSpreadMaxItems)
+        return 0;
+    if (nch > 1 && nkv * nrows * nch * (dk + 2) > (int64_t)kSpreadPartWords)
         return 0;
     return nch * nkv * units * pcl::spread_slices(dk);
 }

@@ -74,8 +74,11 @@ __device__ __forceinline__ void spread_merge_row(const Params &p, int kvl, int r
 {
     const int q4 = p.dim / 4;
     const int64_t slot0 = ((int64_t)kvl * p.nrows + row) * p.nch;
-    // the row's threads poll one word of each chunk partial between them
-    if (!wait_partials<LOCAL ? 1 : 8>(p, slot0, d / 4, q4, p.nch)) {
+    // the threads of each wave of the row poll one word of each chunk
+    // partial between them (a row of more than 64 threads spans two waves,
+    // each of which waits for all chunks)
+    const int wq = q4 < 64 ? q4 : 64;
+    if (!wait_partials<LOCAL ? 1 : 8>(p, slot0, (d / 4) % wq, wq, p.nch)) {
         atomicOr(p.err, kErrWait);
         return;
     }
@@ -547,6 +550,312 @@ __global__ __launch_bounds__(64 * WV, 2) void spread_kv_kernel(Params p)
     }
 }
 
+// ---- Head dim 512 ---------------------------------------------------------
+// The spread decode of short head-dim-512 launches (global layers: 16 query
+// and 2 KV heads, a few thousand keys, which give too few (chunk, unit, KV
+// head) items to fill the chip otherwise). An item's 16 slices are one wave
+// each (a one-wave workgroup): slice j forms the raw scores of the chunk's
+// key block j (its canonical chain over all 512 dims, 128 dependent MFMAs)
+// and owns output dims [32j, 32j + 32) (two 16-dim output blocks, two
+// independent P.V chains). K streams in four pieces of 128 dims, two in
+// flight, each with its Q^T piece (B operands from L2); V of the wave's
+// dims for the chunk's 256 keys goes straight to LDS (32 KiB), requested
+// once the last K piece is (requested behind the first two pieces instead,
+// the later pieces' waits also waited for V: 0.5 us slower at 2K and 4K
+// keys). The scores are published as (epoch, bits)
+// words and every slice gathers all 16 blocks, exactly as the head-dim-256
+// form does, so every kernel's bits follow.
+//
+// A one-dimensional grid deals item i (i = group * nch + chunk) to XCD
+// i % 8 (workgroup b = 8 (16 (i / 8) + j) + i % 8 for slice j): an item's
+// score words are stored plainly into its XCD's L2 and read there. Its
+// chunk partial goes out as device-coherent words to the merge workgroups
+// appended to the grid (one thread per four dims of a row), which may run
+// on any XCD.
+constexpr int kWideSlices = 16;  // one 32-dim slice per key block
+constexpr int kWidePieceU = 4;   // score chain steps (32 dims each) per K piece
+constexpr int kWidePieces = 512 / 32 / kWidePieceU;
+
+__host__ __device__ inline int spread_wide_item_wgs(const Params &p)
+{
+    const int items = p.nch * p.nkv * p.units;
+    return kWideSlices * 8 * ((items + 7) / 8);
+}
+
+template <bool FULL, bool CAP>
+__global__ __launch_bounds__(64) void spread_wide_kernel(Params p)
+{
+    constexpr int DK = 512;
+    const int b = (int)blockIdx.x;
+    const int item_wgs = spread_wide_item_wgs(p);
+    if (b >= item_wgs) { // an appended merge workgroup
+        spread_merge(p, (int64_t)(b - item_wgs) * 64 + threadIdx.x);
+        return;
+    }
+    const int item = 8 * ((b >> 3) / kWideSlices) + (b & 7);
+    const int slice = (b >> 3) % kWideSlices;
+    if (item >= p.nch * p.nkv * p.units)
+        return;
+    const int z = item / p.nch, ci = item % p.nch;
+
+    // V of the wave's 32 dims for the chunk's 256 keys, as the head-dim-256
+    // form lays out 16 dims: [16-dim half][block][slot][dim], slot j of a
+    // block holding key 4(j % 4) + j / 4
+    __shared__ float vlds[2][kBlocksPerChunk][16][16];
+    // the chunk's raw scores, [block][r][lane]
+    __shared__ float slds[kBlocksPerChunk][4][64];
+    const int c = p.c_lo + ci;
+    const int unit = z % p.units;
+    const int kvl = z / p.units;
+    const int lane = threadIdx.x & 63;
+    const int col = lane & 15;
+    const int g = lane >> 4;
+    const int kh = p.kh_first + kvl;
+    const int row = unit * kRows + col;
+    const bool rin = row < p.nrows;
+    const int64_t cbase = (int64_t)c * kChunk;
+    const int64_t klast = p.nkeys - 1;
+    const int64_t hoff = (int64_t)kh * p.dim;
+    uint64_t *words = p.ws_tag + (int64_t)item * (kBlocksPerChunk * 64 * 4);
+    const int d0 = kSpreadSliceDims * slice; // the wave's first output dim
+
+    {
+        const int query = rin ? row / p.group : 0;
+        const int h = kh * p.group + (rin ? row % p.group : 0);
+        const float *qp = p.q + (int64_t)query * p.q_stride + (int64_t)h * p.dim;
+        const int64_t key = cbase + 16 * slice + col;
+        const float *kp = key_row(p, key < klast ? key : klast) + hoff;
+        // piece pc in register slot s: K[key][32u + 8g + 4hh ..] and
+        // Q[row][32u + 8g + jj] * q_scale for u = 4pc + uu (a dim past the
+        // head's last reads dim 0 and becomes 0)
+        f4 kb[2][kWidePieceU][2];
+        f4 qr[2][kWidePieceU][2];
+        auto load_piece = [&](int pc, int sl) {
+#pragma unroll
+            for (int uu = 0; uu < kWidePieceU; ++uu)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int d = 32 * (kWidePieceU * pc + uu) + 8 * g + 4 * hh;
+                    const int dd = FULL || d < p.dim ? d : 0;
+                    kb[sl][uu][hh] = ldg4_stream(kp + dd);
+                    qr[sl][uu][hh] = ldg4(qp + dd);
+                }
+        };
+        load_piece(0, 0);
+        load_piece(1, 1);
+        // V: lane L of block i moves 16 bytes (dims d0 + 16 half + 4(L % 4)
+        // ..) of key 16i + 4(s % 4) + s / 4 into slot s = L / 4
+        auto load_v = [&]() {
+            const int sl = lane >> 2;
+            const int kin = 4 * (sl & 3) + (sl >> 2);
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const int dv = d0 + 16 * half + 4 * (lane & 3);
+                const int dd = FULL || dv < p.dim ? dv : 0;
+#pragma unroll
+                for (int i = 0; i < kBlocksPerChunk; ++i) {
+                    const int64_t vk = cbase + 16 * i + kin;
+                    const float *vp = value_row(p, vk < klast ? vk : klast) + hoff + dd;
+                    __builtin_amdgcn_global_load_lds((spread_gptr_t)vp,
+                                                     (spread_lptr_t)(&vlds[half][i][0][0]), 16,
+                                                     0, 0);
+                }
+            }
+        };
+        f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int pc = 0; pc < kWidePieces; ++pc) {
+            const int sl = pc & 1;
+#pragma unroll
+            for (int uu = 0; uu < kWidePieceU; ++uu) {
+                const int u = kWidePieceU * pc + uu;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int d = 32 * u + 8 * g + 4 * hh;
+                    const bool din = FULL || d < p.dim;
+                    const f4 x = qr[sl][uu][hh] * p.q_scale;
+                    const f4 qv = (rin && din) ? x : f4{0.f, 0.f, 0.f, 0.f};
+                    const f4 kv = din ? kb[sl][uu][hh] : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc = mfma(kv[j], qv[j], acc);
+                }
+            }
+            if (pc + 2 < kWidePieces)
+                load_piece(pc + 2, sl);
+            if (pc == kWidePieces - 3)
+                load_v(); // behind the last K piece
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            publish_to<true>(words + (slice * 4 + r) * 64 + lane, p.epoch, acc[r]);
+    }
+
+    // Every block's raw scores once its words carry this launch's epoch, in
+    // two halves of eight blocks (bounded; a block whose words have not all
+    // arrived when the wait runs out is formed here by the same chain).
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        constexpr int HB = kBlocksPerChunk / 2;
+        uint64_t x[HB][4];
+        bool gave_up = false;
+        for (int polls = 0;;) {
+            const uint64_t *base = words + (half * HB * 4) * 64 + lane;
+            asm volatile("" : "+v"(base));
+            bool fresh = true;
+#pragma unroll
+            for (int bb = 0; bb < HB; ++bb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    x[bb][r] = take(base + (bb * 4 + r) * 64);
+                    fresh &= (uint32_t)(x[bb][r] >> 32) == p.epoch;
+                }
+            if (__all(fresh))
+                break;
+            if (++polls >= p.max_polls) {
+                gave_up = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (gave_up) {
+#pragma unroll
+            for (int bb = 0; bb < HB; ++bb) {
+                bool got = true;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    got &= (uint32_t)(x[bb][r] >> 32) == p.epoch;
+                if (__all(got))
+                    continue;
+                const f4 acc = spread_block_scores<DK, FULL>(p, cbase + 16 * (half * HB + bb), kh,
+                                                             row, rin, col, g);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    x[bb][r] = (uint64_t)__float_as_uint(acc[r]);
+            }
+        }
+#pragma unroll
+        for (int bb = 0; bb < HB; ++bb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                slds[half * HB + bb][r][lane] = __uint_as_float((uint32_t)x[bb][r]);
+    }
+    // the V copies have landed (s_waitcnt covers LDS copies too); the
+    // scores are this wave's own LDS writes
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+
+    // Online softmax and the P.V chains of the wave's two 16-dim blocks.
+    float m = kNegInf, l = 0.f;
+    f4 O[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+    bool bad = false;
+    const ChunkKeys ck = chunk_keys(p, row, cbase);
+    auto tile_step = [&](int t, const bool ok[2][4], bool tile_any) {
+        float pr[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        float alpha, rs = 0.f;
+        if (tile_any) {
+            float sv[2][4];
+#pragma unroll
+            for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    sv[bb][r] = slds[2 * t + bb][r][lane];
+            cap_scores<CAP>(p, sv);
+            bad |= bad_scores(sv, ok);
+            const float mn = fmaxf(m, tile_max(sv, ok));
+            const float ms = safe_max(mn);
+            alpha = fexp(m - ms);
+            rs = tile_probs(sv, ok, ms, pr);
+            m = mn;
+        } else {
+            alpha = fexp(m - safe_max(m));
+        }
+        l = __builtin_fmaf(l, alpha, rs);
+        if (tile_any) {
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                O[half] = O[half] * alpha;
+#pragma unroll
+                for (int br = 0; br < 8; ++br) {
+                    // key 16b + 4g + r of block 2t + b sits in slot 4r + g
+                    const int bb = br >> 2, r = br & 3;
+                    O[half] = mfma(vlds[half][2 * t + bb][4 * r + g][col], pr[bb][r], O[half]);
+                }
+            }
+        }
+    };
+    if (!p.mask && __all(!rin || (ck.lo <= 0 && ck.hi >= kChunk - 1))) {
+        const bool ok[2][4] = {{true, true, true, true}, {true, true, true, true}};
+#pragma unroll
+        for (int t = 0; t < kTilesPerChunk; ++t)
+            tile_step(t, ok, true);
+    } else {
+#pragma unroll
+        for (int t = 0; t < kTilesPerChunk; ++t) {
+            bool ok[2][4];
+            const bool any = tile_keys(ck, t, g, ok);
+            tile_step(t, ok, __any(any));
+        }
+    }
+    if (bad && slice == 0)
+        atomicOr(p.err, kErrScore);
+
+    // O[half][i] is dim d0 + 16 half + 4g + i of row `row`.
+    if (!rin)
+        return;
+    if (p.ws_ptag == nullptr) { // the launch's only chunk: final output
+        const int query = row / p.group;
+        const int h = kh * p.group + row % p.group;
+        if (h < p.h_lo || h >= p.h_hi)
+            return;
+        float *o = p.out + (int64_t)query * p.o_stride + (int64_t)(h - p.h_base) * p.dim;
+        bool nonfinite = false;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int d = d0 + 16 * half + 4 * g;
+            if (!(FULL || d < p.dim))
+                continue;
+            f4 v;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[i] = O[half][i] / l;
+                nonfinite |= !is_finite(v[i]);
+            }
+            stg4(o + d, v);
+        }
+        if (nonfinite)
+            atomicOr(p.err, kErrOutput);
+        return;
+    }
+    // the chunk partial for the merge workgroups (on any XCD)
+    uint64_t *pw = partial_words(p, kvl, row, ci);
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        const int d = d0 + 16 * half + 4 * g;
+        if (!(FULL || d < p.dim))
+            continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            publish_to<false>(pw + d + i, p.epoch, O[half][i]);
+    }
+    if (slice == 0 && g == 0) {
+        publish_to<false>(pw + p.dk, p.epoch, m);
+        publish_to<false>(pw + p.dk + 1, p.epoch, l);
+    }
+}
+
+template <bool CAP>
+static hipError_t launch_wide(const Params &p, hipStream_t stream)
+{
+    int wgs = spread_wide_item_wgs(p);
+    if (p.ws_ptag)
+        wgs += (int)(((int64_t)p.nkv * p.nrows * (p.dim / 4) + 63) / 64);
+    if (p.dim == 512)
+        spread_wide_kernel<true, CAP><<<wgs, 64, 0, stream>>>(p);
+    else
+        spread_wide_kernel<false, CAP><<<wgs, 64, 0, stream>>>(p);
+    return hipGetLastError();
+}
+
 int device_cus();
 
 int spread_slices(int dk)
@@ -617,6 +926,8 @@ hipError_t launch_spread_kv(const Params &p, hipStream_t stream)
     case 64: return launch_dk<64>(p, stream);
     case 128: return launch_dk<128>(p, stream);
     case 256: return launch_dk<256>(p, stream);
+    case 512:
+        return p.softcap > 0.0f ? launch_wide<true>(p, stream) : launch_wide<false>(p, stream);
     default: return hipErrorInvalidValue;
     }
 }

@@ -91,10 +91,20 @@ def test_descriptor_validation_on_the_host(pcl):
     d.dim, d.q_stride, d.o_stride = 512, 16 * 512, 16 * 512
     # also at head dim 512 (two score waves, two value waves)
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
-    d.window = 1024  # five chunks per head: short, so at d512 the fanned kernel
+    d.window = 1024  # five chunks per head: short, so at d512 the spread form
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_SPREAD_KV
+    d.window = 200  # one chunk: spread as well (its slices write the output)
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_SPREAD_KV
+    d.window = 0  # 128 chunks x 8 KV heads: beyond the spread bound, pipelined
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
+    d.window = 8192  # 32 chunks x 8 KV heads: 256 items, beyond it, fanned
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_FAN_KV
-    d.window = 200  # one chunk at d512: the four-phase kernel
+    # one chunk of 64 KV heads at d512: 1024 slices, beyond it: four-phase
+    d.qheads, d.kvheads, d.kh_end, d.window = 64, 64, 64, 200
+    d.q_stride = d.o_stride = 64 * 512
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_SPLIT_KV
+    d.qheads, d.kvheads, d.kh_end = 16, 8, 8
+    d.q_stride = d.o_stride = 16 * 512
     d.window = 1024
     d.dim, d.q_stride, d.o_stride = 256, 16 * 256, 16 * 256
     # up to head dim 256 a short decode (4 chunks x 8 KV heads) spreads each
@@ -109,8 +119,8 @@ def test_descriptor_validation_on_the_host(pcl):
     d.kernel = pcl.KERNEL_PIPE_KV
     d.dim, d.q_stride, d.o_stride = 512, 16 * 512, 16 * 512
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
-    d.kernel = pcl.KERNEL_SPREAD_KV  # no spread form at head dim 512: pipelined
-    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV
+    d.kernel = pcl.KERNEL_SPREAD_KV  # the one-wave-slice spread form at d512
+    assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_SPREAD_KV
     d.dim, d.q_stride, d.o_stride, d.window = 256, 16 * 256, 16 * 256, 0
     # 128 chunks x 8 KV heads is beyond the spread bound: pipelined
     assert lib.pcl_attention_resolve_kernel(ctypes.byref(d)) == pcl.KERNEL_PIPE_KV

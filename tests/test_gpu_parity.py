@@ -564,6 +564,35 @@ def test_spread_waits_give_up_at_the_host_limit_and_keep_the_bits(pcl, torch, ct
         assert_parity(want[0], ref, dim)
 
 
+def test_wide_spread_waits_give_up_and_keep_the_bits(pcl, torch, ctx, oracle):
+    # the head-dim-512 spread decode under a one-poll wait limit: every
+    # slice forms the blocks whose words have not arrived itself, and the
+    # output keeps the pipelined kernel's bits (one chunk and several)
+    qheads, kvh, dim = 16, 2, 512
+    g = np.random.default_rng(512)
+    for nkeys in (2048, 200):
+        q = prescale(g.standard_normal((1, qheads * dim), dtype=np.float32), dim)
+        k = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+        v = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+        want, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, pcl.KERNEL_PIPE_KV, 1, 0, 0,
+                             nkeys - 1)
+        assert err == 0
+        other = pcl.Context(0, torch.cuda.current_stream().cuda_stream)
+        try:
+            other.set_wait_limit(1)
+            for _ in range(2):
+                got, err = run_desc(torch, other, q, k, v, qheads, kvh, dim,
+                                    pcl.KERNEL_SPREAD_KV, 1, 0, 0, nkeys - 1)
+                assert err == 0, (nkeys, err)
+                assert np.array_equal(bits(got), bits(want)), nkeys
+        finally:
+            other.close()
+        ok, ref = oracle.heads(q[0], k, v, qheads, kvh, dim, nkeys,
+                               oracle.encoder_mask(0, nkeys, nkeys - 1, None))
+        assert ok
+        assert_parity(want[0], ref, dim)
+
+
 def test_spread_epochs_across_a_counter_wrap(pcl, torch, ctx):
     # the device's epoch counter set just below a wrap of its low 32 bits:
     # the launches before and after the wrap (when the workspace's published
@@ -605,6 +634,14 @@ SPREAD_FORM_CASES = [
     # the local form (each (KV head, unit) group's workgroups on one XCD)
     # with two groups per XCD: 16 queries, two 16-row units per KV head
     (16, 8, 128, 16, 1000, 984),
+    # head dim 512: one-wave slices, 16 per item, items dealt to XCDs
+    (16, 2, 512, 1, 2048, 2047),  # 16 items, one slice per CU
+    (16, 2, 512, 1, 4096, 4095),  # 32 items, two per CU
+    (16, 2, 512, 1, 6000, 5999),  # 48 items (three per CU), ragged last chunk
+    (16, 2, 320, 1, 2000, 1999),  # a head dim below the padded 512
+    (16, 2, 512, 1, 200, 199),    # one chunk: the output straight from the slices
+    (16, 2, 512, 2, 1500, 1498),  # two queries of eight heads per KV head
+    (8, 1, 512, 3, 1000, 997),    # two 16-row units, one with padding rows
 ]
 
 
