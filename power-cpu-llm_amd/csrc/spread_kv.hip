@@ -572,36 +572,48 @@ __global__ __launch_bounds__(64 * WV, 2) void spread_kv_kernel(Params p)
 // chunk partial goes out as device-coherent words to the merge workgroups
 // appended to the grid (one thread per four dims of a row), which may run
 // on any XCD.
-constexpr int kWideSlices = 16;  // one 32-dim slice per key block
+int device_cus();
+
+constexpr int kWideSlices = 16;  // slices per item: one key block each
 constexpr int kWidePieceU = 4;   // score chain steps (32 dims each) per K piece
 constexpr int kWidePieces = 512 / 32 / kWidePieceU;
 
-__host__ __device__ inline int spread_wide_item_wgs(const Params &p)
+// Item workgroups of a launch of SL slices per item (a whole number of
+// eights of items, so that item i's slices all sit on XCD i % 8).
+template <int SL> __host__ __device__ inline int spread_wide_item_wgs(const Params &p)
 {
     const int items = p.nch * p.nkv * p.units;
-    return kWideSlices * 8 * ((items + 7) / 8);
+    return SL * 8 * ((items + 7) / 8);
 }
 
-template <bool FULL, bool CAP>
+// SL slices per item (kWideSlices: one key block and 32 output dims per
+// slice). Eight slices of two blocks each (their chains interleaved, 64
+// dims, 80 KiB of LDS, two per CU), for launches of up to 64 items, were
+// slower than the fanned kernel at 8K keys (43.3 against 36.2 us) and than
+// sixteen slices at 2K-6K (31.3 against 21.0 us at 2K), so only sixteen run.
+template <bool FULL, bool CAP, int SL>
 __global__ __launch_bounds__(64) void spread_wide_kernel(Params p)
 {
     constexpr int DK = 512;
+    constexpr int BPW = kBlocksPerChunk / SL; // score blocks of a slice
+    constexpr int VD = DK / SL;               // output dims of a slice
+    constexpr int NH = VD / 16;               // its 16-dim output blocks
     const int b = (int)blockIdx.x;
-    const int item_wgs = spread_wide_item_wgs(p);
+    const int item_wgs = spread_wide_item_wgs<SL>(p);
     if (b >= item_wgs) { // an appended merge workgroup
         spread_merge(p, (int64_t)(b - item_wgs) * 64 + threadIdx.x);
         return;
     }
-    const int item = 8 * ((b >> 3) / kWideSlices) + (b & 7);
-    const int slice = (b >> 3) % kWideSlices;
+    const int item = 8 * ((b >> 3) / SL) + (b & 7);
+    const int slice = (b >> 3) % SL;
     if (item >= p.nch * p.nkv * p.units)
         return;
     const int z = item / p.nch, ci = item % p.nch;
 
-    // V of the wave's 32 dims for the chunk's 256 keys, as the head-dim-256
-    // form lays out 16 dims: [16-dim half][block][slot][dim], slot j of a
-    // block holding key 4(j % 4) + j / 4
-    __shared__ float vlds[2][kBlocksPerChunk][16][16];
+    // V of the wave's dims for the chunk's 256 keys, as the head-dim-256
+    // form lays out 16 dims: [16-dim block][key block][slot][dim], slot j of
+    // a key block holding key 4(j % 4) + j / 4
+    __shared__ float vlds[NH][kBlocksPerChunk][16][16];
     // the chunk's raw scores, [block][r][lane]
     __shared__ float slds[kBlocksPerChunk][4][64];
     const int c = p.c_lo + ci;
@@ -617,18 +629,22 @@ __global__ __launch_bounds__(64) void spread_wide_kernel(Params p)
     const int64_t klast = p.nkeys - 1;
     const int64_t hoff = (int64_t)kh * p.dim;
     uint64_t *words = p.ws_tag + (int64_t)item * (kBlocksPerChunk * 64 * 4);
-    const int d0 = kSpreadSliceDims * slice; // the wave's first output dim
+    const int d0 = VD * slice; // the wave's first output dim
 
     {
         const int query = rin ? row / p.group : 0;
         const int h = kh * p.group + (rin ? row % p.group : 0);
         const float *qp = p.q + (int64_t)query * p.q_stride + (int64_t)h * p.dim;
-        const int64_t key = cbase + 16 * slice + col;
-        const float *kp = key_row(p, key < klast ? key : klast) + hoff;
-        // piece pc in register slot s: K[key][32u + 8g + 4hh ..] and
-        // Q[row][32u + 8g + jj] * q_scale for u = 4pc + uu (a dim past the
-        // head's last reads dim 0 and becomes 0)
-        f4 kb[2][kWidePieceU][2];
+        const float *kp[BPW];
+#pragma unroll
+        for (int i = 0; i < BPW; ++i) {
+            const int64_t key = cbase + 16 * (BPW * slice + i) + col;
+            kp[i] = key_row(p, key < klast ? key : klast) + hoff;
+        }
+        // piece pc in register slot s: K[key][32u + 8g + 4hh ..] of each of
+        // the slice's blocks and Q[row][32u + 8g + jj] * q_scale for u =
+        // 4pc + uu (a dim past the head's last reads dim 0 and becomes 0)
+        f4 kb[2][BPW][kWidePieceU][2];
         f4 qr[2][kWidePieceU][2];
         auto load_piece = [&](int pc, int sl) {
 #pragma unroll
@@ -637,32 +653,37 @@ __global__ __launch_bounds__(64) void spread_wide_kernel(Params p)
                 for (int hh = 0; hh < 2; ++hh) {
                     const int d = 32 * (kWidePieceU * pc + uu) + 8 * g + 4 * hh;
                     const int dd = FULL || d < p.dim ? d : 0;
-                    kb[sl][uu][hh] = ldg4_stream(kp + dd);
+#pragma unroll
+                    for (int i = 0; i < BPW; ++i)
+                        kb[sl][i][uu][hh] = ldg4_stream(kp[i] + dd);
                     qr[sl][uu][hh] = ldg4(qp + dd);
                 }
         };
         load_piece(0, 0);
         load_piece(1, 1);
-        // V: lane L of block i moves 16 bytes (dims d0 + 16 half + 4(L % 4)
+        // V: lane L of key block i moves 16 bytes (dims d0 + 16 n + 4(L % 4)
         // ..) of key 16i + 4(s % 4) + s / 4 into slot s = L / 4
         auto load_v = [&]() {
             const int sl = lane >> 2;
             const int kin = 4 * (sl & 3) + (sl >> 2);
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                const int dv = d0 + 16 * half + 4 * (lane & 3);
+            for (int n = 0; n < NH; ++n) {
+                const int dv = d0 + 16 * n + 4 * (lane & 3);
                 const int dd = FULL || dv < p.dim ? dv : 0;
 #pragma unroll
                 for (int i = 0; i < kBlocksPerChunk; ++i) {
                     const int64_t vk = cbase + 16 * i + kin;
                     const float *vp = value_row(p, vk < klast ? vk : klast) + hoff + dd;
                     __builtin_amdgcn_global_load_lds((spread_gptr_t)vp,
-                                                     (spread_lptr_t)(&vlds[half][i][0][0]), 16,
+                                                     (spread_lptr_t)(&vlds[n][i][0][0]), 16,
                                                      0, 0);
                 }
             }
         };
-        f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+        f4 acc[BPW];
+#pragma unroll
+        for (int i = 0; i < BPW; ++i)
+            acc[i] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int pc = 0; pc < kWidePieces; ++pc) {
             const int sl = pc & 1;
@@ -675,10 +696,13 @@ __global__ __launch_bounds__(64) void spread_wide_kernel(Params p)
                     const bool din = FULL || d < p.dim;
                     const f4 x = qr[sl][uu][hh] * p.q_scale;
                     const f4 qv = (rin && din) ? x : f4{0.f, 0.f, 0.f, 0.f};
-                    const f4 kv = din ? kb[sl][uu][hh] : f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
-                        acc = mfma(kv[j], qv[j], acc);
+#pragma unroll
+                        for (int i = 0; i < BPW; ++i) {
+                            const float kv = din ? kb[sl][i][uu][hh][j] : 0.f;
+                            acc[i] = mfma(kv, qv[j], acc[i]);
+                        }
                 }
             }
             if (pc + 2 < kWidePieces)
@@ -687,8 +711,11 @@ __global__ __launch_bounds__(64) void spread_wide_kernel(Params p)
                 load_v(); // behind the last K piece
         }
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            publish_to<true>(words + (slice * 4 + r) * 64 + lane, p.epoch, acc[r]);
+        for (int i = 0; i < BPW; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                publish_to<true>(words + ((BPW * slice + i) * 4 + r) * 64 + lane, p.epoch,
+                                 acc[i][r]);
     }
 
     // Every block's raw scores once its words carry this launch's epoch, in
@@ -746,7 +773,10 @@ __global__ __launch_bounds__(64) void spread_wide_kernel(Params p)
 
     // Online softmax and the P.V chains of the wave's two 16-dim blocks.
     float m = kNegInf, l = 0.f;
-    f4 O[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+    f4 O[NH];
+#pragma unroll
+    for (int n = 0; n < NH; ++n)
+        O[n] = f4{0.f, 0.f, 0.f, 0.f};
     bool bad = false;
     const ChunkKeys ck = chunk_keys(p, row, cbase);
     auto tile_step = [&](int t, const bool ok[2][4], bool tile_any) {
@@ -772,14 +802,15 @@ __global__ __launch_bounds__(64) void spread_wide_kernel(Params p)
         l = __builtin_fmaf(l, alpha, rs);
         if (tile_any) {
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                O[half] = O[half] * alpha;
+            for (int n = 0; n < NH; ++n)
+                O[n] = O[n] * alpha;
 #pragma unroll
-                for (int br = 0; br < 8; ++br) {
-                    // key 16b + 4g + r of block 2t + b sits in slot 4r + g
-                    const int bb = br >> 2, r = br & 3;
-                    O[half] = mfma(vlds[half][2 * t + bb][4 * r + g][col], pr[bb][r], O[half]);
-                }
+            for (int br = 0; br < 8; ++br) {
+                // key 16b + 4g + r of block 2t + b sits in slot 4r + g
+                const int bb = br >> 2, r = br & 3;
+#pragma unroll
+                for (int n = 0; n < NH; ++n)
+                    O[n] = mfma(vlds[n][2 * t + bb][4 * r + g][col], pr[bb][r], O[n]);
             }
         }
     };
@@ -799,7 +830,7 @@ __global__ __launch_bounds__(64) void spread_wide_kernel(Params p)
     if (bad && slice == 0)
         atomicOr(p.err, kErrScore);
 
-    // O[half][i] is dim d0 + 16 half + 4g + i of row `row`.
+    // O[n][i] is dim d0 + 16n + 4g + i of row `row`.
     if (!rin)
         return;
     if (p.ws_ptag == nullptr) { // the launch's only chunk: final output
@@ -810,14 +841,14 @@ __global__ __launch_bounds__(64) void spread_wide_kernel(Params p)
         float *o = p.out + (int64_t)query * p.o_stride + (int64_t)(h - p.h_base) * p.dim;
         bool nonfinite = false;
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const int d = d0 + 16 * half + 4 * g;
+        for (int n = 0; n < NH; ++n) {
+            const int d = d0 + 16 * n + 4 * g;
             if (!(FULL || d < p.dim))
                 continue;
             f4 v;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                v[i] = O[half][i] / l;
+                v[i] = O[n][i] / l;
                 nonfinite |= !is_finite(v[i]);
             }
             stg4(o + d, v);
@@ -829,13 +860,13 @@ __global__ __launch_bounds__(64) void spread_wide_kernel(Params p)
     // the chunk partial for the merge workgroups (on any XCD)
     uint64_t *pw = partial_words(p, kvl, row, ci);
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-        const int d = d0 + 16 * half + 4 * g;
+    for (int n = 0; n < NH; ++n) {
+        const int d = d0 + 16 * n + 4 * g;
         if (!(FULL || d < p.dim))
             continue;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            publish_to<false>(pw + d + i, p.epoch, O[half][i]);
+            publish_to<false>(pw + d + i, p.epoch, O[n][i]);
     }
     if (slice == 0 && g == 0) {
         publish_to<false>(pw + p.dk, p.epoch, m);
@@ -843,20 +874,24 @@ __global__ __launch_bounds__(64) void spread_wide_kernel(Params p)
     }
 }
 
-template <bool CAP>
-static hipError_t launch_wide(const Params &p, hipStream_t stream)
+template <bool CAP, int SL>
+static void launch_wide_sl(const Params &p, hipStream_t stream)
 {
-    int wgs = spread_wide_item_wgs(p);
+    int wgs = spread_wide_item_wgs<SL>(p);
     if (p.ws_ptag)
         wgs += (int)(((int64_t)p.nkv * p.nrows * (p.dim / 4) + 63) / 64);
     if (p.dim == 512)
-        spread_wide_kernel<true, CAP><<<wgs, 64, 0, stream>>>(p);
+        spread_wide_kernel<true, CAP, SL><<<wgs, 64, 0, stream>>>(p);
     else
-        spread_wide_kernel<false, CAP><<<wgs, 64, 0, stream>>>(p);
-    return hipGetLastError();
+        spread_wide_kernel<false, CAP, SL><<<wgs, 64, 0, stream>>>(p);
 }
 
-int device_cus();
+template <bool CAP>
+static hipError_t launch_wide(const Params &p, hipStream_t stream)
+{
+    launch_wide_sl<CAP, kWideSlices>(p, stream);
+    return hipGetLastError();
+}
 
 int spread_slices(int dk)
 {

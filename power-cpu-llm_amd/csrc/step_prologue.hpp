@@ -20,8 +20,11 @@ namespace pcl {
 // The norm's inverse for a row of D floats in LDS (16-byte aligned), by the
 // calling lane: the sum runs in order while the next 16 values' reads are in
 // flight, so the chain of D dependent f64 adds is the time, not D LDS round
-// trips.
-template <int D>
+// trips. Fully unrolled (the head-transform kernel; 3 us faster over a
+// 4K-token prompt) the compiler hoists every read of the row into registers;
+// COMPACT (a decode kernel's prologue, whose registers are spoken for) keeps
+// two batches per iteration.
+template <int D, bool COMPACT = false>
 __device__ __forceinline__ double norm_inverse(const float *row, float eps)
 {
     constexpr int B = D < 16 ? D : 16; // floats per batch
@@ -31,26 +34,47 @@ __device__ __forceinline__ double norm_inverse(const float *row, float eps)
     for (int i = 0; i < B / 4; ++i)
         cur[i] = *(const f4 *)(row + 4 * i);
     double sum = 0.0;
-    // two batches per iteration (fully unrolled, the compiler would hoist
-    // every read of the row and hold it in registers)
+    if constexpr (COMPACT) {
 #pragma unroll 2
-    for (int b = 0; b < D; b += B) {
-        if (b + B < D) {
+        for (int b = 0; b < D; b += B) {
+            if (b + B < D) {
 #pragma unroll
-            for (int i = 0; i < B / 4; ++i)
-                nxt[i] = *(const f4 *)(row + b + B + 4 * i);
-        }
-#pragma unroll
-        for (int i = 0; i < B / 4; ++i)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const double v = (double)cur[i][e];
-                sum = sum + v * v;
+                for (int i = 0; i < B / 4; ++i)
+                    nxt[i] = *(const f4 *)(row + b + B + 4 * i);
             }
-        if (b + B < D) {
 #pragma unroll
             for (int i = 0; i < B / 4; ++i)
-                cur[i] = nxt[i];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const double v = (double)cur[i][e];
+                    sum = sum + v * v;
+                }
+            if (b + B < D) {
+#pragma unroll
+                for (int i = 0; i < B / 4; ++i)
+                    cur[i] = nxt[i];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int b = 0; b < D; b += B) {
+            if (b + B < D) {
+#pragma unroll
+                for (int i = 0; i < B / 4; ++i)
+                    nxt[i] = *(const f4 *)(row + b + B + 4 * i);
+            }
+#pragma unroll
+            for (int i = 0; i < B / 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const double v = (double)cur[i][e];
+                    sum = sum + v * v;
+                }
+            if (b + B < D) {
+#pragma unroll
+                for (int i = 0; i < B / 4; ++i)
+                    cur[i] = nxt[i];
+            }
         }
     }
     return 1.0 / __builtin_sqrt(sum / (double)D + (double)eps);
@@ -136,7 +160,7 @@ __device__ __forceinline__ bool step_kv_row(const Params &p, int kh, float *buf)
     wave_lds_sync();
     double inv = 0.0;
     if (lane == 0)
-        inv = norm_inverse<D>(buf, p.seps);
+        inv = norm_inverse<D, true>(buf, p.seps);
     inv = __shfl(inv, 0);
 #pragma unroll
     for (int m = 0; m < PAIRS; ++m) {
@@ -233,7 +257,7 @@ template <int D> struct StepQueryRows {
         wave_lds_sync();
         double inv = 0.0;
         if (lane < nr)
-            inv = norm_inverse<D>(qb + lane * ld, p.seps);
+            inv = norm_inverse<D, true>(qb + lane * ld, p.seps);
         for (int r = 0; r < nr; ++r) {
             const double iv = __shfl(inv, r);
             float *row = qb + r * ld;
