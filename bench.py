@@ -80,6 +80,9 @@ WORKLOADS = {
     # transform inside the pipelined decode's launch)
     "transform_4k": (16, 8, 256, 4096, 0, True, 0, 0, "transform", False),
     "decode_32k_step": (16, 8, 256, 1, 32768, True, 0, 32767, "step", False),
+    # the same step for a sliding-window layer (window 1024 over a 32K
+    # prompt: the spread decode)
+    "decode_window_step": (16, 8, 256, 1, 32768, True, 1024, 32767, "step", False),
     # the whole attention layer of one decode token on the device: the step
     # above, then the output block on its attended row (LAYER_HIDDEN wide)
     "decode_32k_layer": (16, 8, 256, 1, 32768, True, 0, 32767, "layer", False),
