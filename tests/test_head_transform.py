@@ -481,3 +481,43 @@ def test_attend_token_folds_the_transform_into_the_decode(pcl, torch, ctx, oracl
     cache.rollback(pending)
     cache.close()
     t.close()
+
+
+@pytest.mark.gpu
+def test_attend_token_rejects_bad_arguments_and_leaves_the_cache(pcl, torch, ctx):
+    # the fused entry's errors are append_transformed's and the launch's; a
+    # refused call launches nothing and leaves the cache's counts unchanged
+    qh, kvh, dim = 8, 2, 128
+    ones = np.ones(dim, np.float32)
+    t = pcl.HeadTransform(ctx, qh, kvh, dim, ones, ones, 1e-6, 1e4, sliding=True)
+    other = pcl.HeadTransform(ctx, qh, kvh, 64, ones[:64], ones[:64], 1e-6, 1e4)
+    cache = pcl.LayerCache(ctx, kvh, dim, 100, None, 1 << 30)
+    rq = torch.ones(qh * dim, device="cuda:0")
+    rk = torch.ones(kvh * dim, device="cuda:0")
+    q_out = torch.empty(qh * dim, device="cuda:0")
+    out = torch.empty(qh * dim, device="cuda:0")
+    cases = [
+        (other, rk, rk, q_out, out, 0, "InvalidShape"),  # transform of another head dim
+        (t, rk, None, q_out, out, 0, "InvalidShape"),    # a sliding layer needs V
+        (t, rk, rk, None, out, 0, "InvalidShape"),       # no query output
+        (t, rk, rk, q_out, None, 0, "InvalidShape"),     # no attention output
+        (t, rk, rk, q_out, out, 5, "InvalidParameter"),  # the retired kernel choice
+    ]
+    for tr, k_, v_, qo, o, kernel, kind in cases:
+        with pytest.raises(pcl.AttentionError) as e:
+            cache.attend_token(tr, rq.data_ptr(), k_.data_ptr(), v_.data_ptr() if v_ is not None
+                               else 0, qo.data_ptr() if qo is not None else 0,
+                               o.data_ptr() if o is not None else 0, kernel=kernel)
+        assert e.value.kind == kind
+        assert cache.total_tokens() == 0 and cache.retained_tokens() == 0
+    assert ctx.sync() == 0
+    # a good call then counts its token
+    pending = cache.attend_token(t, rq.data_ptr(), rk.data_ptr(), rk.data_ptr(),
+                                 q_out.data_ptr(), out.data_ptr())
+    assert ctx.sync() == 0
+    assert cache.total_tokens() == 1 and cache.retained_tokens() == 1
+    cache.rollback(pending)
+    assert cache.total_tokens() == 0
+    cache.close()
+    other.close()
+    t.close()
