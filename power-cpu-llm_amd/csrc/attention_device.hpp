@@ -519,38 +519,42 @@ __device__ __forceinline__ bool wait_partials(const Params &p, int64_t slot0, in
 }
 
 // One batch of a span's ordered chunk merge from published words: chunks
-// c0 + b0 + i (i < B; those at or past c1 merge as empty parts,
-// with no loads) of row slot0, four dims from d, merged into s in ascending
-// order. Every word is re-checked (and the batch reloaded until all carry
-// the epoch). False when the wait gave up.
+// c0 + b0 + i (i < B; those at or past c1 are neither loaded nor merged) of
+// row slot0, four dims from d, merged into s in ascending order (c0, b0 and
+// c1 must be the same for every lane of the wave). Every word is re-checked
+// (and the batch reloaded until all carry the epoch). False when the wait
+// gave up.
 template <int B = kMergeBatch, int SLEEP = 2>
 __device__ __forceinline__ bool merge_words_batch(const Params &p, int64_t slot0, int c0,
                                                   int b0, int c1, int d, Merged4 &s)
 {
     const int stride = p.dk + 2;
-    float mv[B], lv[B];
-    f4 ov[B];
+    const int n = c1 - (c0 + b0); // chunks of the batch that exist (uniform)
+    uint64_t wm[B], wl[B], wo[B][4];
     bool ok = true;
-    for (int polls = 0; c0 + b0 < c1; ++polls) {
+    for (int polls = 0; n > 0; ++polls) {
+        // every present chunk's words requested back to back (the checks
+        // below, outside these uniform branches, wait for them together)
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            if (i >= n)
+                continue;
+            const uint64_t *w = p.ws_ptag + (slot0 + c0 + b0 + i) * stride;
+            wm[i] = take(w + p.dk);
+            wl[i] = take(w + p.dk + 1);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                wo[i][j] = take(w + d + j);
+        }
         bool fresh = true;
 #pragma unroll
         for (int i = 0; i < B; ++i) {
-            const int cc = c0 + b0 + i;
-            const uint64_t *w = p.ws_ptag + (slot0 + (cc < c1 ? cc : c0)) * stride;
-            const uint64_t wm = take(w + p.dk), wl = take(w + p.dk + 1);
-            uint64_t wo[4];
+            if (i >= n)
+                continue;
+            fresh &= (uint32_t)(wm[i] >> 32) == p.epoch && (uint32_t)(wl[i] >> 32) == p.epoch;
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                wo[j] = take(w + d + j);
-            bool got = (uint32_t)(wm >> 32) == p.epoch && (uint32_t)(wl >> 32) == p.epoch;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                got &= (uint32_t)(wo[j] >> 32) == p.epoch;
-                ov[i][j] = __uint_as_float((uint32_t)wo[j]);
-            }
-            mv[i] = __uint_as_float((uint32_t)wm);
-            lv[i] = __uint_as_float((uint32_t)wl);
-            fresh &= got || cc >= c1;
+                fresh &= (uint32_t)(wo[i][j] >> 32) == p.epoch;
         }
         if (__all(fresh))
             break;
@@ -560,12 +564,17 @@ __device__ __forceinline__ bool merge_words_batch(const Params &p, int64_t slot0
         }
         __builtin_amdgcn_s_sleep(SLEEP);
     }
+    // absent chunks would merge as empty parts, which leave the state
+    // bit-unchanged; skipping them takes their dependent merges off the chain
 #pragma unroll
     for (int i = 0; i < B; ++i) {
-        // chunks past the span merge as empty parts (no-ops)
-        const bool in = c0 + b0 + i < c1;
-        merge_into4(s, in ? mv[i] : kNegInf, in ? lv[i] : 0.f,
-                    in ? ov[i] : f4{0.f, 0.f, 0.f, 0.f});
+        if (i >= n)
+            continue;
+        f4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            o[j] = __uint_as_float((uint32_t)wo[i][j]);
+        merge_into4(s, __uint_as_float((uint32_t)wm[i]), __uint_as_float((uint32_t)wl[i]), o);
     }
     return ok;
 }

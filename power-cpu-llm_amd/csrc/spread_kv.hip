@@ -89,8 +89,13 @@ __device__ __forceinline__ void spread_merge_row(const Params &p, int kvl, int r
         const int c0 = max(span * kSpanChunks, p.c_lo) - p.c_lo;
         const int c1 = min((span + 1) * kSpanChunks, p.c_lo + p.nch) - p.c_lo;
         Merged4 sm = {kNegInf, 0.f, f4{0.f, 0.f, 0.f, 0.f}};
-        for (int b0 = 0; b0 < kSpanChunks; b0 += kMergeBatch)
-            ok &= merge_words_batch<kMergeBatch, LOCAL ? 1 : 2>(p, slot0, c0, b0, c1, d, sm);
+        // (batches of absent chunks only are not run; four or fewer
+        // chunks left take a batch of four)
+        for (int b0 = 0; b0 < kSpanChunks && c0 + b0 < c1; b0 += kMergeBatch)
+            ok &= c1 - (c0 + b0) <= kMergeBatch / 2
+                      ? merge_words_batch<kMergeBatch / 2, LOCAL ? 1 : 2>(p, slot0, c0, b0, c1,
+                                                                          d, sm)
+                      : merge_words_batch<kMergeBatch, LOCAL ? 1 : 2>(p, slot0, c0, b0, c1, d, sm);
         merge_into4(tot, sm.M, sm.L, sm.acc);
     }
     if (!ok) {
