@@ -227,11 +227,13 @@ __device__ __forceinline__ bool allowed(const Params &p, int row, int64_t t)
 struct RowKeys {
     int64_t lo, hi; // keys t with lo <= t <= hi pass the range
     gu8_cptr mask;  // the row's mask bytes, or null
+    bool masked;    // whether the launch has a mask (the same for every lane)
 };
 
 struct ChunkKeys {
     int lo, hi;    // chunk-relative keys k with lo <= k <= hi pass the range
     gu8_cptr mask; // the row's mask byte of the chunk's first key, or null
+    bool masked;   // whether the launch has a mask (the same for every lane)
 };
 
 __device__ __forceinline__ RowKeys row_keys(const Params &p, int row)
@@ -249,6 +251,7 @@ __device__ __forceinline__ RowKeys row_keys(const Params &p, int row)
             r.lo = rel - p.window + 1;
     }
     r.mask = p.mask ? (gu8_cptr)p.mask + (int64_t)query * p.mask_stride : nullptr;
+    r.masked = p.mask != nullptr;
     return r;
 }
 
@@ -260,6 +263,7 @@ __device__ __forceinline__ ChunkKeys chunk_of(const RowKeys &r, int64_t base)
     c.lo = (int)(lo < 0 ? 0 : lo > kChunk ? kChunk : lo);
     c.hi = (int)(hi < -1 ? -1 : hi > kChunk - 1 ? kChunk - 1 : hi);
     c.mask = r.mask ? r.mask + base : nullptr;
+    c.masked = r.masked;
     return c;
 }
 
@@ -271,19 +275,24 @@ __device__ __forceinline__ ChunkKeys chunk_keys(const Params &p, int row, int64_
 // Allowed flags of keys k0 + 4g + r (r = 0..3) of a chunk; true when any is.
 __device__ __forceinline__ bool block_keys(const ChunkKeys &c, int k0, int g, bool ok[4])
 {
-    bool any = false;
-    uint8_t m[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int k = k0 + 4 * g + r;
         ok[r] = k >= c.lo && k <= c.hi;
-        m[r] = c.mask && ok[r] ? c.mask[k] : (uint8_t)1;
     }
+    if (c.masked) {
+        uint8_t m[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        ok[r] = ok[r] && m[r] != 0;
-        any |= ok[r];
+        for (int r = 0; r < 4; ++r)
+            m[r] = ok[r] ? c.mask[k0 + 4 * g + r] : (uint8_t)1;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            ok[r] = ok[r] && m[r] != 0;
     }
+    bool any = false;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        any |= ok[r];
     return any;
 }
 
