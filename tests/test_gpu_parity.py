@@ -664,6 +664,48 @@ def test_spread_forms_match_the_pipelined_kernel_and_the_oracle(pcl, torch, ctx,
         assert_parity(got[i], want, dim)
 
 
+SPREAD_WINDOW_CASES = [
+    # qheads, kvh, dim, nq, nkeys, window: the query is the last key. A
+    # sliding layer's steady state: the window starts and ends inside chunks
+    # (and inside tiles), so partial chunks mix whole tiles, partial tiles
+    # and tiles with no allowed key
+    (16, 8, 256, 1, 32668, 1024),  # five chunks, both ends partial
+    (16, 8, 256, 1, 32668, 600),   # three chunks
+    (16, 8, 256, 1, 4100, 1000),   # window start 3100: mid-tile
+    (16, 8, 256, 1, 4096, 1024),   # aligned: four whole chunks
+    (16, 8, 256, 1, 3000, 33),     # one partial chunk after another's last key
+    (16, 8, 128, 2, 2000, 700),    # two queries: rows of one unit see different ranges
+    (16, 2, 512, 1, 5000, 1500),   # head dim 512
+    (16, 2, 512, 1, 2077, 300),
+]
+
+
+@pytest.mark.parametrize("case", SPREAD_WINDOW_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_spread_windows_inside_chunks_match_the_pipelined_kernel_and_the_oracle(
+        pcl, torch, ctx, oracle, case):
+    qheads, kvh, dim, nq, nkeys, window = case
+    fq = nkeys - nq
+    g = np.random.default_rng(sum(case))
+    q = prescale(g.standard_normal((nq, qheads * dim), dtype=np.float32), dim)
+    k = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+    v = g.standard_normal((nkeys, kvh, dim), dtype=np.float32)
+    got, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, pcl.KERNEL_SPREAD_KV, 1, window,
+                        0, fq)
+    assert err == 0
+    ref, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, pcl.KERNEL_PIPE_KV, 1, window,
+                        0, fq)
+    assert err == 0
+    assert np.array_equal(bits(got), bits(ref))
+    auto, err = run_desc(torch, ctx, q, k, v, qheads, kvh, dim, pcl.KERNEL_AUTO, 1, window, 0, fq)
+    assert err == 0
+    assert np.array_equal(bits(auto), bits(ref))
+    for i in range(nq):
+        ok, want = oracle.heads(q[i], k, v, qheads, kvh, dim, nkeys,
+                                oracle.encoder_mask(0, nkeys, fq + i, window))
+        assert ok
+        assert_parity(got[i], want, dim)
+
+
 def test_split_launch_tail_with_masks_segments_and_kv_ranges(torch, ctx, oracle):
     # the canvas shape (4 row blocks x 8 KV heads x 9 chunks = 288 items on
     # 256 CUs) leaves one chunk's items for a last round, which runs as
