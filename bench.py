@@ -46,6 +46,10 @@ def load_package():
 WORKLOADS = {
     "decode_2k": (16, 8, 256, 1, 2048, True, 0, 2047, "decode", False),
     "decode_32k_window1024": (16, 8, 256, 1, 32768, True, 1024, 32767, "decode", False),
+    # the sliding layer at a position that is not the last of a 256-key
+    # chunk (255 positions of every 256): its 1024-key window starts and ends
+    # inside chunks and covers five of them
+    "decode_window1024_unaligned": (16, 8, 256, 1, 32668, True, 1024, 32667, "decode", False),
     "decode_32k": (16, 8, 256, 1, 32768, True, 0, 32767, "decode", False),
     "decode_128k_d512": (16, 2, 512, 1, 131072, True, 0, 131071, "decode", True),
     # the same global-layer decode (16/2/512, unit-norm K) at shorter caches
