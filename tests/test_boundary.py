@@ -215,11 +215,14 @@ def _resource_remarks(source):
 @pytest.mark.parametrize("source,kernel", [
     ("tiled.hip", "_ZN3pcl12tiled_kernelILi256ELi8ELb0EEEvNS_6ParamsEii"),
     ("tiled_wide.hip", "_ZN3pcl17tiled_wide_kernelILb0EEEvNS_6ParamsEii"),
-    ("spread_kv.hip", "_ZN3pcl16spread_kv_kernelILi256ELb1ELb0ELb0ELi2ELb0EEEvNS_6ParamsE"),
-    ("spread_kv.hip", "_ZN3pcl16spread_kv_kernelILi256ELb1ELb0ELb1ELi2ELb0EEEvNS_6ParamsE"),
-    ("spread_kv.hip", "_ZN3pcl16spread_kv_kernelILi256ELb1ELb0ELb1ELi4ELb0EEEvNS_6ParamsE"),
-    ("spread_kv.hip", "_ZN3pcl16spread_kv_kernelILi256ELb1ELb0ELb1ELi2ELb1EEEvNS_6ParamsE"),
-    ("spread_kv.hip", "_ZN3pcl16spread_kv_kernelILi256ELb1ELb0ELb1ELi4ELb1EEEvNS_6ParamsE"),
+    ("spread_kv.hip", "_ZN3pcl16spread_kv_kernelILi256ELb1ELb0ELb0ELi2ELb0ELb0EEEvNS_6ParamsE"),
+    ("spread_kv.hip", "_ZN3pcl16spread_kv_kernelILi256ELb1ELb0ELb1ELi2ELb0ELb0EEEvNS_6ParamsE"),
+    ("spread_kv.hip", "_ZN3pcl16spread_kv_kernelILi256ELb1ELb0ELb1ELi4ELb0ELb0EEEvNS_6ParamsE"),
+    ("spread_kv.hip", "_ZN3pcl16spread_kv_kernelILi256ELb1ELb0ELb1ELi2ELb1ELb0EEEvNS_6ParamsE"),
+    ("spread_kv.hip", "_ZN3pcl16spread_kv_kernelILi256ELb1ELb0ELb1ELi4ELb1ELb0EEEvNS_6ParamsE"),
+    # whole-chunk launches (no per-key path)
+    ("spread_kv.hip", "_ZN3pcl16spread_kv_kernelILi256ELb1ELb0ELb1ELi2ELb1ELb1EEEvNS_6ParamsE"),
+    ("spread_kv.hip", "_ZN3pcl16spread_kv_kernelILi256ELb1ELb0ELb1ELi4ELb1ELb1EEEvNS_6ParamsE"),
     ("pipe_kv.hip", "_ZN3pcl14pipe_kv_kernelILi256ELi1ELb1ELb0ELb0EEEvNS_6ParamsEi"),
     ("pipe_kv.hip", "_ZN3pcl14pipe_kv_kernelILi512ELi1ELb1ELb1ELb0EEEvNS_6ParamsEi"),
     # the same with a one-token step's head transform folded in
