@@ -14,6 +14,10 @@
 //     weights: one wave per output row streams the row once with 16-byte
 //     loads, 4096 columns in flight at a time, and keeps one f64 accumulator
 //     per token per lane; the tokens' inputs come from L2.
+//   project_row_lds_kernel: one token (decode), input rows up to 16384
+//     wide: as project_rows_kernel<1>, with the input row staged once per
+//     workgroup in LDS (requested ahead of the weights) instead of read from
+//     L2 by every wave.
 //   project_tiles_kernel: many tokens (prompt). MFMA-bound: 128 x 128 output
 //     tiles, 32-column K steps double-buffered in LDS as f32, the products on
 //     v_mfma_f64_16x16x4f64 after converting the operands to f64.
@@ -307,13 +311,87 @@ __global__ __launch_bounds__(256) void post_norm_kernel(BlockParams p)
         atomicOr(p.err, kErrBlock);
 }
 
+// The largest input row project_row_lds_kernel stages (64 KiB of LDS).
+constexpr int kLdsRowFloats = 16384;
+
+// One token t0 (p.in % 4 == 0, p.in <= kLdsRowFloats), one wave per output
+// row as in project_rows_kernel<1> (the same f64 sums in the same order):
+// the workgroup stages the input row in LDS once, its first 4096 columns
+// requested before the rows' first weights so that the LDS stores wait only
+// for them.
+__global__ __launch_bounds__(256) void project_row_lds_kernel(BlockParams p, int t0)
+{
+    extern __shared__ f4 xs[];
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int vecs = p.in / 4;
+    const bool live = r < p.out;
+    // a wave past the last row streams row 0 (in bounds; unused)
+    const float *wr = p.w + (int64_t)(live ? r : 0) * p.in;
+    const float *xr = p.x + (int64_t)t0 * p.in;
+    f4 wv[16];
+    int v = lane;
+    if (vecs >= 1024) {
+        f4 t[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            t[j] = ldg4(xr + 4 * (threadIdx.x + 256 * j));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            wv[k] = ldg4_stream(wr + 4 * (v + 64 * k));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            xs[threadIdx.x + 256 * j] = t[j];
+        if (vecs > 1024)
+            for (int i = 1024 + threadIdx.x; i < vecs; i += 256)
+                xs[i] = ldg4(xr + 4 * i);
+    } else {
+        for (int i = threadIdx.x; i < vecs; i += 256)
+            xs[i] = ldg4(xr + 4 * i);
+    }
+    __syncthreads();
+    if (!live)
+        return;
+    double acc = 0.0;
+    for (; v + 960 < vecs; v += 1024) {
+        if (v != lane) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k)
+                wv[k] = ldg4_stream(wr + 4 * (v + 64 * k));
+        }
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const f4 xv = xs[v + 64 * k];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                acc = __builtin_fma((double)wv[k][e], (double)xv[e], acc);
+        }
+    }
+    for (; v < vecs; v += 64) {
+        const f4 w1 = ldg4_stream(wr + 4 * v);
+        const f4 xv = xs[v];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            acc = __builtin_fma((double)w1[e], (double)xv[e], acc);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+        acc += __shfl_xor(acc, o);
+    if (lane == 0)
+        stg(p.proj + (int64_t)t0 * p.out + r, (float)acc);
+}
+
 hipError_t launch_output_block(const BlockParams &p, hipStream_t stream)
 {
     if (p.n <= 2 * kRowTokens) {
         const dim3 grid((p.out + 3) / 4);
         for (int t0 = 0; t0 < p.n; t0 += kRowTokens) {
             const int nt = p.n - t0 < kRowTokens ? p.n - t0 : kRowTokens;
-            if (nt == 1)
+            if (nt == 1 && p.in % 4 == 0 && p.in <= kLdsRowFloats)
+                project_row_lds_kernel<<<grid, 256, p.in * 4, stream>>>(p, t0);
+            else if (nt == 1)
                 project_rows_kernel<1><<<grid, 256, 0, stream>>>(p, t0);
             else if (nt == 2)
                 project_rows_kernel<2><<<grid, 256, 0, stream>>>(p, t0);

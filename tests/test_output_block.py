@@ -78,9 +78,15 @@ def run_block(torch, ctx, x, w, scale, res, eps=1e-6, in_place=False):
     return proj.cpu().numpy(), out.cpu().numpy(), err
 
 
-# n = 1, 5, 16, 32: row streaming; 33, 200, 300: f64 MFMA tiles
+# n = 1, 5, 16, 32: row streaming; 33, 200, 300: f64 MFMA tiles. One token
+# with input rows of at most 16384 columns (a multiple of 4) is projected
+# with the input row staged in LDS: rows of 1000 (fewer than 4096 columns),
+# 5000 (4096 and a partial step) and 4096 columns, the last token of 17;
+# 16388 and 1001 columns take the plain one-token kernel.
 BLOCK_CASES = [(1, 4096, 2816), (5, 4096, 2816), (16, 8192, 2816), (32, 4096, 1536),
-               (33, 4096, 2816), (200, 4096, 300), (300, 1000, 130), (7, 1001, 77)]
+               (33, 4096, 2816), (200, 4096, 300), (300, 1000, 130), (7, 1001, 77),
+               (1, 1000, 77), (1, 5000, 300), (17, 4096, 300), (1, 16388, 64),
+               (1, 1001, 77)]
 
 
 @pytest.mark.gpu
@@ -103,6 +109,24 @@ def test_output_block_matches_the_oracle(torch, ctx, oracle, case):
         assert np.max(np.abs(out[t] - want)) <= 1e-5
         same += int(np.sum(proj[t].view(np.uint32) == want_p.view(np.uint32)))
     assert same >= 0.999 * n * rows
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cols", [1000, 4096, 5000, 16384])
+def test_one_token_projection_equals_the_multi_token_one_bitwise(torch, ctx, cols):
+    # the one-token kernel (input row staged in LDS) sums each row's f64
+    # products in the order of the multi-token row kernel
+    rows = 300
+    g = np.random.default_rng(cols)
+    x = g.standard_normal((2, cols)).astype(np.float32)
+    w = (g.standard_normal((rows, cols)) / np.sqrt(cols)).astype(np.float32)
+    scale = (1 + 0.1 * g.standard_normal(rows)).astype(np.float32)
+    res = g.standard_normal((2, rows)).astype(np.float32)
+    proj2, out2, err2 = run_block(torch, ctx, x, w, scale, res)
+    proj1, out1, err1 = run_block(torch, ctx, x[1:], w, scale, res[1:])
+    assert err1 == 0 and err2 == 0
+    assert np.array_equal(proj1[0].view(np.uint32), proj2[1].view(np.uint32))
+    assert np.array_equal(out1[0].view(np.uint32), out2[1].view(np.uint32))
 
 
 @pytest.mark.gpu
