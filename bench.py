@@ -436,7 +436,10 @@ def time_output_workload(torch, pcl, ctx, name, steps, warmup, seed):
     ev = start.elapsed_time(stop) / steps
     if ctx.sync():
         raise RuntimeError("device error flag set for %s" % name)
-    kernel = "project_rows" if nq <= 32 else "project_tiles"
+    if nq == 1 and width % 4 == 0 and width <= 16384:
+        kernel = "project_row_lds"
+    else:
+        kernel = "project_rows" if nq <= 32 else "project_tiles"
     return ev, wall, kernel, None, {"stream_ms": ev, "combine_ms": 0.0}, nsets
 
 
