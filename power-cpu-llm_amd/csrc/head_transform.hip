@@ -66,7 +66,6 @@ __global__ __launch_bounds__(64) void head_transform_kernel(TransformParams p)
     constexpr int kItems = ITEMS;
     constexpr int kStride = DK + 4; // 16-byte aligned rows
     constexpr int kHalf = DK / 2;
-    constexpr int kPairs = (kHalf + 63) / 64;
     constexpr int kVec = DK / 4;                          // float4 per row
     constexpr int kLoads = (kItems * kVec + 63) / 64;     // float4 per lane
     __shared__ __attribute__((aligned(16))) float rows[kItems * kStride];
@@ -76,21 +75,15 @@ __global__ __launch_bounds__(64) void head_transform_kernel(TransformParams p)
     const int s0 = blockIdx.y * kItems;
     const int count = p.slots - s0 < kItems ? p.slots - s0 : kItems;
 
-    // this lane's pairs j = lane + 64m: (sin, cos) of the token's position
-    // and the learned scales of both halves
-    typedef float f2 __attribute__((ext_vector_type(2)));
-    f2 sc[kPairs];
-    float qa[kPairs], qb[kPairs], ka[kPairs], kb[kPairs];
+    // this lane's pairs j0..j0+3 of every row it writes: (sin, cos) of the
+    // token's position and the learned scales of both halves
+    constexpr int kRowLanes = kHalf / 4;
+    constexpr int kPassRows = 64 / kRowLanes;
+    const int j0 = 4 * (lane % kRowLanes);
     const float *tab = p.tab + (p.pos0 + t) * DK;
-#pragma unroll
-    for (int m = 0; m < kPairs; ++m) {
-        const int j = lane + 64 * m < kHalf ? lane + 64 * m : 0;
-        sc[m] = *(const __attribute__((address_space(1))) f2 *)(tab + 2 * j);
-        qa[m] = ldg(p.qs + j);
-        qb[m] = ldg(p.qs + j + kHalf);
-        ka[m] = ldg(p.ks + j);
-        kb[m] = ldg(p.ks + j + kHalf);
-    }
+    const f4 sc0 = ldg4(tab + 2 * j0), sc1 = ldg4(tab + 2 * j0 + 4);
+    const f4 qa4 = ldg4(p.qs + j0), qb4 = ldg4(p.qs + j0 + kHalf);
+    const f4 ka4 = ldg4(p.ks + j0), kb4 = ldg4(p.ks + j0 + kHalf);
 
     // slot s of the token: Q heads, then K heads, then V heads
     auto source = [&](int s) -> const float * {
@@ -127,29 +120,34 @@ __global__ __launch_bounds__(64) void head_transform_kernel(TransformParams p)
     if (lane < count)
         inv[lane] = norm_inverse<DK>(rows + lane * kStride, p.eps);
     __syncthreads();
-    for (int r = 0; r < count; ++r) {
+    // the outputs: kHalf / 4 lanes per row, four consecutive pairs j0..j0+3
+    // each (a 16-byte store into either half), 256 / kHalf rows per pass
+    for (int r = lane / kRowLanes; r < count; r += kPassRows) {
         const int s = s0 + r;
         const int kind = s < p.qheads ? 0 : s < p.qheads + p.kvh ? 1 : 2;
         float *out = kind == 0   ? p.oq + (t * p.qheads + s) * DK
                      : kind == 1 ? p.ok + t * p.o_kv_stride + (int64_t)(s - p.qheads) * DK
                                  : p.ov + t * p.o_kv_stride + (int64_t)(s - p.qheads - p.kvh) * DK;
         const double iv = inv[r];
-        const float *row = rows + r * kStride;
+        const f4 xa = *(const f4 *)(rows + r * kStride + j0);
+        const f4 xb = *(const f4 *)(rows + r * kStride + j0 + kHalf);
+        const float sn[4] = {sc0[0], sc0[2], sc1[0], sc1[2]};
+        const float cs[4] = {sc0[1], sc0[3], sc1[1], sc1[3]};
+        f4 ya, yb;
 #pragma unroll
-        for (int m = 0; m < kPairs; ++m) {
-            const int j = lane + 64 * m;
-            if (j >= kHalf)
-                continue;
+        for (int e = 0; e < 4; ++e) {
             float a, b;
             if (kind == 2)
-                transform_pair<false>(row[j], row[j + kHalf], iv, 0.f, 0.f, 0.f, 0.f, &a, &b);
+                transform_pair<false>(xa[e], xb[e], iv, 0.f, 0.f, 0.f, 0.f, &a, &b);
             else
-                transform_pair<true>(row[j], row[j + kHalf], iv, kind == 0 ? qa[m] : ka[m],
-                                     kind == 0 ? qb[m] : kb[m], sc[m].x, sc[m].y, &a, &b);
+                transform_pair<true>(xa[e], xb[e], iv, kind == 0 ? qa4[e] : ka4[e],
+                                     kind == 0 ? qb4[e] : kb4[e], sn[e], cs[e], &a, &b);
             bad |= !is_finite(a) || !is_finite(b);
-            stg(out + j, a);
-            stg(out + j + kHalf, b);
+            ya[e] = a;
+            yb[e] = b;
         }
+        stg4(out + j0, ya);
+        stg4(out + j0 + kHalf, yb);
     }
     if (bad)
         atomicOr(p.err, kErrTransform);

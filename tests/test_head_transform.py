@@ -254,6 +254,11 @@ TRANSFORM_CASES = [
     (8, 2, 128, 70, 1000, False, False),
     (4, 4, 64, 5, 262143, True, False),
     (6, 3, 16, 9, 7, False, True),
+    # enough tokens for the packed workgroups (16 heads at 256, 8 at 512, a
+    # token's 8 heads of three kinds in one pass at 32)
+    (16, 8, 256, 160, 5000, False, False),
+    (16, 2, 512, 100, 77, True, False),
+    (4, 2, 32, 300, 3, False, False),
 ]
 
 
