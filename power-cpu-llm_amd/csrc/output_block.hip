@@ -356,7 +356,10 @@ __global__ __launch_bounds__(256) void project_row_lds_kernel(BlockParams p, int
         return;
     double acc = 0.0;
     for (; v + 960 < vecs; v += 1024) {
-        if (v != lane) {
+        // the first step's weights are in flight already when every lane
+        // takes it (vecs >= 1024); below that only lanes lane + 960 < vecs
+        // take it, and request them here
+        if (v != lane || vecs < 1024) {
 #pragma unroll
             for (int k = 0; k < 16; ++k)
                 wv[k] = ldg4_stream(wr + 4 * (v + 64 * k));

@@ -81,12 +81,13 @@ def run_block(torch, ctx, x, w, scale, res, eps=1e-6, in_place=False):
 # n = 1, 5, 16, 32: row streaming; 33, 200, 300: f64 MFMA tiles. One token
 # with input rows of at most 16384 columns (a multiple of 4) is projected
 # with the input row staged in LDS: rows of 1000 (fewer than 4096 columns),
-# 5000 (4096 and a partial step) and 4096 columns, the last token of 17;
-# 16388 and 1001 columns take the plain one-token kernel.
+# 5000 (4096 and a partial step), 4000 (one 4096-column step taken by some
+# lanes only) and 4096 columns, the last token of 17; 16388 and 1001
+# columns take the plain one-token kernel.
 BLOCK_CASES = [(1, 4096, 2816), (5, 4096, 2816), (16, 8192, 2816), (32, 4096, 1536),
                (33, 4096, 2816), (200, 4096, 300), (300, 1000, 130), (7, 1001, 77),
-               (1, 1000, 77), (1, 5000, 300), (17, 4096, 300), (1, 16388, 64),
-               (1, 1001, 77)]
+               (1, 1000, 77), (1, 5000, 300), (1, 4000, 300), (17, 4096, 300),
+               (1, 16388, 64), (1, 1001, 77)]
 
 
 @pytest.mark.gpu
@@ -112,7 +113,7 @@ def test_output_block_matches_the_oracle(torch, ctx, oracle, case):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("cols", [1000, 4096, 5000, 16384])
+@pytest.mark.parametrize("cols", [1000, 3848, 4000, 4092, 4096, 5000, 16384])
 def test_one_token_projection_equals_the_multi_token_one_bitwise(torch, ctx, cols):
     # the one-token kernel (input row staged in LDS) sums each row's f64
     # products in the order of the multi-token row kernel
