@@ -230,6 +230,10 @@ def _resource_remarks(source):
     ("pipe_kv.hip", "_ZN3pcl14pipe_kv_kernelILi512ELi1ELb1ELb1ELb1EEEvNS_6ParamsEi"),
     ("fan_kv.hip", "_ZN3pcl13fan_kv_kernelILi256ELb1ELb0ELb1EEEvNS_6ParamsEi"),
     ("fan_kv.hip", "_ZN3pcl13fan_kv_kernelILi256ELb0ELb1ELb0EEEvNS_6ParamsEi"),
+    # the decode step's output projection and the prompt's head transform
+    ("output_block.hip", "_ZN3pcl22project_row_lds_kernelENS_11BlockParamsEi"),
+    ("head_transform.hip", "_ZN3pcl21head_transform_kernelILi256ELi16EEEvNS_15TransformParamsE"),
+    ("head_transform.hip", "_ZN3pcl21head_transform_kernelILi512ELi8EEEvNS_15TransformParamsE"),
 ])
 def test_hot_kernels_do_not_spill_registers(source, kernel):
     # a spill in these kernels costs every tile or block: the prefill once
