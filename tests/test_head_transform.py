@@ -346,7 +346,9 @@ def test_fused_append_writes_prepared_rows_into_the_cache(pcl, torch, ctx, oracl
     t = pcl.HeadTransform(ctx, qh, kvh, dim, qs, ks, 1e-6, 10000.0)
     cache = pcl.LayerCache(ctx, kvh, dim, 10_000, window, 1 << 30)
     ref = oracle.OracleCache(kvh, dim, 10_000, window, 1 << 30)
-    for step, n in enumerate((40, 1, 1, 9)):
+    # 160 tokens take the packed workgroups (16 heads each) writing into the
+    # cache's rows; 40 take four heads a workgroup, one token one head
+    for step, n in enumerate((40, 1, 160, 1, 9)):
         rq = g.standard_normal((n, qh * dim)).astype(np.float32)
         rk = g.standard_normal((n, width)).astype(np.float32)
         rv = None if k_as_v else g.standard_normal((n, width)).astype(np.float32)
