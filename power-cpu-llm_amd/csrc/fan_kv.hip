@@ -43,9 +43,10 @@ namespace pcl {
 constexpr int kFanWaves = 8;
 constexpr int kFanThreads = 64 * kFanWaves;
 
-template <int DK> struct FanCfg {
+template <int DK, int SPLIT = 1> struct FanCfg {
     static constexpr int NU = DK / 32;        // score chain steps
-    static constexpr int VD = DK / kFanWaves; // output dims of a wave
+    // output dims of a wave: a workgroup owns DK / SPLIT of them
+    static constexpr int VD = DK / (kFanWaves * SPLIT);
     static constexpr int VW = VD / 16;        // output blocks of a wave (dims of a lane per key)
     // K of a wave's tile staged through LDS in pieces of KU score steps
     // (32 keys x 32 KU dims, 4 KU one-KiB copies), KB pieces in flight
@@ -76,7 +77,7 @@ template <int DK> struct FanCfg {
     static constexpr bool PREFETCH = kRows * 8 * DK <= kFloats;
     static constexpr int cFloats = 2 * kTilesPerChunk * kRows + kTilesPerChunk + 2 * kRows;
     static constexpr size_t bytes = (size_t)(aFloats + kFloats + cFloats) * sizeof(float);
-    static_assert(VW >= 1 && VW * 16 * kFanWaves == DK, "whole 16-dim output blocks");
+    static_assert(VW >= 1 && VW * 16 * kFanWaves * SPLIT == DK, "whole 16-dim output blocks");
     static_assert(KU * KPN == NU, "whole K pieces");
 };
 
@@ -134,11 +135,15 @@ constexpr int kMergeHead = 8;
 
 // FULL: the head dim equals the padded head dim (no dim clamping). MERGE:
 // the launch's last chunk of one span, merged into the output.
-template <int DK, bool FULL, bool CAP, bool MERGE>
+// SPLIT (a launch of every chunk): SPLIT workgroups share an item, each
+// forming all its scores and the P.V of DK / SPLIT output dims.
+template <int DK, bool FULL, bool CAP, bool MERGE, int SPLIT>
 __global__ __launch_bounds__(kFanThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fan_kv_kernel(Params p, int ci)
 {
-    using C = FanCfg<DK>;
+    static_assert(SPLIT == 1 || !MERGE, "a merging launch keeps whole items");
+    using C = FanCfg<DK, SPLIT>;
+    int split = 0;
     // consecutive workgroups cycle over the KV heads (each XCD's L2 then
     // serves one head's K and V when there are eight)
     int kvl = (int)blockIdx.x % p.nkv;
@@ -149,13 +154,15 @@ void fan_kv_kernel(Params p, int ci)
             // its units in workgroups congruent mod 8, which the dispatcher
             // deals to one XCD, so they share the chunk's K and V in its L2:
             // workgroup b runs unit (b / 8) % units of group
-            // ((b / 8) / units) * 8 + b % 8.
+            // ((b / 8) / units) * 8 + b % 8 (with SPLIT, (unit, split) pairs
+            // in place of units).
             const int b = (int)blockIdx.x;
             const int k = b >> 3;
-            const int gi = (k / p.units) * 8 + (b & 7);
+            const int gi = (k / (p.units * SPLIT)) * 8 + (b & 7);
             if (gi >= p.nkv * p.nch)
                 return; // padding to whole groups of eight
-            unit = k % p.units;
+            unit = k % (p.units * SPLIT) / SPLIT;
+            split = k % SPLIT;
             kvl = gi % p.nkv;
             ci = gi / p.nkv;
         }
@@ -184,7 +191,7 @@ void fan_kv_kernel(Params p, int ci)
     const int64_t cbase = (int64_t)c * kChunk;
     const int64_t klast = p.nkeys - 1;
     const int64_t hoff = (int64_t)kh * p.dim;
-    const int d0 = VD * w; // the wave's output dims
+    const int d0 = VD * w + DK / SPLIT * split; // the wave's output dims
 
     // Allowed flags of the lane's keys of tile w. A chunk that every real
     // row of the unit sees whole needs no per-key test (padding rows then
@@ -499,6 +506,10 @@ void fan_kv_kernel(Params p, int ci)
         mlst[2 * col] = m;
         mlst[2 * col + 1] = l;
     }
+    // the columns this workgroup formed (all but with SPLIT)
+    auto own = [&](int k) {
+        return SPLIT == 1 || (tid % 32 + 32 * k) / (32 * C::NK / SPLIT) == split;
+    };
     // (the earlier partials' copies have landed too)
     __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
     fan_barrier();
@@ -510,7 +521,7 @@ void fan_kv_kernel(Params p, int ci)
 #pragma unroll
     for (int k = 0; k < NK; ++k) {
         const int c4 = tid % 32 + 32 * k;
-        ov[k] = *(const f4 *)(ost + mr * DK + 4 * (c4 ^ (mr & 7)));
+        ov[k] = own(k) ? *(const f4 *)(ost + mr * DK + 4 * (c4 ^ (mr & 7))) : f4{};
     }
     if constexpr (!MERGE) { // chunk partial for the combine kernels
         const int64_t slot = mslot0 + ci;
@@ -518,10 +529,10 @@ void fan_kv_kernel(Params p, int ci)
 #pragma unroll
         for (int k = 0; k < NK; ++k) {
             const int d = 4 * (tid % 32 + 32 * k);
-            if (FULL || d < p.dim)
+            if ((FULL || d < p.dim) && own(k))
                 stg4(wo + d, ov[k]);
         }
-        if (tid % 32 == 0) {
+        if (tid % 32 == 0 && split == 0) {
             stg(p.ws_ml + 2 * slot, mm);
             stg(p.ws_ml + 2 * slot + 1, ml);
         }
@@ -577,7 +588,7 @@ constexpr int kFanMaxDevices = 64;
 
 // Dynamic LDS above 64 KiB must be allowed once per kernel and device; a
 // repeated call from a racing thread is harmless.
-template <int DK, bool FULL, bool CAP, bool MERGE> static hipError_t configure_fan()
+template <int DK, bool FULL, bool CAP, bool MERGE, int SPLIT> static hipError_t configure_fan()
 {
     static std::atomic<bool> configured[kFanMaxDevices];
     int dev = 0;
@@ -587,9 +598,9 @@ template <int DK, bool FULL, bool CAP, bool MERGE> static hipError_t configure_f
     if (dev < 0 || dev >= kFanMaxDevices)
         return hipErrorInvalidDevice;
     if (!configured[dev].load(std::memory_order_acquire)) {
-        e = hipFuncSetAttribute((const void *)fan_kv_kernel<DK, FULL, CAP, MERGE>,
+        e = hipFuncSetAttribute((const void *)fan_kv_kernel<DK, FULL, CAP, MERGE, SPLIT>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)FanCfg<DK>::bytes);
+                                (int)FanCfg<DK, SPLIT>::bytes);
         if (e != hipSuccess)
             return e;
         configured[dev].store(true, std::memory_order_release);
@@ -598,18 +609,34 @@ template <int DK, bool FULL, bool CAP, bool MERGE> static hipError_t configure_f
 }
 
 // ci < 0: every chunk of the launch (grid y), partials for the combine.
-template <int DK, bool FULL, bool CAP, bool MERGE>
-static hipError_t launch_fan_dk(const Params &p, int ci, hipStream_t stream)
+template <int DK, bool FULL, bool CAP, bool MERGE, int SPLIT>
+static hipError_t launch_fan_split(const Params &p, int ci, hipStream_t stream)
 {
-    const hipError_t e = configure_fan<DK, FULL, CAP, MERGE>();
+    const hipError_t e = configure_fan<DK, FULL, CAP, MERGE, SPLIT>();
     if (e != hipSuccess)
         return e;
     // every chunk: (chunk, KV head) groups padded to a multiple of eight,
-    // each group's units on one XCD (see the kernel)
+    // each group's units (and their splits) on one XCD (see the kernel)
     const int groups8 = (p.nkv * p.nch + 7) / 8 * 8;
-    const dim3 grid(ci < 0 ? groups8 * p.units : p.units * p.nkv);
-    fan_kv_kernel<DK, FULL, CAP, MERGE><<<grid, kFanThreads, FanCfg<DK>::bytes, stream>>>(p, ci);
+    const dim3 grid(ci < 0 ? groups8 * p.units * SPLIT : p.units * p.nkv);
+    fan_kv_kernel<DK, FULL, CAP, MERGE, SPLIT>
+        <<<grid, kFanThreads, FanCfg<DK, SPLIT>::bytes, stream>>>(p, ci);
     return hipGetLastError();
+}
+
+// Items (chunk, unit, KV head) up to which a head-dim-512 launch of every
+// chunk splits each item's output dims over two workgroups: one workgroup
+// a CU (its LDS), so at most half the CUs hold an item otherwise.
+constexpr int64_t kFanSplitItems = 128;
+
+template <int DK, bool FULL, bool CAP, bool MERGE>
+static hipError_t launch_fan_dk(const Params &p, int ci, hipStream_t stream)
+{
+    if constexpr (DK == 512 && !MERGE) {
+        if (ci < 0 && (int64_t)p.nkv * p.nch * p.units <= kFanSplitItems)
+            return launch_fan_split<DK, FULL, CAP, MERGE, 2>(p, ci, stream);
+    }
+    return launch_fan_split<DK, FULL, CAP, MERGE, 1>(p, ci, stream);
 }
 
 template <int DK, bool MERGE>
