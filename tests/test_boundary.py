@@ -228,8 +228,11 @@ def _resource_remarks(source):
     # the same with a one-token step's head transform folded in
     ("pipe_kv.hip", "_ZN3pcl14pipe_kv_kernelILi256ELi1ELb1ELb0ELb1EEEvNS_6ParamsEi"),
     ("pipe_kv.hip", "_ZN3pcl14pipe_kv_kernelILi512ELi1ELb1ELb1ELb1EEEvNS_6ParamsEi"),
-    ("fan_kv.hip", "_ZN3pcl13fan_kv_kernelILi256ELb1ELb0ELb1EEEvNS_6ParamsEi"),
-    ("fan_kv.hip", "_ZN3pcl13fan_kv_kernelILi256ELb0ELb1ELb0EEEvNS_6ParamsEi"),
+    ("fan_kv.hip", "_ZN3pcl13fan_kv_kernelILi256ELb1ELb0ELb1ELi1EEEvNS_6ParamsEi"),
+    ("fan_kv.hip", "_ZN3pcl13fan_kv_kernelILi256ELb0ELb1ELb0ELi1EEEvNS_6ParamsEi"),
+    # head-dim-512 decodes of few items, each item's output dims split
+    ("fan_kv.hip", "_ZN3pcl13fan_kv_kernelILi512ELb1ELb0ELb0ELi2EEEvNS_6ParamsEi"),
+    ("fan_kv.hip", "_ZN3pcl13fan_kv_kernelILi512ELb1ELb0ELb0ELi4EEEvNS_6ParamsEi"),
     # the decode step's output projection and the prompt's head transform
     ("output_block.hip", "_ZN3pcl22project_row_lds_kernelENS_11BlockParamsEi"),
     ("head_transform.hip", "_ZN3pcl21head_transform_kernelILi256ELi16EEEvNS_15TransformParamsE"),
