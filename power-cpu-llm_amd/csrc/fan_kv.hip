@@ -624,11 +624,11 @@ static hipError_t launch_fan_split(const Params &p, int ci, hipStream_t stream)
     return hipGetLastError();
 }
 
-// Items (chunk, unit, KV head) up to which a head-dim-512 launch of every
-// chunk splits each item's output dims over two workgroups (four up to half
-// as many): one workgroup a CU (its LDS), so at most half (a quarter of)
-// the CUs would hold an item otherwise. The split workgroups of an item
-// share its K and V through their XCD's L2.
+// Items (chunk, unit, KV head) up to which a launch of every chunk at head
+// dim 256 or 512 splits each item's output dims over two workgroups (at 512
+// four up to half as many): one workgroup a CU (its LDS), so at most half
+// (a quarter of) the CUs would hold an item otherwise. The split workgroups
+// of an item share its K and V through their XCD's L2.
 constexpr int64_t kFanSplitItems = 128;
 
 template <int DK, bool FULL, bool CAP, bool MERGE>
@@ -637,6 +637,10 @@ static hipError_t launch_fan_dk(const Params &p, int ci, hipStream_t stream)
     if constexpr (DK == 512 && !MERGE) {
         if (ci < 0 && (int64_t)p.nkv * p.nch * p.units <= kFanSplitItems / 2)
             return launch_fan_split<DK, FULL, CAP, MERGE, 4>(p, ci, stream);
+        if (ci < 0 && (int64_t)p.nkv * p.nch * p.units <= kFanSplitItems)
+            return launch_fan_split<DK, FULL, CAP, MERGE, 2>(p, ci, stream);
+    }
+    if constexpr (DK == 256 && !MERGE) {
         if (ci < 0 && (int64_t)p.nkv * p.nch * p.units <= kFanSplitItems)
             return launch_fan_split<DK, FULL, CAP, MERGE, 2>(p, ci, stream);
     }

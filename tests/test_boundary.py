@@ -230,7 +230,8 @@ def _resource_remarks(source):
     ("pipe_kv.hip", "_ZN3pcl14pipe_kv_kernelILi512ELi1ELb1ELb1ELb1EEEvNS_6ParamsEi"),
     ("fan_kv.hip", "_ZN3pcl13fan_kv_kernelILi256ELb1ELb0ELb1ELi1EEEvNS_6ParamsEi"),
     ("fan_kv.hip", "_ZN3pcl13fan_kv_kernelILi256ELb0ELb1ELb0ELi1EEEvNS_6ParamsEi"),
-    # head-dim-512 decodes of few items, each item's output dims split
+    # launches of few items, each item's output dims split
+    ("fan_kv.hip", "_ZN3pcl13fan_kv_kernelILi256ELb1ELb0ELb0ELi2EEEvNS_6ParamsEi"),
     ("fan_kv.hip", "_ZN3pcl13fan_kv_kernelILi512ELb1ELb0ELb0ELi2EEEvNS_6ParamsEi"),
     ("fan_kv.hip", "_ZN3pcl13fan_kv_kernelILi512ELb1ELb0ELb0ELi4EEEvNS_6ParamsEi"),
     # the decode step's output projection and the prompt's head transform
